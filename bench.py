@@ -1,0 +1,191 @@
+"""One DiT Euler step at 1024x1024 on one MI355X (4096 image + 256 text rows,
+32 blocks, synthetic Q8_0 weights of the real 7B shape), through libexn-hip.so.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu]
+
+A step is one velocity pass over the image rows against the kept prompt K/V
+(the reference's steps 2..8, src/cuda-dit.lisp:6-9) plus the Euler update,
+with every input already in HBM.  The first (uncached) step and the whole
+8-step loop are reported beside it.  Prints one JSON line.
+
+roofline: the dominant kernel (the gate_up product with SwiGLU fused) from
+HIP events recorded around each of its launches in the timed region, on the
+stream they run on; its algorithmic FLOPs per launch are 2 x 4096 x 24576 x
+4096.  traffic: HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE /
+WRITE_SIZE (profiles/), or null.
+
+cpu_baseline: the oracle (oracle/exn_oracle.py, numpy fp32) timed on this
+host for one cached block of the same workload, x32 blocks (extrapolated).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "ex-nihilo_amd"))
+
+METRIC = "DiT Euler step ms @1024² (4096 img+256 txt tok), 1 GPU; % bf16 MFMA peak"
+PEAK_TFLOPS = 2516.6          # MI355X dense bf16 MFMA (256 CUs x 4096 FLOP/clk x 2.4 GHz)
+HBM_GBS = 8000.0
+H = W = 64                    # latent 64 x 64: 4096 image rows
+P = 256                       # text rows
+LAYERS = 32
+SEED = 2
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_1024sq_traffic.json")
+
+
+def gemm_flops_per_row():
+    Wd, F = 4096, 12288
+    return 2 * (4 * Wd * Wd + Wd * 2 * F + F * Wd)
+
+
+def step_flops(cached):
+    n = H * W if cached else P + H * W
+    l = P + H * W
+    n0 = P if cached else 0
+    pairs = sum((l if g >= P else g + 1) for g in range(n0, n0 + n))
+    gemm = LAYERS * n * gemm_flops_per_row()
+    att = LAYERS * 4 * 128 * 32 * pairs
+    return gemm, att, gemm + att
+
+
+def cpu_baseline():
+    """The oracle's cached block at the workload's shape (4096 image rows over
+    256 kept prompt rows + themselves), one timed call, x32 blocks."""
+    sys.path.insert(0, REPO)
+    from oracle import exn_oracle as xo
+    rng = np.random.default_rng(0)
+    wt = xo.SynthWeights(SEED, cache_bytes=4 << 30)
+    for slot in ("attn.to_q.weight", "attn.to_k.weight", "attn.to_v.weight", "attn.to_out.0.weight",
+                 "img_mlp.gate_up.weight", "img_mlp.out.weight"):
+        wt("transformer_blocks.0." + slot)              # dequantised before the clock starts
+    n, l = H * W, P + H * W
+    x = rng.normal(0, 1, (n, 4096)).astype(np.float32)
+    mod = rng.normal(0, 0.05, (n, 4 * 4096)).astype(np.float32)
+    cos, sin = xo.rope_tables(xo.positions(P, H, W)[P:])
+    kf = np.zeros((l, 32, 128), np.float32)
+    vf = np.zeros((l, 32, 128), np.float32)
+    kf[:P] = rng.normal(0, 1, (P, 32, 128))
+    vf[:P] = rng.normal(0, 1, (P, 32, 128))
+    t0 = time.perf_counter()
+    xo.block(wt, 0, x, mod, cos, sin, kf, vf, P, P, 0, 0)
+    dt = time.perf_counter() - t0
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = int(os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS") or cores)
+    return {"value": round(dt * 1e3 * LAYERS, 1), "unit": "ms/step", "cores": min(cores, threads), "kind": "port",
+            "sample": "one cached block (4096 image rows over 4352 keys) of the 1024^2 step in numpy fp32, "
+                      "timed once (%.1f s), x32 blocks: an extrapolated step" % dt}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py: this build measures one GPU; --gpus %d is not supported (the step shards over image "
+              "rows across GPUs only by design, see DESIGN.md)" % a.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import exn_hip as X
+    ctx = X.Context(0)
+    d = X.Dit(ctx, LAYERS)
+    t0 = time.perf_counter()
+    d.synth(SEED)
+    d.check()
+    print("bench: synthetic 7B Q8_0 DiT on the device in %.1f s" % (time.perf_counter() - t0), file=sys.stderr,
+          flush=True)
+    rng = np.random.default_rng(SEED)
+    context = X.DevBuf.of(ctx, rng.normal(0, 1, (P, 4096)).astype(np.float32))
+    latent = rng.normal(0, 1, (64, H, W)).astype(np.float32)
+    z = X.DevBuf.of(ctx, latent)
+    v = X.DevBuf(ctx, (64, H, W), np.float32)
+    sig = X.TURBO_SIGMAS
+    key = 7
+
+    def step(i, k):
+        s, s2 = sig[i % 8], sig[i % 8 + 1]
+        X.call("exn_dit_velocity_dev", d.h, context.h, P, z.h, H, W, s, k, 0, None, 0, 0, v.h)
+        X.call("exn_euler", ctx.h, 64 * H * W, z.h, v.h, np.float32(s2 - s))
+
+    # the first (uncached) step: the prompt rows too, their K/V kept
+    ctx.sync()
+    t0 = time.perf_counter()
+    step(0, key)
+    ctx.sync()
+    t_uncached = time.perf_counter() - t0
+    for i in range(a.warmup):
+        step(1 + i, key)
+    ctx.sync()
+    d.profile(True)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        step(1 + i, key)
+    ctx.sync()
+    t_steps = time.perf_counter() - t0
+    d.profile(False)
+    prof = d.profile_read()
+    ms = t_steps * 1e3 / a.steps
+
+    # the whole 8-step loop from fresh noise (generate's loop, on the device)
+    z.upload(latent)
+    sg = np.array(sig, np.float64)
+    ctx.sync()
+    t0 = time.perf_counter()
+    X.call("exn_dit_generate_dev", d.h, context.h, P, z.h, H, W, X.ptr(sg), len(sg), 0, None, 0, 0)
+    ctx.sync()
+    t_8 = time.perf_counter() - t0
+    zf = z.get()
+    finite = bool(np.isfinite(zf).all())
+
+    gemm_f, att_f, tot_f = step_flops(True)
+    tflops = tot_f / (ms * 1e-3) / 1e12
+    gu_ms, gu_n, gu_f, gu_b = prof["gate_up"]
+    gu_avg = gu_ms / max(gu_n, 1)
+    achieved = (gu_f / max(gu_n, 1)) / (gu_avg * 1e-3) / 1e12 if gu_n else None
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        traffic = json.load(open(TRAFFIC_FILE)).get("bytes_per_launch")
+    gemm_ms = sum(prof[c][0] for c in ("qkv", "out", "gate_up", "down"))
+    gemm_flops = sum(prof[c][2] for c in ("qkv", "out", "gate_up", "down"))
+    kernels = {c: {"ms_per_step": round(prof[c][0] / a.steps, 3), "launches_per_step": prof[c][1] // a.steps,
+                   **({"tflops": round(prof[c][2] / (prof[c][0] * 1e-3) / 1e12, 1)} if prof[c][2] else {}),
+                   **({"gbs": round(prof[c][3] / (prof[c][0] * 1e-3) / 1e9, 1)} if prof[c][3] and not prof[c][2]
+                      else {})}
+               for c in X.Dit.PROFILE_CLASSES}
+    out = {
+        "metric": METRIC, "value": round(ms, 3), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "dit-euler-step-1024x1024", "image_rows": H * W, "text_rows": P, "blocks": LAYERS,
+                   "weights": "Q8_0 synthetic (7.0B block + 0.14B edge parameters)",
+                   "step": "cached: image rows over kept prompt K/V, + Euler update", "seed": SEED},
+        "tflops": round(tflops, 1), "mfma_peak_frac": round(tflops / PEAK_TFLOPS, 4),
+        "step_tflop": round(tot_f / 1e12, 3),
+        "gemm_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
+        "gemm_peak_frac": round(gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_TFLOPS, 4) if gemm_ms else None,
+        "uncached_step_ms": round(t_uncached * 1e3, 2), "euler_8_steps_ms": round(t_8 * 1e3, 1),
+        "final_latent_finite": finite, "ref_rtx3090_ms_per_step": 1187.5,
+        "kernels": kernels,
+        "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, Q8_0 weights",
+                     "achieved": round(achieved, 1) if achieved else None, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_TFLOPS, 4) if achieved else None, "traffic": traffic,
+                     "avg_launch_ms": round(gu_avg, 4)},
+    }
+    if not a.no_cpu:
+        print("bench: timing the CPU baseline (oracle, one block)", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline()
+    d.destroy()
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,1312 @@
+// api.hip -- libexn-hip.so's C ABI (include/exn_hip.h): contexts, device
+// memory, weights, the op-level entry points, and the DiT step driver that
+// replaces the reference's CUDA backend (src/cuda-dit.lisp).
+#include "exn_common.h"
+#include "../../include/exn_hip.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace exn {
+
+static thread_local std::string g_err;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+}
+
+}  // namespace exn
+
+using namespace exn;
+
+#define FAIL(code, ...)        \
+  do {                         \
+    exn::set_error(__VA_ARGS__); \
+    return code;               \
+  } while (0)
+
+#define HIPCHK(expr)                                                                          \
+  do {                                                                                        \
+    hipError_t e_ = (expr);                                                                   \
+    if (e_ != hipSuccess) FAIL(e_ == hipErrorOutOfMemory ? EXN_ENOMEM : EXN_EHIP, "%s: %s (%s:%d)", #expr, \
+                               hipGetErrorString(e_), __FILE__, __LINE__);                    \
+  } while (0)
+
+#define TRY(expr)              \
+  do {                         \
+    int r_ = (expr);           \
+    if (r_ != EXN_OK) return r_; \
+  } while (0)
+
+struct exn_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  void* tmp = nullptr;  // scratch of the op-level entry points (fp32 -> bf16 inputs)
+  size_t tmp_bytes = 0;
+};
+
+struct exn_w {
+  exn_ctx* ctx = nullptr;
+  int kind = EXN_Q8_0;
+  int64_t rows = 0, cols = 0;
+  int8_t* qs = nullptr;
+  uint16_t* d = nullptr;
+  uint16_t* wb = nullptr;  // bf16 rows (EXN_F32 / EXN_BF16 matrices)
+  bool pairs = false;      // gate/up rows interleaved by 32
+  bool view = false;       // rows inside another allocation (not freed here)
+};
+
+static int dev_alloc(void** p, size_t bytes) {
+  *p = nullptr;
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) {
+    *p = nullptr;
+    (void)hipGetLastError();
+    FAIL(e == hipErrorOutOfMemory ? EXN_ENOMEM : EXN_EHIP, "hipMalloc(%zu bytes): %s", bytes, hipGetErrorString(e));
+  }
+  return EXN_OK;
+}
+
+static void dev_free(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+static int use(exn_ctx* ctx) {
+  if (!ctx) FAIL(EXN_EINVAL, "null context");
+  HIPCHK(hipSetDevice(ctx->device));
+  return EXN_OK;
+}
+
+static int ctx_tmp(exn_ctx* ctx, size_t bytes, void** out) {
+  if (ctx->tmp_bytes < bytes) {
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    dev_free(ctx->tmp);
+    ctx->tmp = nullptr;
+    ctx->tmp_bytes = 0;
+    TRY(dev_alloc(&ctx->tmp, bytes));
+    ctx->tmp_bytes = bytes;
+  }
+  *out = ctx->tmp;
+  return EXN_OK;
+}
+
+extern "C" {
+
+const char* exn_last_error(void) { return g_err.c_str(); }
+
+int exn_version(void) { return 1; }
+
+int exn_device_count(int* n) {
+  if (!n) FAIL(EXN_EINVAL, "null count");
+  *n = 0;
+  int c = 0;
+  hipError_t e = hipGetDeviceCount(&c);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    FAIL(EXN_ENODEV, "no GPU: %s", hipGetErrorString(e));
+  }
+  *n = c;
+  return EXN_OK;
+}
+
+int exn_open(int device, exn_ctx** out) {
+  if (!out) FAIL(EXN_EINVAL, "null output");
+  *out = nullptr;
+  int c = 0;
+  hipError_t e = hipGetDeviceCount(&c);
+  if (e != hipSuccess || c == 0) {
+    (void)hipGetLastError();
+    FAIL(EXN_ENODEV, "no GPU (%s)", e != hipSuccess ? hipGetErrorString(e) : "0 devices");
+  }
+  if (device < 0 || device >= c) FAIL(EXN_ENODEV, "device %d of %d", device, c);
+  HIPCHK(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    FAIL(EXN_ENODEV, "device %d is %s; libexn-hip.so is built for gfx950 only", device, prop.gcnArchName);
+  exn_ctx* ctx = new exn_ctx();
+  ctx->device = device;
+  e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    FAIL(EXN_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  ctx->stream = ctx->own;
+  *out = ctx;
+  return EXN_OK;
+}
+
+int exn_close(exn_ctx* ctx) {
+  if (!ctx) return EXN_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  dev_free(ctx->tmp);
+  if (ctx->own) (void)hipStreamDestroy(ctx->own);
+  delete ctx;
+  return EXN_OK;
+}
+
+int exn_set_stream(exn_ctx* ctx, void* stream) {
+  TRY(use(ctx));
+  ctx->stream = stream ? (hipStream_t)stream : ctx->own;
+  return EXN_OK;
+}
+
+int exn_sync(exn_ctx* ctx) {
+  TRY(use(ctx));
+  HIPCHK(hipStreamSynchronize(ctx->stream));
+  return EXN_OK;
+}
+
+int exn_alloc(exn_ctx* ctx, size_t bytes, void** dptr) {
+  TRY(use(ctx));
+  if (!dptr) FAIL(EXN_EINVAL, "null output");
+  return dev_alloc(dptr, bytes);
+}
+
+int exn_free(exn_ctx* ctx, void* dptr) {
+  TRY(use(ctx));
+  HIPCHK(hipStreamSynchronize(ctx->stream));
+  dev_free(dptr);
+  return EXN_OK;
+}
+
+int exn_upload(exn_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  TRY(use(ctx));
+  if (!dst || (!src && bytes)) FAIL(EXN_EINVAL, "null pointer");
+  HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  HIPCHK(hipStreamSynchronize(ctx->stream));  // the host buffer may be reused on return
+  return EXN_OK;
+}
+
+int exn_download(exn_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  TRY(use(ctx));
+  if (!dst || (!src && bytes)) FAIL(EXN_EINVAL, "null pointer");
+  HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  HIPCHK(hipStreamSynchronize(ctx->stream));
+  return EXN_OK;
+}
+
+int exn_copy(exn_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  TRY(use(ctx));
+  if (!dst || (!src && bytes)) FAIL(EXN_EINVAL, "null pointer");
+  HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return EXN_OK;
+}
+
+// --- weights ----------------------------------------------------------------------
+
+static int w_new(exn_ctx* ctx, int kind, int64_t rows, int64_t cols, exn_w** out) {
+  if (!out) FAIL(EXN_EINVAL, "null output");
+  *out = nullptr;
+  if (rows <= 0 || cols <= 0) FAIL(EXN_EINVAL, "matrix %lld x %lld", (long long)rows, (long long)cols);
+  if (kind == EXN_Q8_0 && cols % 32) FAIL(EXN_EINVAL, "Q8_0 matrix of %lld columns: not a multiple of 32", (long long)cols);
+  exn_w* w = new exn_w();
+  w->ctx = ctx;
+  w->kind = kind;
+  w->rows = rows;
+  w->cols = cols;
+  int r = EXN_OK;
+  if (kind == EXN_Q8_0) {
+    r = dev_alloc((void**)&w->qs, (size_t)(rows * cols));
+    if (r == EXN_OK) r = dev_alloc((void**)&w->d, (size_t)(rows * cols / 32) * 2);
+  } else {
+    r = dev_alloc((void**)&w->wb, (size_t)(rows * cols) * 2);
+  }
+  if (r != EXN_OK) {
+    dev_free(w->qs);
+    dev_free(w->d);
+    dev_free(w->wb);
+    delete w;
+    return r;
+  }
+  *out = w;
+  return EXN_OK;
+}
+
+int exn_weight_free(exn_w* w) {
+  if (!w) return EXN_OK;
+  if (w->ctx) {
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipStreamSynchronize(w->ctx->stream);
+  }
+  if (!w->view) {
+    dev_free(w->qs);
+    dev_free(w->d);
+    dev_free(w->wb);
+  }
+  delete w;
+  return EXN_OK;
+}
+
+// GGUF block_q8_0 records (host) -> qs, d at the given rows (row_map: device int32, or null)
+static int upload_q8_blocks(exn_ctx* ctx, const void* blocks, int64_t rows, int64_t cols, const int32_t* row_map,
+                            int8_t* qs, uint16_t* d) {
+  const int64_t kb = cols / 32;
+  const size_t bytes = (size_t)(rows * kb) * 34;
+  void* staging = nullptr;
+  TRY(ctx_tmp(ctx, bytes, &staging));
+  HIPCHK(hipMemcpyAsync(staging, blocks, bytes, hipMemcpyHostToDevice, ctx->stream));
+  HIPCHK(repack_q8_blocks(ctx->stream, (const uint8_t*)staging, kb, rows, row_map, qs, d));
+  HIPCHK(hipStreamSynchronize(ctx->stream));
+  return EXN_OK;
+}
+
+int exn_weight_q8_0(exn_ctx* ctx, const void* blocks, int64_t rows, int64_t cols, exn_w** out) {
+  TRY(use(ctx));
+  if (!blocks) FAIL(EXN_EINVAL, "null blocks");
+  TRY(w_new(ctx, EXN_Q8_0, rows, cols, out));
+  int r = upload_q8_blocks(ctx, blocks, rows, cols, nullptr, (*out)->qs, (*out)->d);
+  if (r != EXN_OK) {
+    exn_weight_free(*out);
+    *out = nullptr;
+  }
+  return r;
+}
+
+static int upload_bf16_from(exn_ctx* ctx, const void* data, bool is_f32, int64_t count, uint16_t* dst) {
+  if (is_f32) {
+    void* staging = nullptr;
+    TRY(ctx_tmp(ctx, (size_t)count * 4, &staging));
+    HIPCHK(hipMemcpyAsync(staging, data, (size_t)count * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(f32_to_bf16(ctx->stream, (const float*)staging, dst, count));
+  } else {
+    HIPCHK(hipMemcpyAsync(dst, data, (size_t)count * 2, hipMemcpyHostToDevice, ctx->stream));
+  }
+  HIPCHK(hipStreamSynchronize(ctx->stream));
+  return EXN_OK;
+}
+
+int exn_weight_f32(exn_ctx* ctx, const float* data, int64_t rows, int64_t cols, exn_w** out) {
+  TRY(use(ctx));
+  if (!data) FAIL(EXN_EINVAL, "null data");
+  TRY(w_new(ctx, EXN_F32, rows, cols, out));
+  int r = upload_bf16_from(ctx, data, true, rows * cols, (*out)->wb);
+  if (r != EXN_OK) {
+    exn_weight_free(*out);
+    *out = nullptr;
+  }
+  return r;
+}
+
+int exn_weight_bf16(exn_ctx* ctx, const uint16_t* data, int64_t rows, int64_t cols, exn_w** out) {
+  TRY(use(ctx));
+  if (!data) FAIL(EXN_EINVAL, "null data");
+  TRY(w_new(ctx, EXN_BF16, rows, cols, out));
+  int r = upload_bf16_from(ctx, data, false, rows * cols, (*out)->wb);
+  if (r != EXN_OK) {
+    exn_weight_free(*out);
+    *out = nullptr;
+  }
+  return r;
+}
+
+static uint64_t gen_key(uint64_t seed, uint64_t tensor) {
+  auto mix = [](uint64_t z) {
+    z ^= z >> 30; z *= 0xBF58476D1CE4E5B9ull;
+    z ^= z >> 27; z *= 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  };
+  return mix(seed * 0x9E3779B97F4A7C15ull + tensor + 1);
+}
+
+int exn_weight_q8_0_synth(exn_ctx* ctx, uint64_t seed, uint64_t tensor, int64_t rows, int64_t cols, exn_w** out) {
+  TRY(use(ctx));
+  TRY(w_new(ctx, EXN_Q8_0, rows, cols, out));
+  hipError_t e = synth_q8(ctx->stream, gen_key(seed, tensor), rows, cols, cols / 32, nullptr, (*out)->qs, (*out)->d);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    exn_weight_free(*out);
+    *out = nullptr;
+    FAIL(EXN_EHIP, "synthetic weights: %s", hipGetErrorString(e));
+  }
+  return EXN_OK;
+}
+
+int exn_weight_info(const exn_w* w, int64_t* rows, int64_t* cols, int* kind) {
+  if (!w) FAIL(EXN_EINVAL, "null weight");
+  if (rows) *rows = w->rows;
+  if (cols) *cols = w->cols;
+  if (kind) *kind = w->kind;
+  return EXN_OK;
+}
+
+int exn_dequant(exn_ctx* ctx, const exn_w* w, float* f32, uint16_t* bf16) {
+  TRY(use(ctx));
+  if (!w) FAIL(EXN_EINVAL, "null weight");
+  if (w->kind != EXN_Q8_0) FAIL(EXN_EINVAL, "exn_dequant: not a Q8_0 matrix");
+  HIPCHK(dequant_q8(ctx->stream, w->qs, w->d, w->rows * w->cols, f32, bf16));
+  return EXN_OK;
+}
+
+static std::vector<int32_t> pair_rows(int64_t rows) {
+  // gate row i (i < rows/2) -> 64*(i/32) + i%32; up row i -> 64*(i/32) + 32 + i%32
+  const int64_t f = rows / 2;
+  std::vector<int32_t> map((size_t)rows);
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t i = r < f ? r : r - f;
+    map[(size_t)r] = (int32_t)(64 * (i / 32) + (r < f ? 0 : 32) + i % 32);
+  }
+  return map;
+}
+
+int exn_weight_pairs(exn_ctx* ctx, exn_w* w) {
+  TRY(use(ctx));
+  if (!w) FAIL(EXN_EINVAL, "null weight");
+  if (w->pairs) return EXN_OK;
+  if (w->kind != EXN_Q8_0 || w->rows % 64) FAIL(EXN_EINVAL, "pairs: a Q8_0 matrix of a multiple of 64 rows");
+  const std::vector<int32_t> map = pair_rows(w->rows);
+  const int64_t kb = w->cols / 32;
+  int8_t* qs = nullptr;
+  uint16_t* d = nullptr;
+  int32_t* dmap = nullptr;
+  TRY(dev_alloc((void**)&qs, (size_t)(w->rows * w->cols)));
+  int r = dev_alloc((void**)&d, (size_t)(w->rows * kb) * 2);
+  if (r == EXN_OK) r = dev_alloc((void**)&dmap, map.size() * 4);
+  if (r != EXN_OK) {
+    dev_free(qs);
+    dev_free(d);
+    return r;
+  }
+  // permute whole rows with 2D copies: source row r -> destination row map[r]
+  hipError_t e = hipMemcpyAsync(dmap, map.data(), map.size() * 4, hipMemcpyHostToDevice, w->ctx->stream);
+  for (int64_t rr = 0; rr < w->rows && e == hipSuccess; rr += 32) {
+    const int64_t dst = map[(size_t)rr];
+    e = hipMemcpyAsync(qs + dst * w->cols, w->qs + rr * w->cols, (size_t)(32 * w->cols), hipMemcpyDeviceToDevice,
+                       w->ctx->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(d + dst * kb, w->d + rr * kb, (size_t)(32 * kb) * 2, hipMemcpyDeviceToDevice, w->ctx->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(w->ctx->stream);
+  dev_free(dmap);
+  if (e != hipSuccess) {
+    dev_free(qs);
+    dev_free(d);
+    FAIL(EXN_EHIP, "pairs: %s", hipGetErrorString(e));
+  }
+  dev_free(w->qs);
+  dev_free(w->d);
+  w->qs = qs;
+  w->d = d;
+  w->pairs = true;
+  return EXN_OK;
+}
+
+// --- ops ----------------------------------------------------------------------------
+
+static int check_gemm(const exn_w* w, int64_t n) {
+  if (!w) FAIL(EXN_EINVAL, "null weight");
+  if (n < 0) FAIL(EXN_EINVAL, "n = %lld", (long long)n);
+  if (w->cols % 64) FAIL(EXN_EINVAL, "a product over %lld inputs: not a multiple of 64", (long long)w->cols);
+  return EXN_OK;
+}
+
+static hipError_t gemm_any(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, Epi epi,
+                           const EpiArgs& ea) {
+  if (n == 0) return hipSuccess;
+  if (w->kind == EXN_Q8_0) return gemm_q8(s, x, lda, w->qs, w->d, n, w->rows, w->cols, epi, ea);
+  return gemm_wbf16(s, x, lda, w->wb, n, w->rows, w->cols, epi, ea);
+}
+
+int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n) {
+  TRY(use(ctx));
+  TRY(check_gemm(w, n));
+  if (!x || !y) FAIL(EXN_EINVAL, "null pointer");
+  if (w->pairs) FAIL(EXN_EINVAL, "exn_mm on a paired gate_up matrix: use exn_mm_swiglu");
+  if ((xdt != EXN_DT_F32 && xdt != EXN_DT_BF16) || (ydt != EXN_DT_F32 && ydt != EXN_DT_BF16 && ydt != EXN_DT_F16))
+    FAIL(EXN_EINVAL, "dtype");
+  if (xdt == EXN_DT_F32 && n <= 4 && ydt == EXN_DT_F32) {
+    HIPCHK(gemv_q8(ctx->stream, (const float*)x, w->cols, w->qs, w->d, w->wb, n, w->rows, w->cols, (float*)y, w->rows, 0));
+    return EXN_OK;
+  }
+  const uint16_t* xb = (const uint16_t*)x;
+  if (xdt == EXN_DT_F32) {
+    void* t = nullptr;
+    TRY(ctx_tmp(ctx, (size_t)(n * w->cols) * 2, &t));
+    HIPCHK(f32_to_bf16(ctx->stream, (const float*)x, (uint16_t*)t, n * w->cols));
+    xb = (const uint16_t*)t;
+  }
+  EpiArgs ea{};
+  ea.y = y;
+  ea.ldy = w->rows;
+  HIPCHK(gemm_any(ctx->stream, w, xb, w->cols, n,
+                  ydt == EXN_DT_F32 ? EPI_F32 : (ydt == EXN_DT_F16 ? EPI_F16 : EPI_BF16), ea));
+  return EXN_OK;
+}
+
+int exn_mm_gate_add(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, float* resid, int n0, int p,
+                    int mstride, const float* gate) {
+  TRY(use(ctx));
+  TRY(check_gemm(w, n));
+  if (!x_bf16 || !resid || !gate) FAIL(EXN_EINVAL, "null pointer");
+  if (w->pairs) FAIL(EXN_EINVAL, "a paired gate_up matrix");
+  EpiArgs ea{};
+  ea.resid = resid;
+  ea.ldy = w->rows;
+  ea.gate = gate;
+  ea.n0 = n0;
+  ea.p = p;
+  ea.mstride = mstride;
+  HIPCHK(gemm_any(ctx->stream, w, x_bf16, w->cols, n, EPI_GATE_ADD, ea));
+  return EXN_OK;
+}
+
+int exn_mm_swiglu(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, uint16_t* ff, int64_t n) {
+  TRY(use(ctx));
+  TRY(check_gemm(w, n));
+  if (!x_bf16 || !ff) FAIL(EXN_EINVAL, "null pointer");
+  if (!w->pairs) FAIL(EXN_EINVAL, "exn_mm_swiglu wants a matrix interleaved by exn_weight_pairs");
+  EpiArgs ea{};
+  ea.y = ff;
+  ea.ldy = w->rows / 2;
+  HIPCHK(gemm_any(ctx->stream, w, x_bf16, w->cols, n, EPI_SWIGLU, ea));
+  return EXN_OK;
+}
+
+int exn_ln_mod(exn_ctx* ctx, int n, int n0, int p, int mstride, const float* x, int64_t ldx, const float* mod,
+               void* out, int outdt) {
+  TRY(use(ctx));
+  if (n < 0 || !x || !mod || !out || ldx % 4) FAIL(EXN_EINVAL, "ln_mod arguments");
+  HIPCHK(ln_mod(ctx->stream, n, n0, p, mstride, x, ldx, mod, out, outdt == EXN_DT_BF16));
+  return EXN_OK;
+}
+
+int exn_rms(exn_ctx* ctx, int n, int width, float eps, const float* x, const float* w, void* y, int ydt) {
+  TRY(use(ctx));
+  if (n < 0 || width <= 0 || width % 4 || !x || !w || !y) FAIL(EXN_EINVAL, "rms arguments");
+  HIPCHK(rms_norm(ctx->stream, n, width, eps, x, w, y, ydt == EXN_DT_BF16));
+  return EXN_OK;
+}
+
+int exn_gate_add(exn_ctx* ctx, int64_t count, int width, int n0, int p, int mstride, float* x, const float* h,
+                 const float* gate) {
+  TRY(use(ctx));
+  if (count < 0 || count % 4 || width <= 0 || width % 4 || !x || !h || !gate) FAIL(EXN_EINVAL, "gate_add arguments");
+  HIPCHK(gate_add(ctx->stream, count, width, n0, p, mstride, x, h, gate));
+  return EXN_OK;
+}
+
+int exn_swiglu(exn_ctx* ctx, int64_t n, int f, const uint16_t* gu, uint16_t* out) {
+  TRY(use(ctx));
+  if (n < 0 || f <= 0 || f % 8 || !gu || !out) FAIL(EXN_EINVAL, "swiglu arguments");
+  HIPCHK(swiglu(ctx->stream, n, f, gu, out));
+  return EXN_OK;
+}
+
+int exn_gelu_tanh(exn_ctx* ctx, int64_t count, float* x) {
+  TRY(use(ctx));
+  if (count < 0 || !x) FAIL(EXN_EINVAL, "gelu arguments");
+  HIPCHK(gelu_tanh(ctx->stream, count, x));
+  return EXN_OK;
+}
+
+int exn_silu(exn_ctx* ctx, int64_t count, float* x) {
+  TRY(use(ctx));
+  if (count < 0 || !x) FAIL(EXN_EINVAL, "silu arguments");
+  HIPCHK(silu(ctx->stream, count, x));
+  return EXN_OK;
+}
+
+int exn_qkv_prep(exn_ctx* ctx, const uint16_t* qkv, int64_t n, const float* wq, const float* wk, const float* cs,
+                 uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap) {
+  TRY(use(ctx));
+  if (n < 0 || row0 < 0 || row0 + n > lcap || !qkv || !wq || !wk || !cs || !q || !k || !vt)
+    FAIL(EXN_EINVAL, "qkv_prep arguments");
+  HIPCHK(qkv_prep(ctx->stream, qkv, n, wq, wk, cs, q, k, vt, row0, lcap));
+  return EXN_OK;
+}
+
+int exn_attend(exn_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out, int n, int q0,
+               int p, int l, int64_t lcap, int b0, int b1, float scale) {
+  TRY(use(ctx));
+  if (n < 0 || q0 < 0 || l <= 0 || l > lcap || lcap % 64 || q0 + n > l || p < 0 || p > l || b0 < 0 || b1 < b0 ||
+      b1 > p || !q || !k || !vt || !out)
+    FAIL(EXN_EINVAL, "attend arguments (n %d, q0 %d, p %d, l %d, lcap %lld, b0 %d, b1 %d)", n, q0, p, l,
+         (long long)lcap, b0, b1);
+  HIPCHK(attend(ctx->stream, q, k, vt, out, n, q0, p, l, lcap, b0, b1, scale));
+  return EXN_OK;
+}
+
+int exn_euler(exn_ctx* ctx, int64_t count, float* z, const float* v, float ds) {
+  TRY(use(ctx));
+  if (count < 0 || !z || !v) FAIL(EXN_EINVAL, "euler arguments");
+  HIPCHK(euler(ctx->stream, count, z, v, ds));
+  return EXN_OK;
+}
+
+}  // extern "C"
+
+// --- the model ---------------------------------------------------------------------
+
+namespace {
+
+// dit-expected (src/weights.lisp:22-45): ggml dims (contiguous first) and the synthetic tensor id
+struct Expect {
+  int64_t d0, d1;  // d1 = 1 for a vector
+  int id;
+};
+
+enum Slot { S_NORM_Q = 0, S_NORM_K, S_TO_Q, S_TO_K, S_TO_V, S_TO_OUT, S_GATE_UP, S_OUT };
+static const char* kSlots[8] = {"attn.norm_q.weight",   "attn.norm_k.weight",   "attn.to_q.weight",
+                                "attn.to_k.weight",     "attn.to_v.weight",     "attn.to_out.0.weight",
+                                "img_mlp.gate_up.weight", "img_mlp.out.weight"};
+static const char* kEdge[9] = {"img_in.weight",
+                               "txt_in.text_norm.weight",
+                               "txt_in.in_layer.weight",
+                               "txt_in.out_layer.weight",
+                               "time_text_embed.timestep_embedder.linear_1.weight",
+                               "time_text_embed.timestep_embedder.linear_2.weight",
+                               "modulation.1.weight",
+                               "norm_out.linear.weight",
+                               "proj_out.weight"};
+
+static Expect edge_expect(int i) {
+  static const int64_t dims[9][2] = {{EXN_LAT, EXN_W}, {EXN_W, 1},     {EXN_W, EXN_W}, {EXN_W, EXN_W}, {EXN_FREQ, EXN_W},
+                                     {EXN_W, EXN_W},   {EXN_W, 4 * EXN_W}, {EXN_W, EXN_W}, {EXN_W, EXN_LAT}};
+  return Expect{dims[i][0], dims[i][1], i};
+}
+
+static Expect slot_expect(int layer, int s) {
+  static const int64_t dims[8][2] = {{EXN_HD, 1},    {EXN_HD, 1},    {EXN_W, EXN_W}, {EXN_W, EXN_W},
+                                     {EXN_W, EXN_W}, {EXN_W, EXN_W}, {EXN_W, 2 * EXN_F}, {EXN_F, EXN_W}};
+  return Expect{dims[s][0], dims[s][1], 9 + 8 * layer + s};
+}
+
+struct Layer {
+  exn_w* qkv = nullptr;      // to_q | to_k | to_v rows: 12288 x 4096
+  exn_w* out = nullptr;      // to_out.0
+  exn_w* gate_up = nullptr;  // 24576 x 4096, gate/up interleaved by 32 rows
+  exn_w* down = nullptr;     // img_mlp.out: 4096 x 12288
+  float* norm_q = nullptr;
+  float* norm_k = nullptr;
+  uint8_t have = 0;          // bit per slot
+};
+
+struct Buf {
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+
+}  // namespace
+
+struct exn_dit {
+  exn_ctx* ctx = nullptr;
+  int layers = 32;
+  exn_w* edge[9] = {};      // index as kEdge; [1] unused (text_norm is a vector)
+  float* text_norm = nullptr;  // 1 + w
+  bool have_edge[9] = {};
+  std::vector<Layer> L;
+  int32_t* pair_map = nullptr;  // device row map of the gate_up interleave
+  // scratch
+  std::map<std::string, Buf> bufs;
+  // kept prompt K/V: per layer K [32][lcap][128] and V^T [32][128][lcap], bf16
+  int64_t lcap = 0;
+  std::vector<uint16_t*> kc, vt;
+  uint64_t kept_key = 0;
+  int kept_len = 0;
+  bool kept = false;
+  // the rotary table for sequence rows 0..l-1 (cos, sin of 64 pairs)
+  float* cs = nullptr;
+  int64_t cs_rows = 0;
+  std::vector<int> cs_key;
+  // the residual stream after each block, copied out when set (exn_dit_trace)
+  float* trace = nullptr;
+  int64_t trace_cap = 0;
+  // per-launch event pairs by kernel class (exn_dit_profile)
+  struct Rec {
+    int cls;
+    hipEvent_t a, b;
+    double flops, bytes;
+  };
+  bool prof = false;
+  std::vector<Rec> recs;
+  std::vector<hipEvent_t> pool;
+  size_t pool_used = 0;
+};
+
+static hipEvent_t prof_event(exn_dit* d) {
+  if (d->pool_used == d->pool.size()) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    d->pool.push_back(e);
+  }
+  return d->pool[d->pool_used++];
+}
+
+// a recorded launch: the start event before it, the end event after it
+struct ProfScope {
+  exn_dit* d;
+  int cls;
+  double flops, bytes;
+  hipEvent_t a = nullptr;
+  ProfScope(exn_dit* d_, int c, double f, double b) : d(d_), cls(c), flops(f), bytes(b) {
+    if (d->prof && (a = prof_event(d))) (void)hipEventRecord(a, d->ctx->stream);
+  }
+  ~ProfScope() {
+    if (!a) return;
+    hipEvent_t b = prof_event(d);
+    if (!b) return;
+    (void)hipEventRecord(b, d->ctx->stream);
+    d->recs.push_back(exn_dit::Rec{cls, a, b, flops, bytes});
+  }
+};
+
+static int dit_buf(exn_dit* d, const char* key, size_t bytes, void** out) {
+  Buf& b = d->bufs[key];
+  if (b.bytes < bytes) {
+    HIPCHK(hipStreamSynchronize(d->ctx->stream));
+    dev_free(b.p);
+    b.p = nullptr;
+    b.bytes = 0;
+    TRY(dev_alloc(&b.p, bytes));
+    b.bytes = bytes;
+  }
+  *out = b.p;
+  return EXN_OK;
+}
+
+static void dit_free_scratch(exn_dit* d) {
+  for (auto& kv : d->bufs) dev_free(kv.second.p);
+  d->bufs.clear();
+  for (auto p : d->kc) dev_free(p);
+  for (auto p : d->vt) dev_free(p);
+  d->kc.clear();
+  d->vt.clear();
+  d->lcap = 0;
+  d->kept = false;
+  d->kept_key = 0;
+  d->kept_len = 0;
+  dev_free(d->cs);
+  d->cs = nullptr;
+  d->cs_rows = 0;
+  d->cs_key.clear();
+}
+
+// find NAME in dit-expected: edge index (>= 0) or layer/slot
+static bool lookup(const exn_dit* d, const char* name, int* edge, int* layer, int* slot) {
+  *edge = *layer = *slot = -1;
+  for (int i = 0; i < 9; ++i)
+    if (!strcmp(name, kEdge[i])) {
+      *edge = i;
+      return true;
+    }
+  const char* pre = "transformer_blocks.";
+  if (strncmp(name, pre, strlen(pre))) return false;
+  const char* r = name + strlen(pre);
+  char* end = nullptr;
+  const long li = strtol(r, &end, 10);
+  if (end == r || *end != '.' || li < 0 || li >= d->layers) return false;
+  for (int s = 0; s < 8; ++s)
+    if (!strcmp(end + 1, kSlots[s])) {
+      *layer = (int)li;
+      *slot = s;
+      return true;
+    }
+  return false;
+}
+
+extern "C" {
+
+int exn_dit_create(exn_ctx* ctx, int layers, exn_dit** out) {
+  TRY(use(ctx));
+  if (!out) FAIL(EXN_EINVAL, "null output");
+  *out = nullptr;
+  if (layers < 1 || layers > 32) FAIL(EXN_EINVAL, "layers %d: 1..32", layers);
+  exn_dit* d = new exn_dit();
+  d->ctx = ctx;
+  d->layers = layers;
+  d->L.resize((size_t)layers);
+  const std::vector<int32_t> map = pair_rows(2 * EXN_F);
+  int r = dev_alloc((void**)&d->pair_map, map.size() * 4);
+  if (r == EXN_OK) {
+    hipError_t e = hipMemcpy(d->pair_map, map.data(), map.size() * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      exn::set_error("pair map upload: %s", hipGetErrorString(e));
+      r = EXN_EHIP;
+    }
+  }
+  if (r != EXN_OK) {
+    dev_free(d->pair_map);
+    delete d;
+    return r;
+  }
+  *out = d;
+  return EXN_OK;
+}
+
+int exn_dit_destroy(exn_dit* d) {
+  if (!d) return EXN_OK;
+  (void)hipSetDevice(d->ctx->device);
+  (void)hipStreamSynchronize(d->ctx->stream);
+  dit_free_scratch(d);
+  for (auto& w : d->edge) exn_weight_free(w);
+  for (auto& l : d->L) {
+    exn_weight_free(l.qkv);
+    exn_weight_free(l.out);
+    exn_weight_free(l.gate_up);
+    exn_weight_free(l.down);
+    dev_free(l.norm_q);
+    dev_free(l.norm_k);
+  }
+  dev_free(d->text_norm);
+  dev_free(d->pair_map);
+  for (auto e : d->pool) (void)hipEventDestroy(e);
+  delete d;
+  return EXN_OK;
+}
+
+int exn_dit_profile(exn_dit* d, int on) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  TRY(use(d->ctx));
+  if (on) {
+    HIPCHK(hipStreamSynchronize(d->ctx->stream));
+    d->recs.clear();
+    d->pool_used = 0;
+  }
+  d->prof = on != 0;
+  return EXN_OK;
+}
+
+int exn_dit_profile_read(exn_dit* d, int cls, double* ms, int64_t* launches, double* flops, double* bytes) {
+  if (!d || cls < 0 || cls >= EXN_PROF_CLASSES) FAIL(EXN_EINVAL, "profile class %d", cls);
+  TRY(use(d->ctx));
+  HIPCHK(hipStreamSynchronize(d->ctx->stream));
+  double t = 0, f = 0, b = 0;
+  int64_t c = 0;
+  for (const auto& r : d->recs) {
+    if (r.cls != cls) continue;
+    float e = 0.f;
+    HIPCHK(hipEventElapsedTime(&e, r.a, r.b));
+    t += e;
+    f += r.flops;
+    b += r.bytes;
+    ++c;
+  }
+  if (ms) *ms = t;
+  if (launches) *launches = c;
+  if (flops) *flops = f;
+  if (bytes) *bytes = b;
+  return EXN_OK;
+}
+
+int exn_dit_trace(exn_dit* d, float* buf, int64_t cap) {
+  if (!d || (buf && cap < 0)) FAIL(EXN_EINVAL, "trace arguments");
+  d->trace = buf;
+  d->trace_cap = buf ? cap : 0;
+  return EXN_OK;
+}
+
+int exn_dit_release(exn_dit* d) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  TRY(use(d->ctx));
+  HIPCHK(hipStreamSynchronize(d->ctx->stream));
+  dit_free_scratch(d);
+  return EXN_OK;
+}
+
+int exn_dit_memory(exn_dit* d, int64_t* weights, int64_t* scratch) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  int64_t w = 0, s = 0;
+  auto wb = [](const exn_w* x) -> int64_t {
+    if (!x) return 0;
+    return x->kind == EXN_Q8_0 ? x->rows * x->cols + x->rows * x->cols / 16 : 2 * x->rows * x->cols;
+  };
+  for (auto x : d->edge) w += wb(x);
+  for (auto& l : d->L) w += wb(l.qkv) + wb(l.out) + wb(l.gate_up) + wb(l.down) + 2 * 4 * EXN_HD;
+  for (auto& kv : d->bufs) s += (int64_t)kv.second.bytes;
+  s += (int64_t)(d->kc.size() + d->vt.size()) * d->lcap * EXN_W * 2 + d->cs_rows * 128 * 4;
+  if (weights) *weights = w;
+  if (scratch) *scratch = s;
+  return EXN_OK;
+}
+
+// the layer's fused matrix and the rows a tensor takes in it
+static int layer_target(exn_dit* d, int layer, int slot, exn_w** w, int64_t* row0, const int32_t** map) {
+  Layer& L = d->L[(size_t)layer];
+  *row0 = 0;
+  *map = nullptr;
+  exn_w** slotp = nullptr;
+  int64_t rows = EXN_W, cols = EXN_W;
+  switch (slot) {
+    case S_TO_Q: case S_TO_K: case S_TO_V:
+      slotp = &L.qkv; rows = 3 * EXN_W; *row0 = (int64_t)(slot - S_TO_Q) * EXN_W; break;
+    case S_TO_OUT: slotp = &L.out; break;
+    case S_GATE_UP: slotp = &L.gate_up; rows = 2 * EXN_F; *map = d->pair_map; break;
+    case S_OUT: slotp = &L.down; cols = EXN_F; break;
+    default: FAIL(EXN_EINVAL, "not a matrix slot");
+  }
+  if (!*slotp) {
+    TRY(w_new(d->ctx, EXN_Q8_0, rows, cols, slotp));
+    if (slot == S_GATE_UP) (*slotp)->pairs = true;
+  }
+  *w = *slotp;
+  return EXN_OK;
+}
+
+static int set_vector(exn_dit* d, float** dst, int kind, const void* data, int64_t n, bool plus_one) {
+  std::vector<float> v((size_t)n);
+  if (kind == EXN_F32) {
+    memcpy(v.data(), data, (size_t)n * 4);
+  } else if (kind == EXN_BF16) {
+    const uint16_t* b = (const uint16_t*)data;
+    for (int64_t i = 0; i < n; ++i) {
+      const uint32_t u = (uint32_t)b[i] << 16;
+      memcpy(&v[(size_t)i], &u, 4);
+    }
+  } else {
+    FAIL(EXN_EINVAL, "a vector of kind %d (F32 or BF16 expected)", kind);
+  }
+  if (plus_one)
+    for (auto& x : v) x = 1.f + x;
+  if (!*dst) TRY(dev_alloc((void**)dst, (size_t)n * 4));
+  HIPCHK(hipMemcpy(*dst, v.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+  return EXN_OK;
+}
+
+int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_t d0, int64_t d1) {
+  if (!d || !name || !data) FAIL(EXN_EINVAL, "null argument");
+  TRY(use(d->ctx));
+  int edge, layer, slot;
+  if (!lookup(d, name, &edge, &layer, &slot)) FAIL(EXN_EINVAL, "%s: not a tensor of the DiT", name);
+  const Expect ex = edge >= 0 ? edge_expect(edge) : slot_expect(layer, slot);
+  if (d0 != ex.d0 || d1 != ex.d1)
+    FAIL(EXN_EINVAL, "%s is (%lld %lld), not (%lld %lld)", name, (long long)d0, (long long)d1, (long long)ex.d0,
+         (long long)ex.d1);
+  exn_ctx* ctx = d->ctx;
+  if (ex.d1 == 1) {  // a vector
+    if (edge == 1) {
+      TRY(set_vector(d, &d->text_norm, kind, data, d0, true));
+      d->have_edge[1] = true;
+    } else {
+      Layer& L = d->L[(size_t)layer];
+      TRY(set_vector(d, slot == S_NORM_Q ? &L.norm_q : &L.norm_k, kind, data, d0, false));
+      L.have |= (uint8_t)(1u << slot);
+    }
+    return EXN_OK;
+  }
+  if (kind != EXN_Q8_0 && kind != EXN_F32 && kind != EXN_BF16) FAIL(EXN_EINVAL, "%s: kind %d", name, kind);
+  const int64_t rows = d1, cols = d0;
+  if (edge >= 0) {
+    exn_weight_free(d->edge[edge]);
+    d->edge[edge] = nullptr;
+    int r = kind == EXN_Q8_0 ? exn_weight_q8_0(ctx, data, rows, cols, &d->edge[edge])
+            : kind == EXN_F32 ? exn_weight_f32(ctx, (const float*)data, rows, cols, &d->edge[edge])
+                              : exn_weight_bf16(ctx, (const uint16_t*)data, rows, cols, &d->edge[edge]);
+    TRY(r);
+    d->have_edge[edge] = true;
+    return EXN_OK;
+  }
+  if (kind != EXN_Q8_0) FAIL(EXN_EINVAL, "%s: block matrices must be Q8_0 (the real DiT's are)", name);
+  exn_w* w = nullptr;
+  int64_t row0 = 0;
+  const int32_t* map = nullptr;
+  TRY(layer_target(d, layer, slot, &w, &row0, &map));
+  TRY(upload_q8_blocks(ctx, data, rows, cols, map, w->qs + row0 * cols, w->d + row0 * (cols / 32)));
+  d->L[(size_t)layer].have |= (uint8_t)(1u << slot);
+  return EXN_OK;
+}
+
+int exn_dit_synth(exn_dit* d, uint64_t seed) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  TRY(use(d->ctx));
+  hipStream_t s = d->ctx->stream;
+  for (int i = 0; i < 9; ++i) {
+    const Expect ex = edge_expect(i);
+    const uint64_t key = gen_key(seed, (uint64_t)ex.id);
+    if (i == 1) {
+      if (!d->text_norm) TRY(dev_alloc((void**)&d->text_norm, EXN_W * 4));
+      HIPCHK(synth_normal(s, key, EXN_W, 1.f, 0.05f, 1, d->text_norm));  // used as 1 + 0.05 z
+    } else {
+      if (!d->edge[i] || d->edge[i]->kind != EXN_Q8_0) {
+        exn_weight_free(d->edge[i]);
+        d->edge[i] = nullptr;
+        TRY(w_new(d->ctx, EXN_Q8_0, ex.d1, ex.d0, &d->edge[i]));
+      }
+      HIPCHK(synth_q8(s, key, ex.d1, ex.d0, ex.d0 / 32, nullptr, d->edge[i]->qs, d->edge[i]->d));
+    }
+    d->have_edge[i] = true;
+  }
+  for (int layer = 0; layer < d->layers; ++layer) {
+    Layer& L = d->L[(size_t)layer];
+    for (int sl = 0; sl < 8; ++sl) {
+      const Expect ex = slot_expect(layer, sl);
+      const uint64_t key = gen_key(seed, (uint64_t)ex.id);
+      if (sl == S_NORM_Q || sl == S_NORM_K) {
+        float** v = sl == S_NORM_Q ? &L.norm_q : &L.norm_k;
+        if (!*v) TRY(dev_alloc((void**)v, EXN_HD * 4));
+        HIPCHK(synth_normal(s, key, EXN_HD, 1.f, 0.05f, 1, *v));
+      } else {
+        exn_w* w = nullptr;
+        int64_t row0 = 0;
+        const int32_t* map = nullptr;
+        TRY(layer_target(d, layer, sl, &w, &row0, &map));
+        HIPCHK(synth_q8(s, key, ex.d1, ex.d0, ex.d0 / 32, map, w->qs + row0 * ex.d0, w->d + row0 * (ex.d0 / 32)));
+      }
+      L.have |= (uint8_t)(1u << sl);
+    }
+  }
+  HIPCHK(hipStreamSynchronize(s));
+  return EXN_OK;
+}
+
+int exn_dit_check(exn_dit* d) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  std::string missing;
+  int count = 0;
+  for (int i = 0; i < 9; ++i)
+    if (!d->have_edge[i]) {
+      if (count++ < 8) missing += std::string("\n  missing ") + kEdge[i];
+    }
+  for (int l = 0; l < d->layers; ++l)
+    for (int s = 0; s < 8; ++s)
+      if (!(d->L[(size_t)l].have & (1u << s))) {
+        if (count++ < 8) missing += "\n  missing transformer_blocks." + std::to_string(l) + "." + kSlots[s];
+      }
+  if (count) FAIL(EXN_ESTATE, "%d tensors missing:%s%s", count, missing.c_str(), count > 8 ? "\n  ..." : "");
+  return EXN_OK;
+}
+
+}  // extern "C"
+
+// --- a step (dit-velocity, src/cuda-dit.lisp:137-243) --------------------------------
+
+// every row's (frame, row, col) -- dit-positions (src/host.lisp:37-50)
+static void positions(int p, int h, int w, int a, int rh, int rw, bool edit, std::vector<int>& pos) {
+  pos.clear();
+  auto image = [&](int frame, int hh, int ww) {
+    for (int r = 0; r < hh; ++r)
+      for (int c = 0; c < ww; ++c) {
+        pos.push_back(frame);
+        pos.push_back(r - (hh - hh / 2));
+        pos.push_back(c - (ww - ww / 2));
+      }
+  };
+  auto text = [&](int x) { pos.push_back(x); pos.push_back(x); pos.push_back(x); };
+  if (!edit) {
+    for (int i = 0; i < p; ++i) text(i);
+    image(p, h, w);
+  } else {
+    const int after = p - a - rh * rw, start = a + (rh > rw ? rh : rw);
+    for (int i = 0; i < a; ++i) text(i);
+    image(a, rh, rw);
+    for (int i = 0; i < after; ++i) text(start + i);
+    image(start + after, h, w);
+  }
+}
+
+// rope-table (src/host.lisp:19-30): cos, sin of each row's 64 angles, in double, rounded
+static void rope_table(const std::vector<int>& pos, std::vector<float>& cs) {
+  static const int axes[3] = {16, 56, 56};
+  const size_t rows = pos.size() / 3;
+  cs.assign(rows * 128, 0.f);
+  for (size_t t = 0; t < rows; ++t) {
+    int j = 0;
+    for (int a = 0; a < 3; ++a)
+      for (int i = 0; i < axes[a] / 2; ++i, ++j) {
+        const double ang = (double)pos[3 * t + a] * (1.0 / std::pow(10000.0, (double)(2 * i) / axes[a]));
+        cs[t * 128 + 2 * j] = (float)std::cos(ang);
+        cs[t * 128 + 2 * j + 1] = (float)std::sin(ang);
+      }
+  }
+}
+
+// timestep-embedding (src/host.lisp:9-15) of t and of 0, in double on the device: 2 x 256 floats
+__global__ void k_time_embed(double t, float* __restrict__ emb) {
+  const int j = threadIdx.x;  // 128 threads
+  const double f = exp(-log(10000.0) * j / 128.0);
+  const double a = t * f;
+  emb[j] = (float)cos(a);
+  emb[128 + j] = (float)sin(a);
+  emb[256 + j] = 1.f;
+  emb[256 + 128 + j] = 0.f;
+}
+
+static int ensure_kv(exn_dit* d, int64_t l, int keep_rows) {
+  const int64_t need = (l + 63) / 64 * 64;
+  if (d->lcap >= need && (int)d->kc.size() == d->layers) return EXN_OK;
+  const int64_t lcap = need + 256;  // room for a longer prompt without moving again
+  hipStream_t s = d->ctx->stream;
+  std::vector<uint16_t*> kc((size_t)d->layers, nullptr), vt((size_t)d->layers, nullptr);
+  int r = EXN_OK;
+  for (int i = 0; i < d->layers && r == EXN_OK; ++i) {
+    r = dev_alloc((void**)&kc[(size_t)i], (size_t)(EXN_H * lcap * EXN_HD) * 2);
+    if (r == EXN_OK) r = dev_alloc((void**)&vt[(size_t)i], (size_t)(EXN_H * lcap * EXN_HD) * 2);
+    if (r == EXN_OK) {
+      // keys past l are masked, but V^T's columns there enter P V with P = 0: keep them finite
+      if (hipMemsetAsync(kc[(size_t)i], 0, (size_t)(EXN_H * lcap * EXN_HD) * 2, s) != hipSuccess ||
+          hipMemsetAsync(vt[(size_t)i], 0, (size_t)(EXN_H * lcap * EXN_HD) * 2, s) != hipSuccess)
+        r = EXN_EHIP;
+    }
+    if (r == EXN_OK && keep_rows > 0 && i < (int)d->kc.size()) {  // carry the kept prompt rows over
+      if (hipMemcpy2DAsync(kc[(size_t)i], (size_t)(lcap * EXN_HD * 2), d->kc[(size_t)i], (size_t)(d->lcap * EXN_HD * 2),
+                           (size_t)(keep_rows * EXN_HD * 2), EXN_H, hipMemcpyDeviceToDevice, s) != hipSuccess ||
+          hipMemcpy2DAsync(vt[(size_t)i], (size_t)(lcap * 2), d->vt[(size_t)i], (size_t)(d->lcap * 2),
+                           (size_t)(keep_rows * 2), EXN_H * EXN_HD, hipMemcpyDeviceToDevice, s) != hipSuccess)
+        r = EXN_EHIP;
+    }
+  }
+  if (r == EXN_OK && hipStreamSynchronize(s) != hipSuccess) r = EXN_EHIP;
+  if (r != EXN_OK) {
+    for (auto p : kc) dev_free(p);
+    for (auto p : vt) dev_free(p);
+    if (r == EXN_EHIP) exn::set_error("prefix K/V allocation: %s", hipGetErrorString(hipGetLastError()));
+    return r;
+  }
+  for (auto p : d->kc) dev_free(p);
+  for (auto p : d->vt) dev_free(p);
+  d->kc = kc;
+  d->vt = vt;
+  d->lcap = lcap;
+  return EXN_OK;
+}
+
+static int ensure_rope(exn_dit* d, int p, int h, int w, int a, int rh, int rw, bool edit) {
+  const std::vector<int> key = {p, h, w, a, rh, rw, edit ? 1 : 0};
+  if (d->cs && d->cs_key == key) return EXN_OK;
+  std::vector<int> pos;
+  positions(p, h, w, a, rh, rw, edit, pos);
+  std::vector<float> cs;
+  rope_table(pos, cs);
+  const int64_t rows = (int64_t)(pos.size() / 3);
+  HIPCHK(hipStreamSynchronize(d->ctx->stream));
+  if (d->cs_rows < rows) {
+    dev_free(d->cs);
+    d->cs = nullptr;
+    d->cs_rows = 0;
+    TRY(dev_alloc((void**)&d->cs, (size_t)rows * 128 * 4));
+    d->cs_rows = rows;
+  }
+  HIPCHK(hipMemcpy(d->cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  d->cs_key = key;
+  return EXN_OK;
+}
+
+static int velocity(exn_dit* d, const float* context, int ptext, const float* latent, int h, int w, double sigma,
+                    uint64_t prefix_key, int ref_a, const float* ref_latent, int rh, int rw, float* v) {
+  TRY(exn_dit_check(d));
+  if (h <= 0 || w <= 0 || ptext < 0 || !latent || !v) FAIL(EXN_EINVAL, "velocity: h %d, w %d, p %d", h, w, ptext);
+  const bool edit = ref_latent != nullptr;
+  if (edit && (rh <= 0 || rw <= 0 || ref_a < 0 || ref_a > ptext)) FAIL(EXN_EINVAL, "reference picture: a %d, %d x %d", ref_a, rh, rw);
+  exn_ctx* ctx = d->ctx;
+  hipStream_t s = ctx->stream;
+  const int64_t nimg = (int64_t)h * w;
+  const int nref = edit ? rh * rw : 0, a = edit ? ref_a : 0;
+  const int p = ptext + nref;  // the prefix: text and the reference picture
+  const bool cached = prefix_key != 0 && d->kept && d->kept_key == prefix_key && d->kept_len == p;
+  const int n0 = cached ? p : 0;
+  const int64_t n = cached ? nimg : p + nimg, l = p + nimg;
+  if (!cached && ptext > 0 && !context) FAIL(EXN_EINVAL, "velocity: null context on an uncached pass");
+  if (l > (1 << 24)) FAIL(EXN_EINVAL, "sequence of %lld rows", (long long)l);
+
+  TRY(ensure_kv(d, l, cached ? p : 0));
+  TRY(ensure_rope(d, p, h, w, a, rh, rw, edit));
+  if (!cached) d->kept = false;
+
+  float *emb, *e1, *e2, *mod, *sc, *x, *vrows, *tok;
+  uint16_t *y, *qkv, *q, *att, *ff;
+  TRY(dit_buf(d, "emb", 512 * 4, (void**)&emb));
+  TRY(dit_buf(d, "e1", 2 * EXN_W * 4, (void**)&e1));
+  TRY(dit_buf(d, "e2", 2 * EXN_W * 4, (void**)&e2));
+  TRY(dit_buf(d, "mod", 2 * 4 * EXN_W * 4, (void**)&mod));
+  TRY(dit_buf(d, "sc", EXN_W * 4, (void**)&sc));
+  TRY(dit_buf(d, "x", (size_t)(l * EXN_W) * 4, (void**)&x));
+  TRY(dit_buf(d, "y", (size_t)(l * EXN_W) * 2, (void**)&y));
+  TRY(dit_buf(d, "qkv", (size_t)(l * 3 * EXN_W) * 2, (void**)&qkv));
+  TRY(dit_buf(d, "q", (size_t)(l * EXN_W) * 2, (void**)&q));
+  TRY(dit_buf(d, "att", (size_t)(l * EXN_W) * 2, (void**)&att));
+  TRY(dit_buf(d, "ff", (size_t)(l * EXN_F) * 2, (void**)&ff));
+  TRY(dit_buf(d, "tok", (size_t)((nimg > nref ? nimg : nref) * EXN_LAT) * 4, (void**)&tok));
+  TRY(dit_buf(d, "vrows", (size_t)(nimg * EXN_LAT) * 4, (void**)&vrows));
+
+  // an edge product in fp32: Y (m rows, ldy apart) = X (m rows of the matrix's inputs) W^T
+  auto edge_mm = [&](int e, const float* xin, int64_t m, float* yout, int gelu) {
+    const exn_w* W = d->edge[e];
+    return gemm_f32(s, xin, W->cols, W->qs, W->d, W->wb, m, W->rows, W->cols, yout, W->rows, gelu);
+  };
+  {
+  ProfScope prologue(d, EXN_PROF_EDGE, 0, 0);
+  // the timestep: t and 0 through the embedder, SiLU, the shared modulation (src/cuda-dit.lisp:157-167)
+  hipLaunchKernelGGL(k_time_embed, dim3(1), dim3(128), 0, s, 1000.0 * sigma, emb);
+  HIPCHK(hipGetLastError());
+  auto gv = [&](int e, const float* xin, int64_t m, float* yout, int act) {
+    const exn_w* W = d->edge[e];
+    return gemv_q8(s, xin, W->cols, W->qs, W->d, W->wb, m, W->rows, W->cols, yout, W->rows, act);
+  };
+  HIPCHK(gv(4, emb, 2, e1, 1));
+  HIPCHK(gv(5, e1, 2, e2, 1));
+  HIPCHK(gv(6, e2, 2, mod, 0));
+  HIPCHK(gv(7, e2, 1, sc, 0));
+
+  // the joint sequence: the prompt through txt_in (unless cached), the image through img_in
+  if (!cached && ptext > 0) {
+    float *t1, *h1;
+    TRY(dit_buf(d, "t1", (size_t)(ptext * EXN_W) * 4, (void**)&t1));
+    TRY(dit_buf(d, "h1", (size_t)(ptext * EXN_W) * 4, (void**)&h1));
+    HIPCHK(rms_norm(s, ptext, EXN_W, 1e-6f, context, d->text_norm, t1, 0));
+    HIPCHK(edge_mm(2, t1, ptext, h1, 1));
+    float* txt = x;
+    if (edit) TRY(dit_buf(d, "txt", (size_t)(ptext * EXN_W) * 4, (void**)&txt));
+    HIPCHK(edge_mm(3, h1, ptext, txt, 0));
+    if (edit) {  // text before the picture, the picture through img_in, the text after
+      HIPCHK(hipMemcpyAsync(x, txt, (size_t)a * EXN_W * 4, hipMemcpyDeviceToDevice, s));
+      HIPCHK(hipMemcpyAsync(x + (int64_t)(a + nref) * EXN_W, txt + (int64_t)a * EXN_W, (size_t)(ptext - a) * EXN_W * 4,
+                            hipMemcpyDeviceToDevice, s));
+    }
+  }
+  if (!cached && edit) {
+    HIPCHK(latent_rows(s, ref_latent, nref, tok));
+    HIPCHK(edge_mm(0, tok, nref, x + (int64_t)a * EXN_W, 0));
+  }
+  HIPCHK(latent_rows(s, latent, nimg, tok));
+  HIPCHK(edge_mm(0, tok, nimg, x + (int64_t)(p - n0) * EXN_W, 0));
+  }
+  EpiArgs ea{};
+
+  // the blocks (src/cuda-dit.lisp:196-231)
+  const int ms = 4 * EXN_W;
+  const int b0 = a, b1 = a + nref;
+  double pairs = 0;  // visible (query, key) pairs under xa_lim
+  for (int64_t g = n0; g < n0 + n; ++g)
+    pairs += (double)(g >= p ? l : (g >= b0 && g < b1 ? b1 : g + 1));
+  const double nd = (double)n, Wd = EXN_W, Fd = EXN_F;
+  const double ln_bytes = nd * Wd * (4 + 2), qkv_bytes = nd * 3 * Wd * 2 * 2 + nd * 128 * 4;
+  if (d->trace && n * EXN_W <= d->trace_cap)
+    HIPCHK(hipMemcpyAsync(d->trace, x, (size_t)(n * EXN_W) * 4, hipMemcpyDeviceToDevice, s));
+  for (int il = 0; il < d->layers; ++il) {
+    Layer& L = d->L[(size_t)il];
+    {
+      ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes);
+      HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 0 * EXN_W, y, 1));
+    }
+    {
+      ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
+      ea = EpiArgs{};
+      ea.y = qkv;
+      ea.ldy = 3 * EXN_W;
+      HIPCHK(gemm_any(s, L.qkv, y, EXN_W, n, EPI_F16, ea));
+    }
+    {
+      ProfScope ps(d, EXN_PROF_QKV_PREP, 0, qkv_bytes);
+      HIPCHK(qkv_prep(s, qkv, n, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap));
+    }
+    {
+      ProfScope ps(d, EXN_PROF_ATTEND, 4.0 * EXN_HD * EXN_H * pairs, nd * Wd * 2 * 2 + 2.0 * l * Wd * 2);
+      HIPCHK(attend(s, q, d->kc[(size_t)il], d->vt[(size_t)il], att, (int)n, n0, p, (int)l, d->lcap, b0, b1, 1.f));
+    }
+    {
+      ProfScope ps(d, EXN_PROF_OUT, 2 * nd * Wd * Wd, nd * Wd * 2 + Wd * Wd * 1.0625 + nd * Wd * 4 * 2);
+      ea = EpiArgs{};
+      ea.resid = x;
+      ea.ldy = EXN_W;
+      ea.gate = mod + 1 * EXN_W;
+      ea.n0 = n0;
+      ea.p = p;
+      ea.mstride = ms;
+      HIPCHK(gemm_any(s, L.out, att, EXN_W, n, EPI_GATE_ADD, ea));
+    }
+    {
+      ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes);
+      HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 2 * EXN_W, y, 1));
+    }
+    {
+      ProfScope ps(d, EXN_PROF_GATE_UP, 2 * nd * Wd * 2 * Fd, nd * Wd * 2 + 2 * Fd * Wd * 1.0625 + nd * Fd * 2);
+      ea = EpiArgs{};
+      ea.y = ff;
+      ea.ldy = EXN_F;
+      HIPCHK(gemm_any(s, L.gate_up, y, EXN_W, n, EPI_SWIGLU, ea));
+    }
+    {
+      ProfScope ps(d, EXN_PROF_DOWN, 2 * nd * Fd * Wd, nd * Fd * 2 + Fd * Wd * 1.0625 + nd * Wd * 4 * 2);
+      ea = EpiArgs{};
+      ea.resid = x;
+      ea.ldy = EXN_W;
+      ea.gate = mod + 3 * EXN_W;
+      ea.n0 = n0;
+      ea.p = p;
+      ea.mstride = ms;
+      HIPCHK(gemm_any(s, L.down, ff, EXN_F, n, EPI_GATE_ADD, ea));
+    }
+    if (d->trace && (int64_t)(il + 2) * n * EXN_W <= d->trace_cap)
+      HIPCHK(hipMemcpyAsync(d->trace + (int64_t)(il + 1) * n * EXN_W, x, (size_t)(n * EXN_W) * 4,
+                            hipMemcpyDeviceToDevice, s));
+  }
+  if (prefix_key != 0 && !cached) {
+    d->kept = true;
+    d->kept_key = prefix_key;
+    d->kept_len = p;
+  }
+  // the image's rows: LayerNorm * (1 + scale(t)), proj_out (src/cuda-dit.lisp:235-243)
+  ProfScope epilogue(d, EXN_PROF_EDGE, 0, 0);
+  float* yf;
+  TRY(dit_buf(d, "yf", (size_t)(nimg * EXN_W) * 4, (void**)&yf));
+  HIPCHK(ln_mod(s, (int)nimg, 0, 0, 0, x + (int64_t)(p - n0) * EXN_W, EXN_W, sc, yf, 0));
+  HIPCHK(edge_mm(8, yf, nimg, vrows, 0));
+  HIPCHK(rows_to_latent(s, vrows, nimg, v));
+  return EXN_OK;
+}
+
+extern "C" {
+
+int exn_dit_velocity_dev(exn_dit* d, const float* context, int p, const float* latent, int h, int w, double sigma,
+                         uint64_t prefix_key, int ref_a, const float* ref_latent, int rh, int rw, float* v) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  TRY(use(d->ctx));
+  return velocity(d, context, p, latent, h, w, sigma, prefix_key, ref_a, ref_latent, rh, rw, v);
+}
+
+int exn_dit_velocity(exn_dit* d, const float* context, int p, const float* latent, int h, int w, double sigma,
+                     uint64_t prefix_key, int ref_a, const float* ref_latent, int rh, int rw, float* v) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  TRY(use(d->ctx));
+  if (h <= 0 || w <= 0 || p < 0 || !latent || !v || (p > 0 && !context))
+    FAIL(EXN_EINVAL, "velocity: h %d, w %d, p %d", h, w, p);
+  hipStream_t s = d->ctx->stream;
+  const int64_t nimg = (int64_t)h * w;
+  const int64_t nref = ref_latent ? (int64_t)rh * rw : 0;
+  float *dctx = nullptr, *dlat, *dref = nullptr, *dv;
+  if (p > 0) TRY(dit_buf(d, "h_ctx", (size_t)p * EXN_W * 4, (void**)&dctx));
+  TRY(dit_buf(d, "h_lat", (size_t)nimg * EXN_LAT * 4, (void**)&dlat));
+  TRY(dit_buf(d, "h_v", (size_t)nimg * EXN_LAT * 4, (void**)&dv));
+  if (ref_latent) {
+    if (nref <= 0) FAIL(EXN_EINVAL, "reference picture %d x %d", rh, rw);
+    TRY(dit_buf(d, "h_ref", (size_t)nref * EXN_LAT * 4, (void**)&dref));
+    HIPCHK(hipMemcpyAsync(dref, ref_latent, (size_t)nref * EXN_LAT * 4, hipMemcpyHostToDevice, s));
+  }
+  if (p > 0) HIPCHK(hipMemcpyAsync(dctx, context, (size_t)p * EXN_W * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(dlat, latent, (size_t)nimg * EXN_LAT * 4, hipMemcpyHostToDevice, s));
+  TRY(velocity(d, dctx, p, dlat, h, w, sigma, prefix_key, ref_a, dref, rh, rw, dv));
+  HIPCHK(hipMemcpyAsync(v, dv, (size_t)nimg * EXN_LAT * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return EXN_OK;
+}
+
+int exn_dit_generate_dev(exn_dit* d, const float* context, int p, float* z, int h, int w, const double* sigmas,
+                         int nsig, int ref_a, const float* ref_latent, int rh, int rw) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  TRY(use(d->ctx));
+  if (!z || !sigmas || nsig < 2) FAIL(EXN_EINVAL, "generate: %d sigmas", nsig);
+  static uint64_t counter = 0;
+  const uint64_t key = 0x6765000000000000ull + (++counter);  // a fresh key, as edit's (:edit k) is
+  const int64_t count = (int64_t)h * w * EXN_LAT;
+  float* v = nullptr;
+  TRY(dit_buf(d, "gen_v", (size_t)count * 4, (void**)&v));
+  for (int i = 0; i + 1 < nsig; ++i) {
+    TRY(velocity(d, context, p, z, h, w, sigmas[i], key, ref_a, ref_latent, rh, rw, v));
+    HIPCHK(euler(d->ctx->stream, count, z, v, (float)(sigmas[i + 1] - sigmas[i])));
+  }
+  return EXN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,282 @@
+// eltwise.hip -- the DiT's bandwidth kernels: coalesced 16-byte accesses, one
+// pass over HBM each, fp32 arithmetic.
+//
+//   ln_mod      LayerNorm (no affine, eps 1e-6) * (1 + mod[row]); row < p takes
+//               mod row 1 (t = 0), else row 0 -- src/cuda/dit.cu:17-32
+//   rms_norm    x / rms(x) * w (txt_in's text_norm, w = 1 + weight) -- illatio's
+//               v_rms at src/cuda-dit.lisp:176
+//   gate_add    x += tanh(gate[row]) * h -- src/cuda/dit.cu:34-41
+//   swiglu      silu(gu[:, :F]) * gu[:, F:] -- src/cuda/dit.cu:186-192
+//   gelu_tanh   src/cuda/dit.cu:194-199;  silu  src/cuda/dit.cu:201-206
+//   qkv_prep    per head: RMSNorm * w, then the interleaved RoPE (src/cuda/dit.cu:
+//               43-58) of q and k, and v transposed, into the attention's layouts
+//   latent_rows / rows_to_latent   the channel-major latent <-> token rows
+//               (src/cuda-dit.lisp:188-191,238-243)
+//   euler       z += ds * v, two roundings as the host loop's single floats
+//               (src/generate.lisp:133-135)
+#include "exn_common.h"
+
+namespace exn {
+
+static inline unsigned grid_of(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
+
+// sum over a 256-thread block; RED must hold 4 floats and not be reused until a barrier
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// one block a row of 4096: 16 values a thread, kept in registers between the passes
+__global__ void __launch_bounds__(256)
+k_ln_mod(int n, int n0, int p, int mstride, const float* __restrict__ x, int64_t ldx, const float* __restrict__ mod,
+         void* __restrict__ out, int out_bf16) {
+  __shared__ float red[8];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float* r = x + (int64_t)t * ldx;
+  f32x4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = *(const f32x4*)(r + 4 * tid + 1024 * i);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+  const float mean = block_sum256(s, red) * (1.f / 4096.f);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[i][e] -= mean;
+      ss += v[i][e] * v[i][e];
+    }
+  const float inv = rsqrtf(block_sum256(ss, red + 4) * (1.f / 4096.f) + 1e-6f);
+  const float* m = mod + (n0 + t < p ? mstride : 0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = 4 * tid + 1024 * i;
+    const f32x4 mv = *(const f32x4*)(m + c);
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = v[i][e] * inv * (1.f + mv[e]);
+    if (out_bf16) {
+      *(u32x2*)((uint16_t*)out + (int64_t)t * 4096 + c) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    } else {
+      *(f32x4*)((float*)out + (int64_t)t * 4096 + c) = o;
+    }
+  }
+}
+
+hipError_t ln_mod(hipStream_t s, int n, int n0, int p, int mstride, const float* x, int64_t ldx, const float* mod,
+                  void* out, int out_bf16) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_ln_mod, dim3(n), dim3(256), 0, s, n, n0, p, mstride, x, ldx, mod, out, out_bf16);
+  return hipGetLastError();
+}
+
+// y = x / sqrt(mean(x^2) + eps) * w, a block a row of WIDTH (a multiple of 4)
+__global__ void __launch_bounds__(256)
+k_rms(int width, float eps, const float* __restrict__ x, const float* __restrict__ w, void* __restrict__ out,
+      int out_bf16) {
+  __shared__ float red[4];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float* r = x + (int64_t)t * width;
+  float ss = 0.f;
+  for (int c = 4 * tid; c < width; c += 1024) {
+    const f32x4 v = *(const f32x4*)(r + c);
+    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  }
+  const float inv = rsqrtf(block_sum256(ss, red) / (float)width + eps);
+  for (int c = 4 * tid; c < width; c += 1024) {
+    const f32x4 v = *(const f32x4*)(r + c), wv = *(const f32x4*)(w + c);
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = v[e] * inv * wv[e];
+    if (out_bf16)
+      *(u32x2*)((uint16_t*)out + (int64_t)t * width + c) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    else
+      *(f32x4*)((float*)out + (int64_t)t * width + c) = o;
+  }
+}
+
+hipError_t rms_norm(hipStream_t s, int n, int width, float eps, const float* x, const float* w, void* out,
+                    int out_bf16) {
+  if (n <= 0) return hipSuccess;
+  if (width % 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rms, dim3(n), dim3(256), 0, s, width, eps, x, w, out, out_bf16);
+  return hipGetLastError();
+}
+
+// 4 values a thread; COUNT a multiple of 4 and WIDTH of 4
+__global__ void k_gate_add(int64_t count4, int width, int n0, int p, int mstride, float* __restrict__ x,
+                           const float* __restrict__ h, const float* __restrict__ gate) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count4) return;
+  const int64_t e = 4 * i;
+  const int t = n0 + (int)(e / width), c = (int)(e % width);
+  const f32x4 g = *(const f32x4*)(gate + (t < p ? mstride : 0) + c);
+  const f32x4 hv = *(const f32x4*)(h + e);
+  f32x4 xv = *(const f32x4*)(x + e);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) xv[k] += tanh_f(g[k]) * hv[k];
+  *(f32x4*)(x + e) = xv;
+}
+
+hipError_t gate_add(hipStream_t s, int64_t count, int width, int n0, int p, int mstride, float* x, const float* h,
+                    const float* gate) {
+  if (count % 4 || width % 4) return hipErrorInvalidValue;
+  if (count == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gate_add, dim3(grid_of(count / 4, 256)), dim3(256), 0, s, count / 4, width, n0, p, mstride, x,
+                     h, gate);
+  return hipGetLastError();
+}
+
+// bf16 gu (n x 2f) -> bf16 out (n x f), 8 values a thread
+__global__ void k_swiglu(int64_t count8, int f, const uint16_t* __restrict__ gu, uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count8) return;
+  const int64_t e = 8 * i, t = e / f, j = e % f;
+  const u32x4 g = *(const u32x4*)(gu + t * 2 * f + j);
+  const u32x4 u = *(const u32x4*)(gu + t * 2 * f + f + j);
+  u32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float g0 = bf16_lo(g[k]), g1 = bf16_hi(g[k]);
+    o[k] = pack_bf16x2(silu_f(g0) * bf16_lo(u[k]), silu_f(g1) * bf16_hi(u[k]));
+  }
+  *(u32x4*)(out + e) = o;
+}
+
+hipError_t swiglu(hipStream_t s, int64_t n, int f, const uint16_t* gu, uint16_t* out) {
+  if (f % 8) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_swiglu, dim3(grid_of(n * f / 8, 256)), dim3(256), 0, s, n * f / 8, f, gu, out);
+  return hipGetLastError();
+}
+
+__global__ void k_gelu(int64_t count, float* __restrict__ x) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) x[i] = gelu_tanh_f(x[i]);
+}
+
+__global__ void k_silu(int64_t count, float* __restrict__ x) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) x[i] = silu_f(x[i]);
+}
+
+hipError_t gelu_tanh(hipStream_t s, int64_t count, float* x) {
+  if (count == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gelu, dim3(grid_of(count, 256)), dim3(256), 0, s, count, x);
+  return hipGetLastError();
+}
+
+hipError_t silu(hipStream_t s, int64_t count, float* x) {
+  if (count == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_silu, dim3(grid_of(count, 256)), dim3(256), 0, s, count, x);
+  return hipGetLastError();
+}
+
+// qkv: fp16 rows of 3 x 4096 (q | k | v) for tokens 0..n-1, token t being
+// sequence row row0 + t.  Writes, all fp16 (the attention's operands, as the
+// reference's halves): q ([32][n][128], scaled by qscale after the rotation),
+// k into kc ([32][lcap][128]) rows row0.., v transposed into vt
+// ([32][128][lcap]) columns row0...  cs: cos, sin for 64 pairs, 128 floats a
+// sequence row.  grid (ceil(n/64), 32), block 256.
+__global__ void __launch_bounds__(256)
+k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict__ wq, const float* __restrict__ wk,
+           const float* __restrict__ cs, float qscale, uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
+           uint16_t* __restrict__ vt, int64_t row0, int64_t lcap) {
+  __shared__ uint16_t tile[64][128 + 2];
+  const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * 64;
+  const float wq0 = wq[2 * lane], wq1 = wq[2 * lane + 1], wk0 = wk[2 * lane], wk1 = wk[2 * lane + 1];
+  for (int tt = 0; tt < 16; ++tt) {
+    const int64_t t = t0 + wave * 16 + tt;
+    if (t >= n) break;
+    const uint16_t* rq = qkv + t * (3 * 4096) + h * 128;
+    const uint32_t uq = *(const uint32_t*)(rq + 2 * lane);
+    const uint32_t uk = *(const uint32_t*)(rq + 4096 + 2 * lane);
+    const float2 c = *(const float2*)(cs + (row0 + t) * 128 + 2 * lane);
+    {
+      const float a = f16_lo(uq), b = f16_hi(uq);
+      const float inv = rsqrtf(wave_sum(a * a + b * b) * (1.f / 128.f) + 1e-6f);
+      const float an = a * inv * wq0, bn = b * inv * wq1;
+      *(uint32_t*)(q + ((int64_t)h * n + t) * 128 + 2 * lane) =
+          pack_f16x2((an * c.x - bn * c.y) * qscale, (an * c.y + bn * c.x) * qscale);
+    }
+    {
+      const float a = f16_lo(uk), b = f16_hi(uk);
+      const float inv = rsqrtf(wave_sum(a * a + b * b) * (1.f / 128.f) + 1e-6f);
+      const float an = a * inv * wk0, bn = b * inv * wk1;
+      *(uint32_t*)(kc + ((int64_t)h * lcap + row0 + t) * 128 + 2 * lane) =
+          pack_f16x2(an * c.x - bn * c.y, an * c.y + bn * c.x);
+    }
+  }
+  // v: 64 tokens x 128 dims through LDS, out as 128 rows of 64 consecutive keys
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, tok = c >> 4, d8 = (c & 15) * 8;
+    const int64_t t = t0 + tok;
+    u32x4 v = u32x4{0, 0, 0, 0};
+    if (t < n) v = *(const u32x4*)(qkv + t * (3 * 4096) + 2 * 4096 + h * 128 + d8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      *(uint32_t*)&tile[tok][d8 + 2 * e] = v[e];
+    }
+  }
+  __syncthreads();
+  const int tok = tid & 63;
+  const int64_t t = t0 + tok;
+  if (t < n) {
+    for (int d = tid >> 6; d < 128; d += 4) vt[((int64_t)h * 128 + d) * lcap + row0 + t] = tile[tok][d];
+  }
+}
+
+hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk, const float* cs,
+                    uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap) {
+  if (n == 0) return hipSuccess;
+  // q is scaled by 1/sqrt(128) * log2(e): the attention's scores are then in log2 units
+  const float qscale = 0.08838834764831845f * 1.4426950408889634f;
+  hipLaunchKernelGGL(k_qkv_prep, dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, n, wq, wk, cs, qscale, q, k, vt,
+                     row0, lcap);
+  return hipGetLastError();
+}
+
+// latent [64][nimg] fp32 -> rows [nimg][64] fp32
+__global__ void k_latent_rows(const float* __restrict__ lat, int64_t nimg, float* __restrict__ rows) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nimg * 64) return;
+  const int64_t tok = i / 64, c = i % 64;
+  rows[i] = lat[c * nimg + tok];
+}
+
+// rows [nimg][64] fp32 -> latent [64][nimg] fp32
+__global__ void k_rows_latent(const float* __restrict__ rows, int64_t nimg, float* __restrict__ lat) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nimg * 64) return;
+  const int64_t c = i / nimg, tok = i % nimg;
+  lat[i] = rows[tok * 64 + c];
+}
+
+hipError_t latent_rows(hipStream_t s, const float* latent, int64_t nimg, float* rows) {
+  hipLaunchKernelGGL(k_latent_rows, dim3(grid_of(nimg * 64, 256)), dim3(256), 0, s, latent, nimg, rows);
+  return hipGetLastError();
+}
+
+hipError_t rows_to_latent(hipStream_t s, const float* rows, int64_t nimg, float* latent) {
+  hipLaunchKernelGGL(k_rows_latent, dim3(grid_of(nimg * 64, 256)), dim3(256), 0, s, rows, nimg, latent);
+  return hipGetLastError();
+}
+
+__global__ void k_euler(int64_t count, float* __restrict__ z, const float* __restrict__ v, float ds) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) z[i] = z[i] + ds * v[i];   // a product, then a sum: no fused multiply-add
+}
+
+hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float ds) {
+  if (count == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_euler, dim3(grid_of(count, 256)), dim3(256), 0, s, count, z, v, ds);
+  return hipGetLastError();
+}
+
+}  // namespace exn

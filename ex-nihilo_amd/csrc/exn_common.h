@@ -1,0 +1,141 @@
+// exn_common.h -- shared definitions of libexn-hip.so's kernels and host code.
+// gfx950 (CDNA4) only: 64-wide wavefronts, bf16 MFMA, 160 KB LDS per CU.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+namespace exn {
+
+// --- device helpers ------------------------------------------------------------
+
+// two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// two floats -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32)
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  f16x2 v = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float f16_lo(uint32_t u) {
+  return (float)__builtin_bit_cast(f16x2, u)[0];
+}
+__device__ __forceinline__ float f16_hi(uint32_t u) {
+  return (float)__builtin_bit_cast(f16x2, u)[1];
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+
+// fp16 bits -> fp32, exact (subnormals included), without relying on the f16 denormal mode
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  if (e == 0) {
+    const float v = (float)m * 5.9604644775390625e-08f;   // m * 2^-24
+    return sign ? -v : v;
+  }
+  if (e == 31) return __uint_as_float(sign | 0x7F800000u | (m << 13));
+  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// ROCm device-library tanh and exp (ocml)
+__device__ __forceinline__ float tanh_f(float x) { return tanhf(x); }
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+__device__ __forceinline__ float gelu_tanh_f(float v) {
+  return 0.5f * v * (1.f + tanh_f(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+}
+
+// --- host-side status ------------------------------------------------------------
+
+void set_error(const char* fmt, ...);
+
+}  // namespace exn
+
+// The DiT's fixed dimensions (src/weights.lisp:19-20): width, heads x head dim, FFN.
+#define EXN_W 4096
+#define EXN_H 32
+#define EXN_HD 128
+#define EXN_F 12288
+#define EXN_LAT 64
+#define EXN_FREQ 256
+
+// --- kernel launchers (defined in the .hip files, called by api.hip) -----------
+
+namespace exn {
+
+enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_GATE_ADD = 2, EPI_SWIGLU = 3, EPI_GELU_BF16 = 4, EPI_F16 = 5 };
+
+struct EpiArgs {
+  void* y;             // EPI_F32 / EPI_BF16 / EPI_GELU_BF16: output rows (ldy elements apart); EPI_SWIGLU: bf16 out (N/2 wide)
+  int64_t ldy;         // output row stride in elements
+  float* resid;        // EPI_GATE_ADD: the fp32 residual rows, ldy apart
+  const float* gate;   // EPI_GATE_ADD: gate rows (row 0, row 1 = gate + mstride)
+  int n0, p, mstride;  // EPI_GATE_ADD: the sequence row of output row 0, the prefix length, the modulation row stride
+};
+
+// Y = X W^T with X bf16 (M x K, lda), W Q8_0 SoA (qs N x K int8, d N x K/32 fp16) or bf16 (N x K)
+hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d,
+                   int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
+hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w,
+                      int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
+// the edge products: Y = X W^T all fp32 on the SIMD lanes (K % 32 == 0); optional GELU-tanh on Y
+hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
+                    const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int gelu);
+// small M (<= 4): Y = X W^T, X fp32, fp32 sums; optional SiLU on the output
+hipError_t gemv_q8(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
+                   const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int silu);
+
+hipError_t synth_q8(hipStream_t s, uint64_t key, int64_t rows, int64_t cols, int64_t row_stride_blocks,
+                    const int32_t* row_map, int8_t* qs, uint16_t* d);
+hipError_t synth_normal(hipStream_t s, uint64_t key, int64_t n, float base, float scale, int add_base, float* out);
+hipError_t dequant_q8(hipStream_t s, const int8_t* qs, const uint16_t* d, int64_t n, float* f32, uint16_t* bf16);
+hipError_t repack_q8_blocks(hipStream_t s, const uint8_t* blocks, int64_t nblocks_row, int64_t rows,
+                            const int32_t* row_map, int8_t* qs, uint16_t* d);
+hipError_t f32_to_bf16(hipStream_t s, const float* x, uint16_t* y, int64_t n);
+
+hipError_t ln_mod(hipStream_t s, int n, int n0, int p, int mstride, const float* x, int64_t ldx,
+                  const float* mod, void* out, int out_bf16);
+hipError_t rms_norm(hipStream_t s, int n, int width, float eps, const float* x, const float* w, void* out, int out_bf16);
+hipError_t gate_add(hipStream_t s, int64_t count, int width, int n0, int p, int mstride, float* x, const float* h,
+                    const float* gate);
+hipError_t swiglu(hipStream_t s, int64_t n, int f, const uint16_t* gu, uint16_t* out);
+hipError_t gelu_tanh(hipStream_t s, int64_t count, float* x);
+hipError_t silu(hipStream_t s, int64_t count, float* x);
+hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk,
+                    const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap);
+hipError_t latent_rows(hipStream_t s, const float* latent, int64_t nimg, float* rows);
+hipError_t rows_to_latent(hipStream_t s, const float* rows, int64_t nimg, float* latent);
+hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float ds);
+hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out,
+                  int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale);
+
+}  // namespace exn

@@ -1,0 +1,377 @@
+// gemm.hip -- Y = X W^T for the DiT's weight products on gfx950's bf16 MFMA.
+//
+// X: bf16 rows (M x K, lda apart).  W: Q8_0 as SoA -- qs (N x K int8, a row's
+// K/32 blocks of 32 contiguous) and d (N x K/32 fp16) -- or plain bf16 (N x K).
+// The Q8_0 tile is dequantised on its way into LDS: each thread takes one
+// 32-value block, converts fp32(d) * q (exact) to bf16 (round to nearest
+// even) and stores 64 bytes; the MFMAs then read X and W tiles alike.
+// This replaces the reference's mm dispatch (src/cuda-dit.lisp:115-130) and
+// illatio's Q8_0 products behind it; the epilogues fuse the reference's
+// x_gate_add (src/cuda/dit.cu:34-41), x_swiglu2 (:186-192) and x_gelu_tanh
+// (:194-199) into the product's store.
+//
+// Tiles: BM x BN per workgroup, BK = 64 (two Q8_0 blocks) per step, waves
+// of WM x WN, each a grid of 32x32 accumulators (v_mfma_f32_32x32x16_bf16).
+// LDS is double-buffered; the next step's global loads are in registers
+// while the current step's MFMAs run.
+#include "exn_common.h"
+
+namespace exn {
+
+#define BK 64
+#define SA (BK + 8)   // LDS row stride in bf16: 144 bytes, conflict-free 16-byte fragment reads
+
+// MFMA 32x32x16 bf16 operand/accumulator layout (wave64):
+//   A (32 x 16): lane l holds row l%32, k = 8*(l/32) .. +7
+//   B (16 x 32): lane l holds column l%32, k = 8*(l/32) .. +7
+//   D (32 x 32): lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15
+
+template <int BM, int BN, int WM, int WN, bool WBF16, int EPI>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+k_gemm(const uint16_t* __restrict__ X, int64_t lda, const int8_t* __restrict__ QS, const uint16_t* __restrict__ D,
+       const uint16_t* __restrict__ WB, int64_t M, int64_t N, int64_t K, EpiArgs ea) {
+  constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  constexpr int MI = WM / 32, NI = WN / 32;
+  constexpr int A_CH = BM * (BK / 8) / NT;         // 16-byte X chunks per thread
+  constexpr int B_PAIRS = BN * (BK / 32) / NT;     // Q8_0 blocks per thread
+  constexpr int B_CH = BN * (BK / 8) / NT;         // 16-byte bf16 W chunks per thread
+  static_assert(A_CH * NT == BM * (BK / 8), "A tile split");
+  static_assert(WBF16 ? (B_CH * NT == BN * (BK / 8)) : (B_PAIRS * NT == BN * (BK / 32)), "B tile split");
+
+  extern __shared__ __align__(16) uint16_t lds[];
+  // buffer b: X tile at lds + b*(BM+BN)*SA, W tile right after it
+#define As(b) (lds + (b) * (BM + BN) * SA)
+#define Bs(b) (lds + (b) * (BM + BN) * SA + BM * SA)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / (BN / WN), wn = wave % (BN / WN);
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  const int64_t kb = K / 32;
+
+  u32x4 ra[A_CH];
+  u32x4 rq[WBF16 ? B_CH : 2 * B_PAIRS];
+  uint16_t rd[WBF16 ? 1 : B_PAIRS];
+
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int c = tid + i * NT, row = c >> 3, c8 = c & 7;
+      const int64_t m = min(m0 + row, M - 1);
+      ra[i] = *(const u32x4*)(X + m * lda + k0 + c8 * 8);
+    }
+    if constexpr (WBF16) {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int c = tid + i * NT, row = c >> 3, c8 = c & 7;
+        const int64_t n = min(n0 + row, N - 1);
+        rq[i] = *(const u32x4*)(WB + n * K + k0 + c8 * 8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_PAIRS; ++i) {
+        const int c = tid + i * NT, row = c >> 1, blk = c & 1;
+        const int64_t n = min(n0 + row, N - 1);
+        const u32x4* src = (const u32x4*)(QS + n * K + k0 + 32 * blk);
+        rq[2 * i] = src[0];
+        rq[2 * i + 1] = src[1];
+        rd[i] = D[n * kb + k0 / 32 + blk];
+      }
+    }
+  };
+
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int c = tid + i * NT, row = c >> 3, c8 = c & 7;
+      *(u32x4*)(As(buf) + row * SA + c8 * 8) = ra[i];
+    }
+    if constexpr (WBF16) {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int c = tid + i * NT, row = c >> 3, c8 = c & 7;
+        *(u32x4*)(Bs(buf) + row * SA + c8 * 8) = rq[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_PAIRS; ++i) {
+        const int c = tid + i * NT, row = c >> 1, blk = c & 1;
+        const float dv = f16_to_f32(rd[i]);
+        uint32_t o[16];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          const uint32_t q = rq[2 * i + w / 4][w % 4];
+          const float f0 = (float)(int8_t)(q & 0xFF) * dv, f1 = (float)(int8_t)((q >> 8) & 0xFF) * dv;
+          const float f2 = (float)(int8_t)((q >> 16) & 0xFF) * dv, f3 = (float)(int8_t)(q >> 24) * dv;
+          o[2 * w] = pack_bf16x2(f0, f1);
+          o[2 * w + 1] = pack_bf16x2(f2, f3);
+        }
+        u32x4* dst = (u32x4*)(Bs(buf) + row * SA + 32 * blk);
+        dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+        dst[1] = u32x4{o[4], o[5], o[6], o[7]};
+        dst[2] = u32x4{o[8], o[9], o[10], o[11]};
+        dst[3] = u32x4{o[12], o[13], o[14], o[15]};
+      }
+    }
+  };
+
+  f32x16 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
+
+  const int KT = (int)(K / BK);
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) load((int64_t)(kt + 1) * BK);
+    const uint16_t* a_base = As(buf) + (wm * WM + (lane & 31)) * SA + 8 * (lane >> 5);
+    const uint16_t* b_base = Bs(buf) + (wn * WN + (lane & 31)) * SA + 8 * (lane >> 5);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8 a[MI], b[NI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) a[i] = *(const bf16x8*)(a_base + i * 32 * SA + kk * 16);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) b[j] = *(const bf16x8*)(b_base + j * 32 * SA + kk * 16);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // --- epilogue ---
+  const int64_t wrow = m0 + wm * WM, wcol = n0 + wn * WN;
+  if constexpr (EPI == EPI_SWIGLU) {
+    // accumulator pairs (2jj, 2jj+1) hold matching gate and up columns (rows interleaved by 32 at load)
+    uint16_t* y = (uint16_t*)ea.y;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int jj = 0; jj < NI / 2; ++jj) {
+        const int64_t col = wcol / 2 + jj * 32 + (lane & 31);
+        if (2 * (col - (lane & 31)) >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = wrow + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+          if (m < M) {
+            const float g = acc[i][2 * jj][r], u = acc[i][2 * jj + 1][r];
+            y[m * ea.ldy + col] = (uint16_t)(pack_bf16x2(silu_f(g) * u, 0.f) & 0xFFFF);
+          }
+        }
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int64_t n = wcol + j * 32 + (lane & 31);
+      if (n >= N) continue;
+      float g0 = 0.f, g1 = 0.f;
+      if constexpr (EPI == EPI_GATE_ADD) {
+        g0 = tanh_f(ea.gate[n]);
+        g1 = tanh_f(ea.gate[ea.mstride + n]);
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = wrow + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+          if (m >= M) continue;
+          const float v = acc[i][j][r];
+          if constexpr (EPI == EPI_F32) {
+            ((float*)ea.y)[m * ea.ldy + n] = v;
+          } else if constexpr (EPI == EPI_BF16) {
+            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFF);
+          } else if constexpr (EPI == EPI_F16) {
+            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFF);
+          } else if constexpr (EPI == EPI_GELU_BF16) {
+            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_bf16x2(gelu_tanh_f(v), 0.f) & 0xFFFF);
+          } else if constexpr (EPI == EPI_GATE_ADD) {
+            const float g = (ea.n0 + m < ea.p) ? g1 : g0;
+            float* x = ea.resid + m * ea.ldy + n;
+            *x = *x + g * v;
+          }
+        }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, bool WBF16, int EPI>
+static hipError_t launch(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d,
+                         const uint16_t* wb, int64_t M, int64_t N, int64_t K, const EpiArgs& ea) {
+  constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  const size_t shm = 2 * (size_t)(BM + BN) * SA * sizeof(uint16_t);
+  auto kern = k_gemm<BM, BN, WM, WN, WBF16, EPI>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  hipLaunchKernelGGL(kern, grid, dim3(NT), shm, s, x, lda, qs, d, wb, M, N, K, ea);
+  return hipGetLastError();
+}
+
+template <bool WBF16>
+static hipError_t dispatch(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d,
+                           const uint16_t* wb, int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea) {
+  switch (epi) {
+    case EPI_F32: return launch<128, 128, 64, 64, WBF16, EPI_F32>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_BF16: return launch<128, 128, 64, 64, WBF16, EPI_BF16>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_GATE_ADD: return launch<128, 128, 64, 64, WBF16, EPI_GATE_ADD>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_SWIGLU: return launch<128, 128, 64, 64, WBF16, EPI_SWIGLU>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_GELU_BF16: return launch<128, 128, 64, 64, WBF16, EPI_GELU_BF16>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_F16: return launch<128, 128, 64, 64, WBF16, EPI_F16>(s, x, lda, qs, d, wb, M, N, K, ea);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d, int64_t M,
+                   int64_t N, int64_t K, Epi epi, const EpiArgs& ea) {
+  return dispatch<false>(s, x, lda, qs, d, nullptr, M, N, K, epi, ea);
+}
+
+hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
+                      int64_t K, Epi epi, const EpiArgs& ea) {
+  return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
+}
+
+// --- the edge products in fp32 -------------------------------------------------------
+// img_in, txt_in and proj_out feed the residual stream and the velocity straight,
+// and are 0.01% of a step's FLOPs: they run in fp32 on the SIMD lanes, the Q8_0
+// weights dequantised exactly.  64 x 64 tiles, K 32 (a Q8_0 block) a step, each
+// thread 4 x 4 outputs at a 16-row and 16-column stride.
+__global__ void __launch_bounds__(256)
+k_gemm_f32(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ QS, const uint16_t* __restrict__ D,
+           const uint16_t* __restrict__ WB, int64_t M, int64_t N, int64_t K, float* __restrict__ Y, int64_t ldy,
+           int gelu) {
+  __shared__ float xs[32][64 + 1];
+  __shared__ float ws[32][64 + 1];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+  const int lr = tid >> 2, lk = (tid & 3) * 8;   // loader: row lr of the tile, k lk .. lk+7
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < K; k0 += 32) {
+    {
+      const int64_t m = min(m0 + lr, M - 1);
+      const f32x4* src = (const f32x4*)(X + m * ldx + k0 + lk);
+      const f32x4 a = src[0], b = src[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xs[lk + e][lr] = a[e];
+        xs[lk + 4 + e][lr] = b[e];
+      }
+      const int64_t n = min(n0 + lr, N - 1);
+      if (WB) {
+        const u32x4 w = *(const u32x4*)(WB + n * K + k0 + lk);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ws[lk + 2 * e][lr] = bf16_lo(w[e]);
+          ws[lk + 2 * e + 1][lr] = bf16_hi(w[e]);
+        }
+      } else {
+        const u32x2 q = *(const u32x2*)(QS + n * K + k0 + lk);
+        const float dv = f16_to_f32(D[n * (K / 32) + k0 / 32]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ws[lk + e][lr] = (float)(int8_t)((q[e / 4] >> (8 * (e % 4))) & 0xFF) * dv;
+      }
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int kk = 0; kk < 32; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = xs[kk][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = ws[kk][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + ty + 16 * i;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + tx + 16 * j;
+      if (n < N) Y[m * ldy + n] = gelu ? gelu_tanh_f(acc[i][j]) : acc[i][j];
+    }
+  }
+}
+
+hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
+                    const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int gelu) {
+  if (K % 32 || M <= 0) return M == 0 ? hipSuccess : hipErrorInvalidValue;
+  dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+  hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, M, N, K, y, ldy, gelu);
+  return hipGetLastError();
+}
+
+// --- small M: a wave per output column, fp32 activations and sums ---------------------
+
+__global__ void __launch_bounds__(256)
+k_gemv(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ QS, const uint16_t* __restrict__ D,
+       const uint16_t* __restrict__ WB, int M, int64_t N, int64_t K, float* __restrict__ Y, int64_t ldy, int silu) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t c = lane; c < K / 16; c += 64) {
+    const int64_t k = 16 * c;
+    float w[16];
+    if (WB) {
+      const u32x4* src = (const u32x4*)(WB + n * K + k);
+      const u32x4 a = src[0], b = src[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[2 * e] = bf16_lo(a[e]); w[2 * e + 1] = bf16_hi(a[e]);
+        w[8 + 2 * e] = bf16_lo(b[e]); w[8 + 2 * e + 1] = bf16_hi(b[e]);
+      }
+    } else {
+      const u32x4 q = *(const u32x4*)(QS + n * K + k);
+      const float dv = f16_to_f32(D[n * (K / 32) + k / 32]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) w[e] = (float)(int8_t)((q[e / 4] >> (8 * (e % 4))) & 0xFF) * dv;
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if (m < M) {
+        const f32x4* xs = (const f32x4*)(X + m * ldx + k);
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const f32x4 xv = xs[e4];
+          acc[m] = fmaf(w[4 * e4], xv[0], acc[m]);
+          acc[m] = fmaf(w[4 * e4 + 1], xv[1], acc[m]);
+          acc[m] = fmaf(w[4 * e4 + 2], xv[2], acc[m]);
+          acc[m] = fmaf(w[4 * e4 + 3], xv[3], acc[m]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if (m < M) {
+      const float v = wave_sum(acc[m]);
+      if (lane == 0) Y[m * ldy + n] = silu ? silu_f(v) : v;
+    }
+  }
+}
+
+hipError_t gemv_q8(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
+                   const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int silu) {
+  if (M > 4 || K % 16) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gemv, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s, x, ldx, qs, d, wbf16, (int)M, N, K, y, ldy,
+                     silu);
+  return hipGetLastError();
+}
+
+}  // namespace exn

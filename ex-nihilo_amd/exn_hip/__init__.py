@@ -1,0 +1,352 @@
+"""exn_hip -- the host side of libexn-hip.so in Python: a ctypes binding of
+include/exn_hip.h and the reference's DiT backend trio on top of it.
+
+The reference's host is Common Lisp (src/cuda-dit.lisp); its trio is
+
+    (upload-dit path &key device)                                  src/cuda-dit.lisp:52
+    (dit-velocity d context p latent h w sigma &key prefix-key ref) src/cuda-dit.lisp:137
+    (dit-release d)                                                 src/cuda-dit.lisp:99
+
+and generate's Euler loop (src/generate.lisp:112-137) calls it.  This module
+mirrors those names, argument meanings and error behaviour (a failed call
+raises ExnError carrying the library's message, as the reference signals a
+Lisp error) for hosts that are not SBCL -- the tests and the benchmark.  The
+SBCL binding is lisp/hip-dit.lisp.  There is no CPU fallback: without the
+built library or a GPU every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_uint16, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(HERE), "libexn-hip.so")
+
+OK, ENODEV, EINVAL, ENOMEM, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
+Q8_0, F32, BF16 = 8, 0, 30
+DT_F32, DT_BF16 = 0, 1
+WIDTH, HEADS, HEAD_DIM, FFN, LATENT = 4096, 32, 128, 12288, 64
+# Qwen-Image-2.1-Turbo's schedule (src/generate.lisp:7-9)
+TURBO_SIGMAS = (1.0, 0.978453, 0.95418, 0.926626, 0.89508, 0.845148, 0.704534, 0.414568, 0.0)
+
+
+class ExnError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("exn error %d: %s" % (code, msg))
+        self.code = code
+
+
+_lib = None
+vp = c_void_p
+
+# name -> (restype, argtypes); every function of include/exn_hip.h
+SIGNATURES = {
+    "exn_last_error": (c_char_p, []),
+    "exn_version": (c_int, []),
+    "exn_device_count": (c_int, [POINTER(c_int)]),
+    "exn_open": (c_int, [c_int, POINTER(vp)]),
+    "exn_close": (c_int, [vp]),
+    "exn_set_stream": (c_int, [vp, vp]),
+    "exn_sync": (c_int, [vp]),
+    "exn_alloc": (c_int, [vp, c_size_t, POINTER(vp)]),
+    "exn_free": (c_int, [vp, vp]),
+    "exn_upload": (c_int, [vp, vp, vp, c_size_t]),
+    "exn_download": (c_int, [vp, vp, vp, c_size_t]),
+    "exn_copy": (c_int, [vp, vp, vp, c_size_t]),
+    "exn_weight_q8_0": (c_int, [vp, vp, c_int64, c_int64, POINTER(vp)]),
+    "exn_weight_f32": (c_int, [vp, vp, c_int64, c_int64, POINTER(vp)]),
+    "exn_weight_bf16": (c_int, [vp, vp, c_int64, c_int64, POINTER(vp)]),
+    "exn_weight_q8_0_synth": (c_int, [vp, c_uint64, c_uint64, c_int64, c_int64, POINTER(vp)]),
+    "exn_weight_info": (c_int, [vp, POINTER(c_int64), POINTER(c_int64), POINTER(c_int)]),
+    "exn_weight_free": (c_int, [vp]),
+    "exn_dequant": (c_int, [vp, vp, vp, vp]),
+    "exn_mm": (c_int, [vp, vp, vp, c_int, vp, c_int, c_int64]),
+    "exn_mm_gate_add": (c_int, [vp, vp, vp, c_int64, vp, c_int, c_int, c_int, vp]),
+    "exn_mm_swiglu": (c_int, [vp, vp, vp, vp, c_int64]),
+    "exn_weight_pairs": (c_int, [vp, vp]),
+    "exn_ln_mod": (c_int, [vp, c_int, c_int, c_int, c_int, vp, c_int64, vp, vp, c_int]),
+    "exn_rms": (c_int, [vp, c_int, c_int, c_float, vp, vp, vp, c_int]),
+    "exn_gate_add": (c_int, [vp, c_int64, c_int, c_int, c_int, c_int, vp, vp, vp]),
+    "exn_swiglu": (c_int, [vp, c_int64, c_int, vp, vp]),
+    "exn_gelu_tanh": (c_int, [vp, c_int64, vp]),
+    "exn_silu": (c_int, [vp, c_int64, vp]),
+    "exn_qkv_prep": (c_int, [vp, vp, c_int64, vp, vp, vp, vp, vp, vp, c_int64, c_int64]),
+    "exn_attend": (c_int, [vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int64, c_int, c_int, c_float]),
+    "exn_euler": (c_int, [vp, c_int64, vp, vp, c_float]),
+    "exn_dit_create": (c_int, [vp, c_int, POINTER(vp)]),
+    "exn_dit_set": (c_int, [vp, c_char_p, c_int, vp, c_int64, c_int64]),
+    "exn_dit_synth": (c_int, [vp, c_uint64]),
+    "exn_dit_check": (c_int, [vp]),
+    "exn_dit_velocity": (c_int, [vp, vp, c_int, vp, c_int, c_int, c_double, c_uint64, c_int, vp, c_int, c_int, vp]),
+    "exn_dit_velocity_dev": (c_int, [vp, vp, c_int, vp, c_int, c_int, c_double, c_uint64, c_int, vp, c_int, c_int,
+                                     vp]),
+    "exn_dit_generate_dev": (c_int, [vp, vp, c_int, vp, c_int, c_int, vp, c_int, c_int, vp, c_int, c_int]),
+    "exn_dit_trace": (c_int, [vp, vp, c_int64]),
+    "exn_dit_profile": (c_int, [vp, c_int]),
+    "exn_dit_profile_read": (c_int, [vp, c_int, POINTER(c_double), POINTER(c_int64), POINTER(c_double),
+                                     POINTER(c_double)]),
+    "exn_dit_release": (c_int, [vp]),
+    "exn_dit_destroy": (c_int, [vp]),
+    "exn_dit_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
+}
+
+
+def lib():
+    """libexn-hip.so, loaded once.  Raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ExnError(ENODEV, "%s is not built (make -C ex-nihilo_amd)" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def check(code):
+    if code != OK:
+        raise ExnError(code, lib().exn_last_error().decode(errors="replace"))
+    return code
+
+
+def call(name, *args):
+    return check(getattr(lib(), name)(*args))
+
+
+def ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(vp)
+
+
+# --- context and device buffers -------------------------------------------------------
+
+class Context:
+    """A device and its stream (exn_open)."""
+
+    def __init__(self, device: int = 0):
+        h = vp()
+        call("exn_open", device, ctypes.byref(h))
+        self.h = h
+        self.device = device
+
+    def sync(self):
+        call("exn_sync", self.h)
+
+    def close(self):
+        if self.h:
+            call("exn_close", self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
+class DevBuf:
+    """Device memory of a numpy dtype and shape (exn_alloc), freed on close/GC."""
+
+    def __init__(self, ctx: Context, shape, dtype):
+        self.ctx, self.shape, self.dtype = ctx, tuple(np.atleast_1d(shape)), np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        h = vp()
+        call("exn_alloc", ctx.h, max(self.nbytes, 1), ctypes.byref(h))
+        self.h = h
+
+    @classmethod
+    def of(cls, ctx, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        b = cls(ctx, a.shape, a.dtype)
+        b.upload(a)
+        return b
+
+    @property
+    def ptr(self):
+        return self.h.value
+
+    def at(self, byte_offset: int):
+        return vp(self.h.value + byte_offset)
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.nbytes, self.nbytes)
+        call("exn_upload", self.ctx.h, self.h, ptr(a), a.nbytes)
+
+    def get(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        call("exn_download", self.ctx.h, ptr(out), self.h, self.nbytes)
+        return out
+
+    def free(self):
+        if getattr(self, "h", None) and self.ctx.h:
+            call("exn_free", self.ctx.h, self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    """A matrix on the device (exn_weight_*): ROWS outputs of COLS inputs."""
+
+    def __init__(self, ctx, handle, rows, cols):
+        self.ctx, self.h, self.rows, self.cols = ctx, handle, rows, cols
+
+    @classmethod
+    def q8_0(cls, ctx, blocks: np.ndarray, rows: int, cols: int):
+        h = vp()
+        call("exn_weight_q8_0", ctx.h, ptr(np.ascontiguousarray(blocks, dtype=np.uint8)), rows, cols, ctypes.byref(h))
+        return cls(ctx, h, rows, cols)
+
+    @classmethod
+    def f32(cls, ctx, m: np.ndarray):
+        m = np.ascontiguousarray(m, dtype=np.float32)
+        h = vp()
+        call("exn_weight_f32", ctx.h, ptr(m), m.shape[0], m.shape[1], ctypes.byref(h))
+        return cls(ctx, h, m.shape[0], m.shape[1])
+
+    @classmethod
+    def synth(cls, ctx, seed: int, tensor: int, rows: int, cols: int):
+        h = vp()
+        call("exn_weight_q8_0_synth", ctx.h, seed, tensor, rows, cols, ctypes.byref(h))
+        return cls(ctx, h, rows, cols)
+
+    def pairs(self):
+        call("exn_weight_pairs", self.ctx.h, self.h)
+        return self
+
+    def free(self):
+        if getattr(self, "h", None):
+            call("exn_weight_free", self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# --- the backend trio (src/cuda-dit.lisp) -------------------------------------------------
+
+DIT_PREFIX = "model.diffusion_model."
+
+
+class Dit:
+    """The DiT on the device: weights, scratch and the kept prompt K/V (gdit)."""
+
+    def __init__(self, ctx: Context, layers: int = 32):
+        h = vp()
+        call("exn_dit_create", ctx.h, layers, ctypes.byref(h))
+        self.ctx, self.h, self.layers = ctx, h, layers
+        self._keys = {}
+
+    def set(self, name: str, kind: int, data: np.ndarray, dims):
+        """One tensor by its GGUF name (with or without the model prefix) and ggml dims."""
+        if name.startswith(DIT_PREFIX):
+            name = name[len(DIT_PREFIX):]
+        d0 = dims[0]
+        d1 = dims[1] if len(dims) > 1 else 1
+        call("exn_dit_set", self.h, name.encode(), kind, ptr(np.ascontiguousarray(data)), d0, d1)
+
+    def synth(self, seed: int):
+        call("exn_dit_synth", self.h, seed)
+
+    def check(self):
+        call("exn_dit_check", self.h)
+
+    def prefix_key(self, key) -> int:
+        """A 64-bit key for a Lisp-style prefix key (EQUAL objects -> one key)."""
+        if key is None:
+            return 0
+        if key not in self._keys:
+            self._keys[key] = len(self._keys) + 1
+        return self._keys[key]
+
+    def memory(self):
+        w, s = c_int64(), c_int64()
+        call("exn_dit_memory", self.h, ctypes.byref(w), ctypes.byref(s))
+        return w.value, s.value
+
+    PROFILE_CLASSES = ("qkv", "attend", "out", "gate_up", "down", "ln_mod", "qkv_prep", "edge")
+
+    def profile(self, on: bool):
+        call("exn_dit_profile", self.h, 1 if on else 0)
+
+    def profile_read(self):
+        """{class: (ms, launches, flops, bytes)} over the recorded launches."""
+        out = {}
+        for i, name in enumerate(self.PROFILE_CLASSES):
+            ms, n, f, b = c_double(), c_int64(), c_double(), c_double()
+            call("exn_dit_profile_read", self.h, i, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(f), ctypes.byref(b))
+            out[name] = (ms.value, n.value, f.value, b.value)
+        return out
+
+    def release(self):
+        call("exn_dit_release", self.h)
+
+    def destroy(self):
+        if self.h:
+            call("exn_dit_destroy", self.h)
+            self.h = None
+
+
+def upload_dit(tensors=None, *, device: int = 0, layers: int = 32, seed: int | None = None, ctx=None) -> Dit:
+    """upload-dit (src/cuda-dit.lisp:52-86).  TENSORS: an iterable of
+    (name, kind, data, ggml dims) as read from the GGUF (block_q8_0 bytes for
+    Q8_0); or SEED: the synthetic weights made on the device.  The model is
+    checked against dit-expected (src/weights.lisp:47-61) before return."""
+    ctx = ctx or Context(device)
+    d = Dit(ctx, layers)
+    if seed is not None:
+        d.synth(seed)
+    for name, kind, data, dims in tensors or ():
+        d.set(name, kind, data, dims)
+    d.check()
+    return d
+
+
+def dit_velocity(d: Dit, context: np.ndarray, p: int, latent: np.ndarray, h: int, w: int, sigma: float,
+                 prefix_key=None, ref=None) -> np.ndarray:
+    """dit-velocity (src/cuda-dit.lisp:137-144): CONTEXT (P x 4096 fp32),
+    LATENT (64 x H x W fp32, channel-major) -> the velocity, same shape.
+    REF = (a, ref_latent, rh, rw): an edit's reference picture."""
+    ctxa = np.ascontiguousarray(context, dtype=np.float32).reshape(-1)
+    lat = np.ascontiguousarray(latent, dtype=np.float32).reshape(-1)
+    if lat.size != 64 * h * w:
+        raise ExnError(EINVAL, "latent of %d floats for %d x %d" % (lat.size, h, w))
+    v = np.empty((64, h, w), np.float32)
+    if ref is not None:
+        a, rl, rh, rw = ref
+        rl = np.ascontiguousarray(rl, dtype=np.float32).reshape(-1)
+        refargs = (a, ptr(rl), rh, rw)
+    else:
+        refargs = (0, None, 0, 0)
+    call("exn_dit_velocity", d.h, ptr(ctxa) if p > 0 else None, p, ptr(lat), h, w, float(sigma),
+         d.prefix_key(prefix_key), *refargs, ptr(v))
+    return v
+
+
+def dit_release(d: Dit):
+    """dit-release (src/cuda-dit.lisp:99-108)."""
+    d.release()
+
+
+def generate_latent(d: Dit, context: np.ndarray, p: int, z: np.ndarray, h: int, w: int,
+                    sigmas=TURBO_SIGMAS, prefix_key="prompt", ref=None) -> np.ndarray:
+    """generate's Euler loop (src/generate.lisp:133-135) on host arrays:
+    z <- z + (s' - s) v, (s' - s) rounded to a single float."""
+    z = np.array(z, dtype=np.float32, copy=True)
+    for s, s2 in zip(sigmas[:-1], sigmas[1:]):
+        v = dit_velocity(d, context, p, z, h, w, s, prefix_key=prefix_key, ref=ref)
+        z = z + np.float32(s2 - s) * v
+    return z

@@ -1,0 +1,199 @@
+/* exn_hip.h -- the C ABI of libexn-hip.so: ex-nihilo's DiT denoising step on
+ * one MI355X (gfx950), hand-written HIP kernels behind plain C entry points.
+ *
+ * It replaces the CUDA layer under the reference's DiT backend trio
+ * (upload-dit / dit-velocity / dit-release, src/cuda-dit.lisp:52,137,99):
+ * illatio's device, memory and launch calls (il::open-cuda, il::cuda-alloc,
+ * il::cuda-upload, il::cuda-download, il::cuda-copy-dd, il::launch) and the
+ * kernels they launch (src/cuda/dit.cu; illatio's repack_q8, quant_q8,
+ * MM_Q8_MMA2, d4_mm_q8_0, g53_mm_bf16, d41_mm_f32, v_rms).  A host binds it
+ * with any C FFI (sb-alien in lisp/hip-dit.lisp, ctypes in exn_hip).
+ *
+ * Conventions:
+ *   - Every call returns an int status, EXN_OK (0) or an EXN_E* code; the
+ *     message of the calling thread's last failure is exn_last_error().
+ *     No call aborts the process.
+ *   - Matrices follow ggml's order (src/weights.lisp:23-24): ROWS outputs of
+ *     COLS inputs, each row contiguous along COLS; Y = X W^T.
+ *   - Device pointers are plain addresses (void*); a byte offset into a
+ *     buffer, the reference's (cons buf off), is the pointer plus the offset.
+ *   - Work is ordered on the context's stream; exn_download and the
+ *     host-pointer velocity call synchronise, everything else is
+ *     asynchronous.  One thread at a time per context (the reference
+ *     serialises callers with *gpu-lock*, src/server.lisp:24-28).
+ */
+#ifndef EXN_HIP_H
+#define EXN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXN_OK 0
+#define EXN_ENODEV 1  /* no GPU, or no device of that index */
+#define EXN_EINVAL 2  /* bad argument: size, shape, name, null pointer */
+#define EXN_ENOMEM 3  /* device allocation failed */
+#define EXN_EHIP 4    /* a HIP runtime call failed */
+#define EXN_ESTATE 5  /* out of order: a tensor missing, a model released */
+
+/* weight kinds (the GGUF tensor types the reference accepts, src/cuda-dit.lisp:65-81) */
+#define EXN_Q8_0 8
+#define EXN_F32 0
+#define EXN_BF16 30
+
+/* activation dtypes of the op-level entry points */
+#define EXN_DT_F32 0
+#define EXN_DT_BF16 1
+#define EXN_DT_F16 2 /* outputs of exn_mm only */
+
+typedef struct exn_ctx exn_ctx; /* a device and its stream (il::open-cuda / exn-device, src/cuda-dit.lisp:25-40) */
+typedef struct exn_w exn_w;     /* a weight matrix on the device (the gdit-w entries, src/cuda-dit.lisp:46) */
+typedef struct exn_dit exn_dit; /* a DiT: weights, scratch, kept prompt K/V (the gdit struct, src/cuda-dit.lisp:44-50) */
+
+/* --- status and context ------------------------------------------------------------ */
+
+const char* exn_last_error(void);
+int exn_version(void);
+int exn_device_count(int* n);
+/* il::open-cuda + exn-device (src/cuda-dit.lisp:25-40): EXN_ENODEV cleanly when there is no GPU */
+int exn_open(int device, exn_ctx** out);
+int exn_close(exn_ctx* ctx);
+/* order the context's work on STREAM (a hipStream_t); NULL restores the context's own */
+int exn_set_stream(exn_ctx* ctx, void* stream);
+int exn_sync(exn_ctx* ctx); /* il::cuda-sync */
+
+/* --- device memory: il::cuda-alloc / cuda-free / cuda-upload / cuda-download / cuda-copy-dd ------------ */
+
+int exn_alloc(exn_ctx* ctx, size_t bytes, void** dptr);
+int exn_free(exn_ctx* ctx, void* dptr);
+int exn_upload(exn_ctx* ctx, void* dst, const void* src, size_t bytes);
+int exn_download(exn_ctx* ctx, void* dst, const void* src, size_t bytes); /* synchronous */
+int exn_copy(exn_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* --- weights (upload-dit's per-tensor branch, src/cuda-dit.lisp:59-81) ------------------------------ */
+
+/* ROWS x COLS Q8_0 from GGUF block_q8_0 records in host memory (34 bytes a block:
+ * fp16 d, 32 int8 q), e.g. the mmapped file itself; repacked on the device as
+ * repack_q8 does (src/cuda-dit.lisp:71-76).  COLS % 32 == 0. */
+int exn_weight_q8_0(exn_ctx* ctx, const void* blocks, int64_t rows, int64_t cols, exn_w** out);
+/* a non-Q8_0 matrix (src/cuda-dit.lisp:77-80): fp32 or bf16 rows, kept as bf16 */
+int exn_weight_f32(exn_ctx* ctx, const float* data, int64_t rows, int64_t cols, exn_w** out);
+int exn_weight_bf16(exn_ctx* ctx, const uint16_t* data, int64_t rows, int64_t cols, exn_w** out);
+/* test hook, no reference counterpart: a synthetic Q8_0 matrix made on the device by the
+ * counter-based generator (seed, tensor id) that the host oracle restates bit for bit */
+int exn_weight_q8_0_synth(exn_ctx* ctx, uint64_t seed, uint64_t tensor, int64_t rows, int64_t cols, exn_w** out);
+int exn_weight_info(const exn_w* w, int64_t* rows, int64_t* cols, int* kind);
+int exn_weight_free(exn_w* w);
+/* test hook: W dequantised, fp32(d) * q into F32 and its bf16 rounding into BF16 (either may be NULL) */
+int exn_dequant(exn_ctx* ctx, const exn_w* w, float* f32, uint16_t* bf16);
+
+/* --- ops: the kernels of src/cuda/dit.cu and illatio's products, on device pointers ------------------ */
+
+/* mm (src/cuda-dit.lisp:115-130): Y (n rows) = X (n rows) W^T.  X is fp32 or bf16
+ * (XDT), Y fp32, bf16 or fp16 (YDT); n <= 4 with fp32 X and Y goes through a GEMV in fp32. */
+int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n);
+/* mm, then x_gate_add fused into the product's store (src/cuda/dit.cu:34-41):
+ * RESID[t] += tanh(GATE[row]) * (X W^T)[t]; sequence row N0 + t < P takes GATE + MSTRIDE */
+int exn_mm_gate_add(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, float* resid, int n0, int p,
+                    int mstride, const float* gate);
+/* mm on a gate_up matrix uploaded with exn_weight_pairs, then x_swiglu2 (src/cuda/dit.cu:186-192)
+ * fused: FF (n x rows/2, bf16) = silu(gate) * up */
+int exn_mm_swiglu(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, uint16_t* ff, int64_t n);
+/* interleave a gate_up matrix's halves by 32 rows in place (gate rows 0..31, up rows
+ * 0..31, gate 32..63, ...) so that exn_mm_swiglu finds each pair in one tile */
+int exn_weight_pairs(exn_ctx* ctx, exn_w* w);
+/* x_ln_mod (src/cuda/dit.cu:17-32): OUT = LayerNorm(X) * (1 + MOD[row]), width 4096,
+ * X rows LDX apart; sequence row N0 + t < P takes MOD + MSTRIDE.  OUT fp32 or bf16. */
+int exn_ln_mod(exn_ctx* ctx, int n, int n0, int p, int mstride, const float* x, int64_t ldx, const float* mod,
+               void* out, int outdt);
+/* v_rms (src/cuda-dit.lisp:176): Y = X / rms(X) * W, eps as given; Y fp32 or bf16 */
+int exn_rms(exn_ctx* ctx, int n, int width, float eps, const float* x, const float* w, void* y, int ydt);
+/* x_gate_add (src/cuda/dit.cu:34-41), fp32: X += tanh(GATE[row]) * H over COUNT values */
+int exn_gate_add(exn_ctx* ctx, int64_t count, int width, int n0, int p, int mstride, float* x, const float* h,
+                 const float* gate);
+/* x_swiglu2 (src/cuda/dit.cu:186-192), bf16: OUT (n x f) = silu(GU[:, :f]) * GU[:, f:] */
+int exn_swiglu(exn_ctx* ctx, int64_t n, int f, const uint16_t* gu, uint16_t* out);
+/* x_gelu_tanh, x_silu (src/cuda/dit.cu:194-206), fp32 in place */
+int exn_gelu_tanh(exn_ctx* ctx, int64_t count, float* x);
+int exn_silu(exn_ctx* ctx, int64_t count, float* x);
+/* x_qk_norm_rope (src/cuda/dit.cu:43-58) for q and k, plus v, from one fused QKV
+ * product: QKV fp16 rows of 3 x 4096 for tokens 0..n-1 = sequence rows ROW0..;
+ * CS 128 floats a sequence row (cos, sin of 64 pairs).  Writes, fp16, Q [32][n][128]
+ * scaled by log2(e)/sqrt(128), K into [32][LCAP][128] rows ROW0.., V transposed
+ * into [32][128][LCAP] columns ROW0.. */
+int exn_qkv_prep(exn_ctx* ctx, const uint16_t* qkv, int64_t n, const float* wq, const float* wk, const float* cs,
+                 uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap);
+/* x_attend_mma (src/cuda/dit.cu:208-336) with xa_lim's mask (:60-66): OUT [n][4096]
+ * bf16 for queries = sequence rows Q0..Q0+n-1 over keys 0..l-1; Q, K, V^T fp16 in the
+ * layouts exn_qkv_prep writes.  SCALE multiplies the scores, which are in log2
+ * units (1 for exn_qkv_prep's Q).  LCAP % 64 == 0, V^T's columns l..LCAP-1 finite. */
+int exn_attend(exn_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out, int n, int q0,
+               int p, int l, int64_t lcap, int b0, int b1, float scale);
+/* the Euler update of generate's loop (src/generate.lisp:133-135): Z += DS * V */
+int exn_euler(exn_ctx* ctx, int64_t count, float* z, const float* v, float ds);
+
+/* --- the model: the backend trio ----------------------------------------------------------------- */
+
+/* an empty DiT of LAYERS blocks (32 in the real model; fewer to look at part of a step, as
+ * *dit-layers* does in src/metal-dit.lisp:112) on CTX */
+int exn_dit_create(exn_ctx* ctx, int layers, exn_dit** out);
+/* one tensor of upload-dit (src/cuda-dit.lisp:59-81), by its name without the
+ * "model.diffusion_model." prefix and its ggml dims D0 (contiguous) x D1 (1 for a vector);
+ * KIND EXN_Q8_0 (block_q8_0 records), EXN_F32 or EXN_BF16.  Dims and names are held
+ * against dit-expected (src/weights.lisp:22-45); txt_in.text_norm.weight is used as 1 + w. */
+int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_t d0, int64_t d1);
+/* test hook: every tensor of the model made on the device by the synthetic generator */
+int exn_dit_synth(exn_dit* d, uint64_t seed);
+/* EXN_OK when every expected tensor is present, else EXN_ESTATE naming each missing one
+ * (open-dit's check, src/weights.lisp:47-61) */
+int exn_dit_check(exn_dit* d);
+/* dit-velocity (src/cuda-dit.lisp:137-243): CONTEXT (P x 4096 fp32, the encoder's states),
+ * LATENT (64 x H x W fp32, channel-major) -> V (64 x H x W), host memory, synchronous.
+ * SIGMA is a double, as the reference's schedule (src/generate.lisp:7-9); t = 1000 sigma.
+ * PREFIX_KEY != 0 keeps the prompt's K/V after the first call and reuses them while the
+ * key and prefix length stay.  REF_LATENT != NULL: an edit's reference picture (64 x RH x
+ * RW) put in the prefix after the first REF_A text rows (P counts the text only). */
+int exn_dit_velocity(exn_dit* d, const float* context, int p, const float* latent, int h, int w, double sigma,
+                     uint64_t prefix_key, int ref_a, const float* ref_latent, int rh, int rw, float* v);
+/* the same on device pointers, asynchronous on the context's stream */
+int exn_dit_velocity_dev(exn_dit* d, const float* context, int p, const float* latent, int h, int w, double sigma,
+                         uint64_t prefix_key, int ref_a, const float* ref_latent, int rh, int rw, float* v);
+/* generate's loop (src/generate.lisp:133-135) on the device: Z (device, 64 x H x W) through
+ * the NSIG - 1 Euler steps of SIGMAS, the prompt's K/V kept under PREFIX_KEY (0: a fresh key) */
+int exn_dit_generate_dev(exn_dit* d, const float* context, int p, float* z, int h, int w, const double* sigmas,
+                         int nsig, int ref_a, const float* ref_latent, int rh, int rw);
+/* *dit-trace* (src/metal-dit.lisp:114-124), as a copy: while BUF (device, fp32) is set,
+ * each velocity pass copies the residual stream's n rows before the first block to
+ * BUF and after block i to BUF + (i + 1) * n * 4096, as far as CAP floats reach;
+ * NULL turns it off */
+int exn_dit_trace(exn_dit* d, float* buf, int64_t cap);
+/* EXN_PROFILE's per-kernel GPU time (src/tenant.lisp:53-62), on the context's stream:
+ * exn_dit_profile(d, 1) clears and starts recording a HIP event pair around every
+ * launch of the step, by kernel class; (d, 0) stops.  exn_dit_profile_read gives a
+ * class's summed milliseconds, launches, and algorithmic FLOPs and HBM bytes (one
+ * read of each input, one write of each output) over the recorded launches. */
+#define EXN_PROF_QKV 0      /* LayerNormed rows x to_q|to_k|to_v, Q8_0 */
+#define EXN_PROF_ATTEND 1   /* attention */
+#define EXN_PROF_OUT 2      /* attention rows x to_out.0, gated residual fused */
+#define EXN_PROF_GATE_UP 3  /* LayerNormed rows x gate_up, SwiGLU fused */
+#define EXN_PROF_DOWN 4     /* SwiGLU rows x img_mlp.out, gated residual fused */
+#define EXN_PROF_LN_MOD 5   /* LayerNorm x (1 + scale) */
+#define EXN_PROF_QKV_PREP 6 /* QK RMSNorm + RoPE, V transposed */
+#define EXN_PROF_EDGE 7     /* timestep, txt_in, img_in, proj_out and the rest */
+#define EXN_PROF_CLASSES 8
+int exn_dit_profile(exn_dit* d, int on);
+int exn_dit_profile_read(exn_dit* d, int cls, double* ms, int64_t* launches, double* flops, double* bytes);
+/* dit-release (src/cuda-dit.lisp:99-108): scratch and kept prompt K/V freed, weights kept */
+int exn_dit_release(exn_dit* d);
+int exn_dit_destroy(exn_dit* d);
+/* bytes of device memory the model holds: weights, scratch, kept K/V */
+int exn_dit_memory(exn_dit* d, int64_t* weights, int64_t* scratch);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXN_HIP_H */

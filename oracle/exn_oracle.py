@@ -274,14 +274,22 @@ class SynthWeights:
     gates far from zero.  Dequantised matrices are cached per name up to
     `cache_bytes`."""
 
-    def __init__(self, seed: int, shape: Shape = Shape(), cache_bytes: int = 2 << 30, gain: float = 1.0):
+    def __init__(self, seed: int, shape: Shape = Shape(), cache_bytes: int = 2 << 30, gain: float = 1.0,
+                 keep_q8: bool = False):
         self.seed, self.shape, self.gain = seed, shape, np.float32(gain)
         self.dims = dict(dit_expected(shape))
         self.cache, self.cache_bytes = {}, cache_bytes
+        self.keep_q8, self.q8cache = keep_q8, {}
 
     def q8(self, name):
+        """The SoA codes (kept per name when keep_q8: 1.06 bytes a weight, not 4)."""
+        if name in self.q8cache:
+            return self.q8cache[name]
         dims = self.dims[name]
-        return q8_0_synth_fast(self.seed, tensor_id(name), dims[1], dims[0])
+        c = q8_0_synth_fast(self.seed, tensor_id(name), dims[1], dims[0])
+        if self.keep_q8:
+            self.q8cache[name] = c
+        return c
 
     def __call__(self, name):
         dims = self.dims[name]
@@ -410,12 +418,15 @@ def attention(q, k, v, q0, p, b0=0, b1=0, head_chunk=4):
     out = np.empty_like(q)
     for h0 in range(0, heads, head_chunk):
         hs = slice(h0, min(heads, h0 + head_chunk))
-        s = np.einsum("nhd,lhd->hnl", q[:, hs], k[:, hs], optimize=True) * scale
-        s = np.where(mask[None], np.float32(-np.inf), s)
+        qh = np.ascontiguousarray(q[:, hs].transpose(1, 0, 2))          # (h, n, hd)
+        kt = np.ascontiguousarray(k[:, hs].transpose(1, 2, 0))          # (h, hd, l)
+        vh = np.ascontiguousarray(v[:, hs].transpose(1, 0, 2))          # (h, l, hd)
+        s = np.matmul(qh, kt) * scale
+        s = np.where(mask[None], np.asarray(-np.inf, dtype=s.dtype), s)
         s = s - s.max(-1, keepdims=True)
         e = np.exp(s)
         pr = e / e.sum(-1, keepdims=True)
-        out[:, hs] = np.einsum("hnl,lhd->nhd", pr, v[:, hs], optimize=True)
+        out[:, hs] = np.matmul(pr, vh).transpose(1, 0, 2)
     return out
 
 

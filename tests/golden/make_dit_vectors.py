@@ -1,0 +1,54 @@
+"""Writes the oracle's results for the full-depth GPU parity tests, which the
+GPU box cannot afford to recompute inside a test (a 32-block numpy step is
+minutes of CPU).  These are the oracle's outputs (oracle/exn_oracle.py,
+itself pinned against the reference's ref_dit.py vectors), cached:
+
+    python tests/golden/make_dit_vectors.py small      # dit_depth32_small.npz
+    python tests/golden/make_dit_vectors.py cfg2       # dit_cfg2_8step.npz (about half an hour)
+
+small: 32 blocks of the real shape, synthetic Q8_0 weights (seed 1), 32 text
+rows, an 8 x 8 latent: the velocity of each of the 8 Turbo steps (the first
+uncached, the rest on the kept prompt K/V) and the final latent.
+cfg2: the 1024^2 workload -- 4096 image rows, 256 text rows, 32 blocks (seed
+2) -- through the 8 Euler steps: the first step's velocity and the final
+latent, stored as float16 (far below the 2e-2 tolerance).
+"""
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+from oracle import exn_oracle as xo  # noqa: E402
+
+
+def run(seed, p, h, w, out, half=False):
+    sh = xo.Shape()
+    wt = xo.SynthWeights(seed, sh, cache_bytes=0, keep_q8=True)
+    ctx, lat = xo.synth_inputs(seed, p, h, w, sh)
+    vs = []
+    t0 = time.time()
+
+    def on_step(s, v, z):
+        vs.append(v)
+        print("step sigma %.6f: |v| %.4f, %.0fs" % (s, float(np.sqrt((v * v).mean())), time.time() - t0), flush=True)
+
+    z = xo.euler(wt, ctx, lat, sh, on_step=on_step)
+    dt = np.float16 if half else np.float32
+    arrays = {"meta": np.array([seed, p, h, w], np.int64), "z_final": z.astype(dt)}
+    if half:
+        arrays["v_step0"] = vs[0].astype(dt)
+    else:
+        arrays["v_steps"] = np.stack(vs).astype(dt)
+    np.savez_compressed(os.path.join(HERE, out), **arrays)
+    print("wrote", out)
+
+
+if __name__ == "__main__":
+    which = sys.argv[1] if len(sys.argv) > 1 else "small"
+    if which == "small":
+        run(1, 32, 8, 8, "dit_depth32_small.npz")
+    elif which == "cfg2":
+        run(2, 256, 64, 64, "dit_cfg2_8step.npz", half=True)

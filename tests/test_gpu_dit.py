@@ -1,0 +1,183 @@
+"""The DiT step on the GPU through the C ABI's backend trio, against the
+oracle: per block (relative L2 <= 1e-2, on the block's output and on its
+update), per step, the prefix cache, edit mode, and the 8 Euler steps
+(<= 2e-2 on the final latent).  Needs an MI355X."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import exn_hip as X
+from oracle import exn_oracle as xo
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def say(*a):
+    print("[gpu]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = X.Context(0)
+    yield c
+    c.close()
+
+
+def model(ctx, layers, seed):
+    d = X.Dit(ctx, layers)
+    d.synth(seed)
+    d.check()
+    return d
+
+
+def test_missing_and_misshapen_tensors(ctx):
+    say("dit check / set errors")
+    d = X.Dit(ctx, 2)
+    with pytest.raises(X.ExnError) as e:
+        d.check()
+    assert e.value.code == X.ESTATE and "missing img_in.weight" in str(e.value)
+    with pytest.raises(X.ExnError) as e:
+        d.set("transformer_blocks.0.attn.norm_q.weight", X.F32, np.zeros(64, np.float32), (64,))
+    assert e.value.code == X.EINVAL and "not (128 1)" in str(e.value)
+    with pytest.raises(X.ExnError) as e:
+        d.set("transformer_blocks.2.attn.to_q.weight", X.Q8_0, np.zeros(34, np.uint8), (4096, 4096))
+    assert e.value.code == X.EINVAL
+    with pytest.raises(X.ExnError):
+        X.dit_velocity(d, np.zeros((4, 4096), np.float32), 4, np.zeros((64, 2, 2), np.float32), 2, 2, 0.5)
+    d.destroy()
+
+
+def _trace(ctx, d, rows):
+    """The residual stream before the first block (slot 0) and after each block."""
+    buf = X.DevBuf(ctx, (d.layers + 1, rows, 4096), np.float32)
+    X.call("exn_dit_trace", d.h, buf.h, (d.layers + 1) * rows * 4096)
+    return buf
+
+
+def test_one_block_cfg0(ctx):
+    """The single-block workload: 1024 image rows (32 x 32) and 64 text rows,
+    sigma 0.5, reference dims (width 4096, 32 x 128 heads, SwiGLU 12288)."""
+    seed, p, h, w = 0, 64, 32, 32
+    say("one block, p", p, "image", h, "x", w)
+    d = model(ctx, 1, seed)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    tr = _trace(ctx, d, p + h * w)
+    v = X.dit_velocity(d, ctxa, p, lat, h, w, 0.5)
+    t = tr.get()
+    x_in_gpu, x_gpu = t[0], t[1]
+    wt = xo.SynthWeights(seed)
+    dump = {}
+    v_ref = xo.forward(wt, ctxa, lat, 0.5, dump=dump, layers=1)
+    x_in = np.concatenate([dump["txt"], xo.linear(xo.tokens(lat), wt("img_in.weight"))])
+    x_ref = dump["blk"][0]
+    e_in = xo.rel_l2(x_in_gpu, x_in)                        # txt_in and img_in, fp32 on the device
+    e_x, e_v = xo.rel_l2(x_gpu, x_ref), xo.rel_l2(v, v_ref)
+    e_dx = xo.rel_l2(x_gpu - x_in_gpu, x_ref - x_in)        # the block's own update
+    say("rel-L2: block input %.2e, block output %.2e, block update %.2e, velocity %.2e" % (e_in, e_x, e_dx, e_v))
+    assert e_in < 1e-4
+    assert e_x < 1e-2 and e_dx < 1e-2 and e_v < 1e-2
+    d.destroy()
+
+
+def test_prefix_cache(ctx):
+    """A cached pass gives the uncached pass's velocity (src/cuda-dit.lisp:6-9)."""
+    say("prefix cache, 2 blocks")
+    d = model(ctx, 2, 3)
+    ctxa, lat = xo.synth_inputs(3, 20, 4, 6)
+    v0 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9)
+    v1 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9, prefix_key="a")
+    v2 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9, prefix_key="a")          # cached
+    assert xo.rel_l2(v1, v0) < 1e-6 and xo.rel_l2(v2, v0) < 1e-5
+    v3 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.5, prefix_key="a")          # cached, another t
+    v4 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.5)
+    assert xo.rel_l2(v3, v4) < 1e-5
+    # a changed prompt length invalidates the kept K/V
+    v5 = X.dit_velocity(d, ctxa[:17], 17, lat, 4, 6, 0.5, prefix_key="a")
+    v6 = X.dit_velocity(d, ctxa[:17], 17, lat, 4, 6, 0.5)
+    assert xo.rel_l2(v5, v6) < 1e-6 and xo.rel_l2(v5, v4) > 1e-4
+    wt = xo.SynthWeights(3)
+    ref = xo.forward(wt, ctxa, lat, 0.5, layers=2)
+    assert xo.rel_l2(v4, ref) < 1e-2
+    X.dit_release(d)
+    v7 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.5, prefix_key="a")          # released: recomputed
+    assert xo.rel_l2(v7, v4) < 1e-6
+    d.destroy()
+
+
+def test_edit_mode(ctx):
+    """A reference picture in the prefix (src/cuda-dit.lisp:179-192; host.lisp:37-50):
+    3 text rows, a 4 x 5 picture, 9 text rows more, a 4 x 6 image."""
+    say("edit mode, 2 blocks")
+    seed = 4
+    d = model(ctx, 2, seed)
+    ctxa, lat, rl = xo.synth_inputs(seed, 12, 4, 6, ref_hw=(4, 5))
+    v1 = X.dit_velocity(d, ctxa, 12, lat, 4, 6, 0.8, prefix_key="e", ref=(3, rl, 4, 5))
+    v2 = X.dit_velocity(d, ctxa, 12, lat, 4, 6, 0.8, prefix_key="e", ref=(3, rl, 4, 5))
+    assert xo.rel_l2(v2, v1) < 1e-5
+    wt = xo.SynthWeights(seed)
+    ref = xo.forward(wt, ctxa, lat, 0.8, ref=(3, rl), layers=2)
+    e = xo.rel_l2(v1, ref)
+    say("edit velocity rel-L2 %.2e" % e)
+    assert e < 1e-2
+    d.destroy()
+
+
+def test_device_and_host_paths_agree(ctx):
+    """exn_dit_velocity (host arrays) and exn_dit_velocity_dev (device arrays) give
+    the same velocity; generate's Euler loop on the device gives the host loop's
+    latent (z + ds v, two single roundings either way)."""
+    say("host and device paths, 2 blocks")
+    seed, p, h, w = 5, 24, 8, 8
+    d = model(ctx, 2, seed)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    v_host = X.dit_velocity(d, ctxa, p, lat, h, w, 1.0)
+    cd, zd = X.DevBuf.of(ctx, ctxa), X.DevBuf.of(ctx, lat)
+    vd = X.DevBuf(ctx, (64, h, w), np.float32)
+    X.call("exn_dit_velocity_dev", d.h, cd.h, p, zd.h, h, w, 1.0, 0, 0, None, 0, 0, vd.h)
+    e = xo.rel_l2(vd.get(), v_host)
+    say("velocity host vs device rel-L2 %.2e" % e)
+    assert e < 1e-6
+    sig = (1.0, 0.978453, 0.95418)
+    z = lat.copy()
+    for s, s2 in zip(sig[:-1], sig[1:]):
+        v = X.dit_velocity(d, ctxa, p, z, h, w, s, prefix_key="k")
+        z = z + np.float32(s2 - s) * v
+    sg = np.array(sig, np.float64)
+    X.call("exn_dit_generate_dev", d.h, cd.h, p, zd.h, h, w, X.ptr(sg), len(sg), 0, None, 0, 0)
+    e = xo.rel_l2(zd.get(), z)
+    say("two Euler steps, device loop vs host loop rel-L2 %.2e" % e)
+    assert e < 1e-6
+    d.destroy()
+
+
+def test_full_depth_steps_against_oracle(ctx):
+    """32 blocks, 32 text rows, an 8 x 8 latent: each of the 8 Turbo steps'
+    velocity (<= 1e-2) and the final latent after the Euler loop (<= 2e-2),
+    against the oracle's results cached in tests/golden/dit_depth32_small.npz."""
+    g = np.load(os.path.join(GOLDEN, "dit_depth32_small.npz"))
+    seed, p, h, w = (int(v) for v in g["meta"])
+    say("32 blocks, 8 steps, p", p, "image", h, "x", w)
+    d = model(ctx, 32, seed)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    z = lat.copy()
+    sig = xo.TURBO_SIGMAS
+    for i, (s, s2) in enumerate(zip(sig[:-1], sig[1:])):
+        v = X.dit_velocity(d, ctxa, p, z, h, w, s, prefix_key="prompt")
+        e = xo.rel_l2(v, g["v_steps"][i])
+        say("step %d velocity rel-L2 %.2e" % (i, e))
+        assert e < 1e-2
+        z = z + np.float32(s2 - s) * v
+    ez = xo.rel_l2(z, g["z_final"])
+    say("final latent rel-L2 %.2e" % ez)
+    assert ez < 2e-2
+    # the same loop on the device (exn_dit_generate_dev) gives the same latent
+    zd = X.DevBuf.of(ctx, lat)
+    cd = X.DevBuf.of(ctx, ctxa)
+    sg = np.array(sig, np.float64)
+    X.call("exn_dit_generate_dev", d.h, cd.h, p, zd.h, h, w, X.ptr(sg), len(sg), 0, None, 0, 0)
+    assert xo.rel_l2(zd.get(), z) < 1e-5
+    d.destroy()

@@ -1,0 +1,358 @@
+"""The HIP kernels against the oracle, through the C ABI (libexn-hip.so).
+Integer and byte work bit-exact; floating point to the tolerance written in
+each test.  Needs an MI355X."""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import exn_hip as X
+from oracle import exn_oracle as xo
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[gpu]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = X.Context(0)
+    yield c
+    c.close()
+
+
+_KEEP = []
+
+
+@pytest.fixture(autouse=True)
+def _keep_alive():
+    """Device buffers made inline for a call stay alive until the test ends
+    (a temporary's exn_free would otherwise run before the kernel does)."""
+    yield
+    _KEEP.clear()
+
+
+def dev(ctx, a):
+    b = X.DevBuf.of(ctx, np.ascontiguousarray(a))
+    _KEEP.append(b)
+    return b
+
+
+def bf16(a):
+    return xo.bf16_bits(np.asarray(a, np.float32))
+
+
+def from_bf16(b):
+    return xo.bf16_to_f32(b)
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def from_f16(b):
+    return np.asarray(b, np.uint16).view(np.float16).astype(np.float32)
+
+
+# --- Q8_0: generator, repack, dequant (bit-exact) -------------------------------------
+
+def test_synth_q8_bit_exact(ctx):
+    say("synth q8 96x4096 seed 5 tensor 17")
+    w = X.Weight.synth(ctx, 5, 17, 96, 4096)
+    f = X.DevBuf(ctx, (96, 4096), np.float32)
+    b = X.DevBuf(ctx, (96, 4096), np.uint16)
+    X.call("exn_dequant", ctx.h, w.h, f.h, b.h)
+    qs, d = xo.q8_0_synth(5, 17, 96, 4096)
+    want = xo.dequant_q8_0(qs, d)
+    got = f.get()
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    assert (b.get() == xo.bf16_bits(want)).all()
+
+
+def test_repack_dequant_exhaustive(ctx):
+    """Every fp16 scale (subnormals, zero, +-inf, NaN included) times every int8
+    value through GGUF block_q8_0 records: the device's fp32 equals fp32(d) * q
+    bit for bit (NaN where the product is NaN), its bf16 the RNE rounding."""
+    say("repack exhaustive 4096 x 4096")
+    d = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    q = np.arange(-128, 128, dtype=np.int16).astype(np.int8)
+    nb = d.size * 8
+    blocks = np.empty((nb, 34), np.uint8)
+    blocks[:, 0:2] = np.repeat(d, 8).view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:] = np.tile(q.view(np.uint8).reshape(8, 32), (d.size, 1))
+    rows, cols = 4096, 4096
+    w = X.Weight.q8_0(ctx, blocks.reshape(-1), rows, cols)
+    f = X.DevBuf(ctx, (rows, cols), np.float32)
+    b = X.DevBuf(ctx, (rows, cols), np.uint16)
+    X.call("exn_dequant", ctx.h, w.h, f.h, b.h)
+    with np.errstate(invalid="ignore"):
+        want = xo.dequant_q8_0_blocks(blocks.reshape(-1)).reshape(rows, cols)
+    got = f.get()
+    nan = np.isnan(want)
+    assert (np.isnan(got) == nan).all()
+    assert (got[~nan].view(np.uint32) == want[~nan].view(np.uint32)).all()
+    gb = b.get()
+    wb = xo.bf16_bits(want)
+    assert (gb[~nan] == wb[~nan]).all()
+
+
+# --- the products -----------------------------------------------------------------------
+
+GEMM_CASES = [  # (M, N, K): ragged, the block shapes, proj_out's N = 64, img_in's K = 64, down's K = 12288
+    (77, 96, 128), (256, 512, 4096), (300, 4096, 4096), (257, 64, 4096), (130, 4096, 12288), (64, 4096, 64),
+    (4352, 12288, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_CASES)
+def test_gemm_q8_bf16(ctx, M, N, K):
+    say("gemm q8", M, N, K)
+    rng = np.random.default_rng(M + N + K)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    xb = bf16(x)
+    w = X.Weight.synth(ctx, 3, 200, N, K)
+    qs, d = xo.q8_0_synth(3, 200, N, K)
+    wf = xo.dequant_q8_0(qs, d)
+    dx = dev(ctx, xb)
+    y = X.DevBuf(ctx, (M, N), np.float32)
+    X.call("exn_mm", ctx.h, w.h, dx.h, X.DT_BF16, y.h, X.DT_F32, M)
+    got = y.get()
+    # same bf16 operands, fp32 sums: only the summation order differs
+    rows = slice(None) if M <= 512 else np.r_[0:64, M - 64:M]
+    want_b = from_bf16(xb[rows]).astype(np.float64) @ from_bf16(bf16(wf)).astype(np.float64).T
+    assert xo.rel_l2(got[rows], want_b) < 2e-6
+    # against the fp32 oracle product: the bf16 rounding of the operands only
+    want = x[rows] @ wf.T
+    assert xo.rel_l2(got[rows], want) < 1e-2
+
+
+def test_gemm_bf16_out_and_f32_in(ctx):
+    say("gemm f32 in, bf16 out; gemv n <= 4")
+    rng = np.random.default_rng(1)
+    M, N, K = 40, 256, 4096
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    w = X.Weight.synth(ctx, 4, 201, N, K)
+    wf = xo.dequant_q8_0(*xo.q8_0_synth(4, 201, N, K))
+    dx = dev(ctx, x)
+    y = X.DevBuf(ctx, (M, N), np.uint16)
+    X.call("exn_mm", ctx.h, w.h, dx.h, X.DT_F32, y.h, X.DT_BF16, M)
+    want = from_bf16(bf16(x)).astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)
+    assert xo.rel_l2(from_bf16(y.get()), want) < 4e-3
+    # n <= 4, fp32 activations: the GEMV in fp32 (the timestep path)
+    for m in (1, 2, 4):
+        yg = X.DevBuf(ctx, (m, N), np.float32)
+        X.call("exn_mm", ctx.h, w.h, dev(ctx, x[:m]).h, X.DT_F32, yg.h, X.DT_F32, m)
+        assert xo.rel_l2(yg.get(), x[:m].astype(np.float64) @ wf.T.astype(np.float64)) < 1e-6
+
+
+def test_gemm_weight_f32_branch(ctx):
+    """A non-Q8_0 matrix (src/cuda-dit.lisp:77-80): kept as bf16."""
+    say("gemm f32 weight")
+    rng = np.random.default_rng(2)
+    M, N, K = 100, 192, 256
+    wf = rng.normal(0, 0.05, (N, K)).astype(np.float32)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    w = X.Weight.f32(ctx, wf)
+    y = X.DevBuf(ctx, (M, N), np.float32)
+    X.call("exn_mm", ctx.h, w.h, dev(ctx, bf16(x)).h, X.DT_BF16, y.h, X.DT_F32, M)
+    want = from_bf16(bf16(x)).astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)
+    assert xo.rel_l2(y.get(), want) < 2e-6
+    yg = X.DevBuf(ctx, (2, N), np.float32)
+    X.call("exn_mm", ctx.h, w.h, dev(ctx, x[:2]).h, X.DT_F32, yg.h, X.DT_F32, 2)
+    assert xo.rel_l2(yg.get(), x[:2].astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)) < 1e-6
+
+
+def test_mm_gate_add(ctx):
+    """x += tanh(gate[row]) * (X W^T), rows below p taking the second gate row."""
+    say("mm gate_add")
+    rng = np.random.default_rng(3)
+    M, N, K, n0, p = 200, 4096, 4096, 30, 100
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    resid = rng.normal(0, 1, (M, N)).astype(np.float32)
+    gate = rng.normal(0, 0.5, (2, 4 * N)).astype(np.float32)
+    w = X.Weight.synth(ctx, 6, 202, N, K)
+    wf = xo.dequant_q8_0(*xo.q8_0_synth(6, 202, N, K))
+    r = dev(ctx, resid)
+    g = dev(ctx, gate)
+    X.call("exn_mm_gate_add", ctx.h, w.h, dev(ctx, bf16(x)).h, M, r.h, n0, p, 4 * N, g.h)
+    h = from_bf16(bf16(x)).astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)
+    rows = np.where(n0 + np.arange(M) < p, 1, 0)
+    want = resid + np.tanh(gate[rows, :N].astype(np.float64)) * h
+    assert xo.rel_l2(r.get() - resid, want - resid) < 1e-5
+
+
+def test_mm_swiglu(ctx):
+    say("mm swiglu")
+    rng = np.random.default_rng(4)
+    M, F, K = 150, 512, 4096
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    w = X.Weight.synth(ctx, 7, 203, 2 * F, K).pairs()
+    wf = xo.dequant_q8_0(*xo.q8_0_synth(7, 203, 2 * F, K))
+    ff = X.DevBuf(ctx, (M, F), np.uint16)
+    X.call("exn_mm_swiglu", ctx.h, w.h, dev(ctx, bf16(x)).h, ff.h, M)
+    gu = from_bf16(bf16(x)).astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)
+    want = gu[:, :F] / (1 + np.exp(-gu[:, :F])) * gu[:, F:]
+    assert xo.rel_l2(from_bf16(ff.get()), want) < 4e-3
+    assert xo.rel_l2(from_bf16(ff.get()), xo.silu((x @ wf.T)[:, :F]) * (x @ wf.T)[:, F:]) < 2e-2
+
+
+# --- bandwidth kernels -------------------------------------------------------------------
+
+def test_ln_mod(ctx):
+    """inspect/metal-kernels-test.lisp:91-102's case: width 4096, n 9, n0 3, p 6, inputs x50."""
+    say("ln_mod")
+    rng = np.random.default_rng(7)
+    n, n0, p = 9, 3, 6
+    x = rng.uniform(-50, 50, (n, 4096)).astype(np.float32)
+    mod = rng.uniform(-1, 1, (2, 4096)).astype(np.float32)
+    rows = np.where(n0 + np.arange(n) < p, 1, 0)
+    want = xo.layernorm(x.astype(np.float64)) * (1 + mod[rows])
+    out = X.DevBuf(ctx, (n, 4096), np.float32)
+    X.call("exn_ln_mod", ctx.h, n, n0, p, 4096, dev(ctx, x).h, 4096, dev(ctx, mod).h, out.h, X.DT_F32)
+    assert np.abs(out.get() - want).max() / np.abs(want).max() < 1e-5
+    outb = X.DevBuf(ctx, (n, 4096), np.uint16)
+    X.call("exn_ln_mod", ctx.h, n, n0, p, 4096, dev(ctx, x).h, 4096, dev(ctx, mod).h, outb.h, X.DT_BF16)
+    assert np.abs(from_bf16(outb.get()) - want).max() / np.abs(want).max() < 4e-3
+    # the final norm: one scale row for all rows (mstride 0, p 0), rows LDX apart
+    xs = rng.normal(0, 3, (5, 2 * 4096)).astype(np.float32)
+    sc = rng.normal(0, 1, 4096).astype(np.float32)
+    o2 = X.DevBuf(ctx, (5, 4096), np.float32)
+    X.call("exn_ln_mod", ctx.h, 5, 0, 0, 0, dev(ctx, xs).h, 2 * 4096, dev(ctx, sc).h, o2.h, X.DT_F32)
+    w2 = xo.layernorm(xs[:, :4096].astype(np.float64)) * (1 + sc)
+    assert np.abs(o2.get() - w2).max() / np.abs(w2).max() < 1e-5
+
+
+def test_rms(ctx):
+    """inspect/metal-kernels-test.lisp:104-111's case: width 3072, n 5, inputs x100."""
+    say("rms")
+    rng = np.random.default_rng(8)
+    x = rng.uniform(-100, 100, (5, 3072)).astype(np.float32)
+    w = rng.uniform(-1, 1, 3072).astype(np.float32)
+    want = xo.rmsnorm(x.astype(np.float64), w)
+    y = X.DevBuf(ctx, (5, 3072), np.float32)
+    X.call("exn_rms", ctx.h, 5, 3072, 1e-6, dev(ctx, x).h, dev(ctx, w).h, y.h, X.DT_F32)
+    assert np.abs(y.get() - want).max() / np.abs(want).max() < 1e-5
+
+
+def test_gate_add_swiglu_gelu_silu_euler(ctx):
+    say("gate_add swiglu gelu silu euler")
+    rng = np.random.default_rng(9)
+    n, W, n0, p = 37, 4096, 5, 20
+    x = rng.normal(0, 1, (n, W)).astype(np.float32)
+    h = rng.normal(0, 1, (n, W)).astype(np.float32)
+    gate = rng.normal(0, 1, (2, 4 * W)).astype(np.float32)
+    dx = dev(ctx, x)
+    X.call("exn_gate_add", ctx.h, n * W, W, n0, p, 4 * W, dx.h, dev(ctx, h).h, dev(ctx, gate).h)
+    rows = np.where(n0 + np.arange(n) < p, 1, 0)
+    want = x + np.tanh(gate[rows, :W]) * h
+    assert np.abs(dx.get() - want).max() < 1e-5
+    # swiglu (bf16 in and out)
+    f = 12288
+    gu = rng.normal(0, 2, (7, 2 * f)).astype(np.float32)
+    gub = bf16(gu)
+    o = X.DevBuf(ctx, (7, f), np.uint16)
+    X.call("exn_swiglu", ctx.h, 7, f, dev(ctx, gub).h, o.h)
+    g64 = from_bf16(gub).astype(np.float64)
+    wsw = g64[:, :f] / (1 + np.exp(-g64[:, :f])) * g64[:, f:]
+    assert np.abs(from_bf16(o.get()) - wsw).max() / np.abs(wsw).max() < 4e-3
+    # gelu, silu (fp32 in place)
+    v = np.linspace(-10, 10, 5001).astype(np.float32)
+    dv = dev(ctx, v)
+    X.call("exn_gelu_tanh", ctx.h, v.size, dv.h)
+    assert np.abs(dv.get() - xo.gelu_tanh(v.astype(np.float64))).max() < 2e-6
+    dv = dev(ctx, v)
+    X.call("exn_silu", ctx.h, v.size, dv.h)
+    assert np.abs(dv.get() - xo.silu(v.astype(np.float64))).max() < 2e-6
+    # euler: z + ds * v, two single-float roundings (src/generate.lisp:135)
+    z = rng.normal(0, 1, 1000).astype(np.float32)
+    vv = rng.normal(0, 1, 1000).astype(np.float32)
+    ds = np.float32(0.414568 - 0.704534)
+    dz = dev(ctx, z)
+    X.call("exn_euler", ctx.h, 1000, dz.h, dev(ctx, vv).h, ds)
+    assert (dz.get() == z + ds * vv).all()
+
+
+def _qkv_case(ctx, n, row0, lcap, seed):
+    rng = np.random.default_rng(seed)
+    qkv = rng.normal(0, 3, (n, 3 * 4096)).astype(np.float32)
+    qkvb = f16(qkv)
+    wq = (1 + 0.1 * rng.normal(0, 1, 128)).astype(np.float32)
+    wk = (1 + 0.1 * rng.normal(0, 1, 128)).astype(np.float32)
+    pos = rng.integers(-32, 300, (row0 + n, 3)).astype(np.float32)
+    cos, sin = xo.rope_tables(pos)
+    cs = np.stack([cos, sin], -1).reshape(row0 + n, 128).astype(np.float32)
+    q = X.DevBuf(ctx, (32, n, 128), np.uint16)
+    k = X.DevBuf(ctx, (32, lcap, 128), np.uint16)
+    vt = X.DevBuf(ctx, (32, 128, lcap), np.uint16)
+    X.call("exn_qkv_prep", ctx.h, dev(ctx, qkvb).h, n, dev(ctx, wq).h, dev(ctx, wk).h, dev(ctx, cs).h, q.h, k.h,
+           vt.h, row0, lcap)
+    f = from_f16(qkvb).reshape(n, 3, 32, 128).astype(np.float64)
+    c, s = cos[row0:], sin[row0:]
+    wantq = xo.rope(xo.rmsnorm(f[:, 0], wq), c, s) * (math.log2(math.e) / math.sqrt(128))
+    wantk = xo.rope(xo.rmsnorm(f[:, 1], wk), c, s)
+    return q.get(), k.get(), vt.get(), wantq, wantk, f[:, 2]
+
+
+def test_qkv_prep(ctx):
+    """x_qk_norm_rope's computation (src/cuda/dit.cu:43-58), its outputs rounded to
+    halves as the Metal twin's are (bound 2e-3 there, inspect/metal-kernels-test.lisp:
+    113-128), and v transposed."""
+    say("qkv_prep n 70 row0 33 lcap 128")
+    n, row0, lcap = 70, 33, 128
+    gq, gk, gvt, wq, wk, wv = _qkv_case(ctx, n, row0, lcap, 11)
+    gotq = from_f16(gq).transpose(1, 0, 2)
+    gotk = from_f16(gk[:, row0:row0 + n]).transpose(1, 0, 2)
+    assert np.abs(gotq - wq).max() / np.abs(wq).max() < 2e-3
+    assert np.abs(gotk - wk).max() / np.abs(wk).max() < 2e-3
+    gotv = from_f16(gvt[:, :, row0:row0 + n]).transpose(2, 0, 1)
+    assert (gotv == wv).all()                                   # v only moves: bit-exact
+
+
+def _attend_case(ctx, n, q0, p, l, b0, b1, seed, heads_checked=(0, 7, 31)):
+    rng = np.random.default_rng(seed)
+    lcap = (l + 63) // 64 * 64
+    q = rng.uniform(-2, 2, (n, 32, 128)).astype(np.float32)
+    k = rng.uniform(-2, 2, (l, 32, 128)).astype(np.float32)
+    v = rng.uniform(-1, 1, (l, 32, 128)).astype(np.float32)
+    scale = 1 / math.sqrt(128)
+    qb, kb, vb = f16(q), f16(k), f16(v)
+    qh = np.ascontiguousarray(qb.transpose(1, 0, 2))                         # [32][n][128]
+    kh = np.zeros((32, lcap, 128), np.uint16)
+    kh[:, :l] = kb.transpose(1, 0, 2)
+    vth = np.zeros((32, 128, lcap), np.uint16)
+    vth[:, :, :l] = vb.transpose(1, 2, 0)
+    out = X.DevBuf(ctx, (n, 4096), np.uint16)
+    X.call("exn_attend", ctx.h, dev(ctx, qh).h, dev(ctx, kh).h, dev(ctx, vth).h, out.h, n, q0, p, l, lcap, b0, b1,
+           scale * math.log2(math.e))
+    got = from_bf16(out.get()).reshape(n, 32, 128)
+    qf, kf, vf = (from_f16(a).astype(np.float64) for a in (qb, kb, vb))
+    want = np.zeros((n, len(heads_checked), 128))
+    for t in range(n):
+        lim = int(xo.xa_lim(q0 + t, p, l, b0, b1))
+        for j, h in enumerate(heads_checked):
+            s = kf[:lim + 1, h] @ qf[t, h] * scale
+            e = np.exp(s - s.max())
+            want[t, j] = e @ vf[:lim + 1, h] / e.sum()
+    return got[:, list(heads_checked)], want
+
+
+@pytest.mark.parametrize("n,q0,p,l,b0,b1", [(77, 0, 20, 77, 20, 20), (70, 33, 33, 103, 33, 33),
+                                            (90, 0, 40, 90, 12, 30)])
+def test_attention_mask_cases(ctx, n, q0, p, l, b0, b1):
+    """The three mask cases of inspect/metal-kernels-test.lisp:144-146, float64
+    brute force on the same fp16 inputs; the bound is the Metal test's 3e-3 for
+    P in halves, plus the output's rounding to bf16 (2^-9 of |out| <= 1)."""
+    say("attend", n, q0, p, l, b0, b1)
+    got, want = _attend_case(ctx, n, q0, p, l, b0, b1, n + l)
+    assert np.abs(got - want).max() < 3e-3 + 2 ** -9
+    assert xo.rel_l2(got, want) < 3e-3
+
+
+def test_attention_longer(ctx):
+    """Image queries after a cached prompt over several key tiles, every head."""
+    say("attend 300 queries over 556 keys")
+    got, want = _attend_case(ctx, 300, 256, 256, 556, 0, 0, 5, heads_checked=tuple(range(0, 32, 3)))
+    assert xo.rel_l2(got, want) < 3e-3
