@@ -99,8 +99,11 @@ def main():
     t0 = time.perf_counter()
     d.synth(SEED)
     d.check()
-    print("bench: synthetic 7B Q8_0 DiT on the device in %.1f s" % (time.perf_counter() - t0), file=sys.stderr,
-          flush=True)
+    t1 = time.perf_counter()
+    d.resident(True)
+    w_bytes, _ = d.memory()
+    print("bench: synthetic 7B Q8_0 DiT on the device in %.1f s, block matrices expanded to resident bf16 in %.1f s "
+          "(%.1f GB of weights)" % (t1 - t0, time.perf_counter() - t1, w_bytes / 1e9), file=sys.stderr, flush=True)
     rng = np.random.default_rng(SEED)
     context = X.DevBuf.of(ctx, rng.normal(0, 1, (P, 4096)).astype(np.float32))
     latent = rng.normal(0, 1, (64, H, W)).astype(np.float32)

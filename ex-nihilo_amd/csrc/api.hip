@@ -63,6 +63,8 @@ struct exn_w {
   int8_t* qs = nullptr;
   uint16_t* d = nullptr;
   uint16_t* wb = nullptr;  // bf16 rows (EXN_F32 / EXN_BF16 matrices)
+  uint16_t* wx = nullptr;  // a Q8_0 matrix's resident bf16 expansion, bf16(fp32(d) * q) exactly
+  bool wx_ok = false;      // wx matches qs/d
   bool pairs = false;      // gate/up rows interleaved by 32
   bool view = false;       // rows inside another allocation (not freed here)
 };
@@ -246,6 +248,7 @@ int exn_weight_free(exn_w* w) {
     dev_free(w->qs);
     dev_free(w->d);
     dev_free(w->wb);
+    dev_free(w->wx);
   }
   delete w;
   return EXN_OK;
@@ -351,6 +354,33 @@ int exn_dequant(exn_ctx* ctx, const exn_w* w, float* f32, uint16_t* bf16) {
   return EXN_OK;
 }
 
+// keep (bf16 = 1) or drop (0) a Q8_0 matrix's bf16 expansion; products use it while it is kept
+static int w_resident(exn_w* w, bool bf16) {
+  if (w->kind != EXN_Q8_0) return EXN_OK;
+  if (!bf16) {
+    if (w->wx) {
+      HIPCHK(hipStreamSynchronize(w->ctx->stream));
+      dev_free(w->wx);
+    }
+    w->wx = nullptr;
+    w->wx_ok = false;
+    return EXN_OK;
+  }
+  if (w->wx_ok) return EXN_OK;
+  if (!w->wx) TRY(dev_alloc((void**)&w->wx, (size_t)(w->rows * w->cols) * 2));
+  HIPCHK(dequant_q8(w->ctx->stream, w->qs, w->d, w->rows * w->cols, nullptr, w->wx));
+  w->wx_ok = true;
+  return EXN_OK;
+}
+
+int exn_weight_resident(exn_ctx* ctx, exn_w* w, int bf16) {
+  TRY(use(ctx));
+  if (!w) FAIL(EXN_EINVAL, "null weight");
+  TRY(w_resident(w, bf16 != 0));
+  HIPCHK(hipStreamSynchronize(ctx->stream));
+  return EXN_OK;
+}
+
 static std::vector<int32_t> pair_rows(int64_t rows) {
   // gate row i (i < rows/2) -> 64*(i/32) + i%32; up row i -> 64*(i/32) + 32 + i%32
   const int64_t f = rows / 2;
@@ -401,6 +431,11 @@ int exn_weight_pairs(exn_ctx* ctx, exn_w* w) {
   w->qs = qs;
   w->d = d;
   w->pairs = true;
+  if (w->wx) {
+    w->wx_ok = false;
+    TRY(w_resident(w, true));
+    HIPCHK(hipStreamSynchronize(w->ctx->stream));
+  }
   return EXN_OK;
 }
 
@@ -416,8 +451,8 @@ static int check_gemm(const exn_w* w, int64_t n) {
 static hipError_t gemm_any(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, Epi epi,
                            const EpiArgs& ea) {
   if (n == 0) return hipSuccess;
-  if (w->kind == EXN_Q8_0) return gemm_q8(s, x, lda, w->qs, w->d, n, w->rows, w->cols, epi, ea);
-  return gemm_wbf16(s, x, lda, w->wb, n, w->rows, w->cols, epi, ea);
+  if (w->kind == EXN_Q8_0 && !w->wx_ok) return gemm_q8(s, x, lda, w->qs, w->d, n, w->rows, w->cols, epi, ea);
+  return gemm_wbf16(s, x, lda, w->kind == EXN_Q8_0 ? w->wx : w->wb, n, w->rows, w->cols, epi, ea);
 }
 
 int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n) {
@@ -609,6 +644,7 @@ struct exn_dit {
   bool have_edge[9] = {};
   std::vector<Layer> L;
   int32_t* pair_map = nullptr;  // device row map of the gate_up interleave
+  bool bf16 = true;             // block matrices run from resident bf16 expansions (exn_dit_resident)
   // scratch
   std::map<std::string, Buf> bufs;
   // kept prompt K/V: per layer K [32][lcap][128] and V^T [32][128][lcap], bf16
@@ -821,7 +857,8 @@ int exn_dit_memory(exn_dit* d, int64_t* weights, int64_t* scratch) {
   int64_t w = 0, s = 0;
   auto wb = [](const exn_w* x) -> int64_t {
     if (!x) return 0;
-    return x->kind == EXN_Q8_0 ? x->rows * x->cols + x->rows * x->cols / 16 : 2 * x->rows * x->cols;
+    return (x->kind == EXN_Q8_0 ? x->rows * x->cols + x->rows * x->cols / 16 : 2 * x->rows * x->cols) +
+           (x->wx ? 2 * x->rows * x->cols : 0);
   };
   for (auto x : d->edge) w += wb(x);
   for (auto& l : d->L) w += wb(l.qkv) + wb(l.out) + wb(l.gate_up) + wb(l.down) + 2 * 4 * EXN_HD;
@@ -914,6 +951,7 @@ int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_
   const int32_t* map = nullptr;
   TRY(layer_target(d, layer, slot, &w, &row0, &map));
   TRY(upload_q8_blocks(ctx, data, rows, cols, map, w->qs + row0 * cols, w->d + row0 * (cols / 32)));
+  w->wx_ok = false;
   d->L[(size_t)layer].have |= (uint8_t)(1u << slot);
   return EXN_OK;
 }
@@ -953,11 +991,23 @@ int exn_dit_synth(exn_dit* d, uint64_t seed) {
         const int32_t* map = nullptr;
         TRY(layer_target(d, layer, sl, &w, &row0, &map));
         HIPCHK(synth_q8(s, key, ex.d1, ex.d0, ex.d0 / 32, map, w->qs + row0 * ex.d0, w->d + row0 * (ex.d0 / 32)));
+        w->wx_ok = false;
       }
       L.have |= (uint8_t)(1u << sl);
     }
   }
   HIPCHK(hipStreamSynchronize(s));
+  return EXN_OK;
+}
+
+int exn_dit_resident(exn_dit* d, int bf16) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  TRY(use(d->ctx));
+  d->bf16 = bf16 != 0;
+  for (auto& l : d->L)
+    for (exn_w* w : {l.qkv, l.out, l.gate_up, l.down})
+      if (w) TRY(w_resident(w, d->bf16));
+  HIPCHK(hipStreamSynchronize(d->ctx->stream));
   return EXN_OK;
 }
 
@@ -1099,6 +1149,9 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   if (h <= 0 || w <= 0 || ptext < 0 || !latent || !v) FAIL(EXN_EINVAL, "velocity: h %d, w %d, p %d", h, w, ptext);
   const bool edit = ref_latent != nullptr;
   if (edit && (rh <= 0 || rw <= 0 || ref_a < 0 || ref_a > ptext)) FAIL(EXN_EINVAL, "reference picture: a %d, %d x %d", ref_a, rh, rw);
+  if (d->bf16)
+    for (auto& l : d->L)
+      for (exn_w* m : {l.qkv, l.out, l.gate_up, l.down}) TRY(w_resident(m, true));
   exn_ctx* ctx = d->ctx;
   hipStream_t s = ctx->stream;
   const int64_t nimg = (int64_t)h * w;

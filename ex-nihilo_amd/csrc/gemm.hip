@@ -26,6 +26,64 @@ namespace exn {
 //   B (16 x 32): lane l holds column l%32, k = 8*(l/32) .. +7
 //   D (32 x 32): lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15
 
+// The store of a wave's accumulators (rows wrow.., columns wcol..), fused with the
+// reference's elementwise step that follows the product.
+template <int EPI, int MI, int NI>
+__device__ __forceinline__ void epilogue(const f32x16 (&acc)[MI][NI], int64_t wrow, int64_t wcol, int lane, int64_t M,
+                                         int64_t N, const EpiArgs& ea) {
+  if constexpr (EPI == EPI_SWIGLU) {
+    // accumulator pairs (2jj, 2jj+1) hold matching gate and up columns (rows interleaved by 32 at load)
+    uint16_t* y = (uint16_t*)ea.y;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int jj = 0; jj < NI / 2; ++jj) {
+        const int64_t col = wcol / 2 + jj * 32 + (lane & 31);
+        if (2 * (col - (lane & 31)) >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = wrow + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+          if (m < M) {
+            const float g = acc[i][2 * jj][r], u = acc[i][2 * jj + 1][r];
+            y[m * ea.ldy + col] = (uint16_t)(pack_bf16x2(silu_f(g) * u, 0.f) & 0xFFFF);
+          }
+        }
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int64_t n = wcol + j * 32 + (lane & 31);
+      if (n >= N) continue;
+      float g0 = 0.f, g1 = 0.f;
+      if constexpr (EPI == EPI_GATE_ADD) {
+        g0 = tanh_f(ea.gate[n]);
+        g1 = tanh_f(ea.gate[ea.mstride + n]);
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = wrow + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+          if (m >= M) continue;
+          const float v = acc[i][j][r];
+          if constexpr (EPI == EPI_F32) {
+            ((float*)ea.y)[m * ea.ldy + n] = v;
+          } else if constexpr (EPI == EPI_BF16) {
+            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFF);
+          } else if constexpr (EPI == EPI_F16) {
+            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFF);
+          } else if constexpr (EPI == EPI_GELU_BF16) {
+            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_bf16x2(gelu_tanh_f(v), 0.f) & 0xFFFF);
+          } else if constexpr (EPI == EPI_GATE_ADD) {
+            const float g = (ea.n0 + m < ea.p) ? g1 : g0;
+            float* x = ea.resid + m * ea.ldy + n;
+            *x = *x + g * v;
+          }
+        }
+    }
+  }
+}
+
 template <int BM, int BN, int WM, int WN, bool WBF16, int EPI>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 k_gemm(const uint16_t* __restrict__ X, int64_t lda, const int8_t* __restrict__ QS, const uint16_t* __restrict__ D,
@@ -145,59 +203,7 @@ k_gemm(const uint16_t* __restrict__ X, int64_t lda, const int8_t* __restrict__ Q
     __syncthreads();
   }
 
-  // --- epilogue ---
-  const int64_t wrow = m0 + wm * WM, wcol = n0 + wn * WN;
-  if constexpr (EPI == EPI_SWIGLU) {
-    // accumulator pairs (2jj, 2jj+1) hold matching gate and up columns (rows interleaved by 32 at load)
-    uint16_t* y = (uint16_t*)ea.y;
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int jj = 0; jj < NI / 2; ++jj) {
-        const int64_t col = wcol / 2 + jj * 32 + (lane & 31);
-        if (2 * (col - (lane & 31)) >= N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = wrow + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-          if (m < M) {
-            const float g = acc[i][2 * jj][r], u = acc[i][2 * jj + 1][r];
-            y[m * ea.ldy + col] = (uint16_t)(pack_bf16x2(silu_f(g) * u, 0.f) & 0xFFFF);
-          }
-        }
-      }
-  } else {
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int64_t n = wcol + j * 32 + (lane & 31);
-      if (n >= N) continue;
-      float g0 = 0.f, g1 = 0.f;
-      if constexpr (EPI == EPI_GATE_ADD) {
-        g0 = tanh_f(ea.gate[n]);
-        g1 = tanh_f(ea.gate[ea.mstride + n]);
-      }
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = wrow + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-          if (m >= M) continue;
-          const float v = acc[i][j][r];
-          if constexpr (EPI == EPI_F32) {
-            ((float*)ea.y)[m * ea.ldy + n] = v;
-          } else if constexpr (EPI == EPI_BF16) {
-            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFF);
-          } else if constexpr (EPI == EPI_F16) {
-            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_f16x2(v, 0.f) & 0xFFFF);
-          } else if constexpr (EPI == EPI_GELU_BF16) {
-            ((uint16_t*)ea.y)[m * ea.ldy + n] = (uint16_t)(pack_bf16x2(gelu_tanh_f(v), 0.f) & 0xFFFF);
-          } else if constexpr (EPI == EPI_GATE_ADD) {
-            const float g = (ea.n0 + m < ea.p) ? g1 : g0;
-            float* x = ea.resid + m * ea.ldy + n;
-            *x = *x + g * v;
-          }
-        }
-    }
-  }
+  epilogue<EPI, MI, NI>(acc, m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
 template <int BM, int BN, int WM, int WN, bool WBF16, int EPI>
@@ -221,12 +227,12 @@ template <bool WBF16>
 static hipError_t dispatch(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d,
                            const uint16_t* wb, int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea) {
   switch (epi) {
-    case EPI_F32: return launch<128, 128, 64, 64, WBF16, EPI_F32>(s, x, lda, qs, d, wb, M, N, K, ea);
-    case EPI_BF16: return launch<128, 128, 64, 64, WBF16, EPI_BF16>(s, x, lda, qs, d, wb, M, N, K, ea);
-    case EPI_GATE_ADD: return launch<128, 128, 64, 64, WBF16, EPI_GATE_ADD>(s, x, lda, qs, d, wb, M, N, K, ea);
-    case EPI_SWIGLU: return launch<128, 128, 64, 64, WBF16, EPI_SWIGLU>(s, x, lda, qs, d, wb, M, N, K, ea);
-    case EPI_GELU_BF16: return launch<128, 128, 64, 64, WBF16, EPI_GELU_BF16>(s, x, lda, qs, d, wb, M, N, K, ea);
-    case EPI_F16: return launch<128, 128, 64, 64, WBF16, EPI_F16>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_F32: return launch<256, 256, 128, 64, WBF16, EPI_F32>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_BF16: return launch<256, 256, 128, 64, WBF16, EPI_BF16>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_GATE_ADD: return launch<256, 256, 128, 64, WBF16, EPI_GATE_ADD>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_SWIGLU: return launch<256, 256, 128, 64, WBF16, EPI_SWIGLU>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_GELU_BF16: return launch<256, 256, 128, 64, WBF16, EPI_GELU_BF16>(s, x, lda, qs, d, wb, M, N, K, ea);
+    case EPI_F16: return launch<256, 256, 128, 64, WBF16, EPI_F16>(s, x, lda, qs, d, wb, M, N, K, ea);
   }
   return hipErrorInvalidValue;
 }
@@ -236,9 +242,147 @@ hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* 
   return dispatch<false>(s, x, lda, qs, d, nullptr, M, N, K, epi, ea);
 }
 
+// --- bf16 weights: the pipelined kernel ----------------------------------------------
+// 256 x 256 tiles, 8 waves of 128 x 64, BK = 64.  Both tiles go HBM/L2 -> LDS by the
+// LDS DMA path (global_load_lds_dwordx4: no VGPR staging, no ds_write), two stages.
+// Inside a step the wave's fragment registers are double-buffered: the ds_reads of
+// slice kk+1 are interleaved with the MFMAs of slice kk (sched_group_barrier), and the
+// step's one barrier sits before the last slice, so the next step's DMA and first
+// fragment reads overlap that slice's MFMAs.
+// LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by (row/2)%8: the
+// fragment reads of 32 rows x 16 bytes are bank-conflict free.
+typedef __attribute__((address_space(3))) void lds_void;
+#define LDS_VMCNT0_BARRIER()                                     \
+  do {                                                           \
+    asm volatile("" ::: "memory");                               \
+    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));         \
+    __builtin_amdgcn_s_barrier();                                \
+    asm volatile("" ::: "memory");                               \
+  } while (0)
+#define SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+
+__device__ __forceinline__ int chunk_swz(int r) { return (r >> 1) & 7; }
+
+template <int EPI>
+__global__ void __launch_bounds__(512)
+k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB, int64_t M, int64_t N,
+          int64_t K, EpiArgs ea) {
+  constexpr int NW = 8, WM = 128, WN = 64, MI = WM / 32, NI = WN / 32, ROUNDS = 256 / (NW * 8);
+  constexpr int NMF = MI * NI, NRD = MI + NI;
+  extern __shared__ __align__(1024) uint8_t smem[];   // 2 stages x (X tile 32 KB | W tile 32 KB)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / (256 / WN), wn = wave % (256 / WN);
+  const int64_t m0 = (int64_t)blockIdx.y * 256, n0 = (int64_t)blockIdx.x * 256;
+  const int KT = (int)(K / 64);
+  // DMA: round i of wave w moves rows (i*8 + w)*8 .. +7, lane l row +l/8, LDS chunk l%8
+  const uint16_t* a_src[ROUNDS];
+  const uint16_t* w_src[ROUNDS];
+#pragma unroll
+  for (int i = 0; i < ROUNDS; ++i) {
+    const int row = (i * NW + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ chunk_swz(row);
+    a_src[i] = X + min(m0 + row, M - 1) * lda + 8 * c;
+    w_src[i] = WB + min(n0 + row, N - 1) * K + 8 * c;
+  }
+  auto dma = [&](int t) {
+    uint8_t* a = smem + (t & 1) * 65536;
+    uint8_t* b = a + 32768;
+#pragma unroll
+    for (int i = 0; i < ROUNDS; ++i) {
+      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + (int64_t)t * 64), (lds_void*)(a + (i * NW + wave) * 1024),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + (int64_t)t * 64), (lds_void*)(b + (i * NW + wave) * 1024),
+                                       16, 0, 0);
+    }
+  };
+  const int lo = lane & 31, hi = lane >> 5, fs = chunk_swz(lo);
+  const uint8_t* a_rd = smem + (wm * WM + lo) * 128;
+  const uint8_t* b_rd = smem + 32768 + (wn * WN + lo) * 128;
+  struct Frag {
+    bf16x8 a[MI], b[NI];
+  };
+  auto rd = [&](Frag& f, int stage, int kk) {
+    const int off = stage * 65536 + (((2 * kk + hi) ^ fs) << 4);
+#pragma unroll
+    for (int i = 0; i < MI; ++i) f.a[i] = *(const bf16x8*)(a_rd + off + i * 32 * 128);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) f.b[j] = *(const bf16x8*)(b_rd + off + j * 32 * 128);
+  };
+  f32x16 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+  };
+  Frag F0, F1;
+  dma(0);
+  LDS_VMCNT0_BARRIER();
+  if (KT > 1) dma(1);
+  rd(F0, 0, 0);
+  for (int t = 0; t < KT; ++t) {
+    const int cur = t & 1;
+    rd(F1, cur, 1);
+    mma(F0);
+#pragma unroll
+    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); }
+    SGB(0x008, NMF - NRD);
+    rd(F0, cur, 2);
+    mma(F1);
+#pragma unroll
+    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); }
+    SGB(0x008, NMF - NRD);
+    rd(F1, cur, 3);
+    mma(F0);
+#pragma unroll
+    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); }
+    SGB(0x008, NMF - NRD);
+    // every wave has its slice-3 fragments and its DMA of step t+1 has landed: stage cur is free
+    LDS_VMCNT0_BARRIER();
+    if (t + 2 < KT) dma(t + 2);
+    if (t + 1 < KT) rd(F0, cur ^ 1, 0);
+    mma(F1);
+#pragma unroll
+    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); SGB(0x020, 2); }
+    SGB(0x008, NMF - NRD);
+  }
+  epilogue<EPI, MI, NI>(acc, m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
+}
+
+template <int EPI>
+static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* wb, int64_t M, int64_t N,
+                            int64_t K, const EpiArgs& ea) {
+  const size_t shm = 2 * 65536;
+  auto kern = k_gemm_bt<EPI>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256));
+  hipLaunchKernelGGL(kern, grid, dim3(512), shm, s, x, lda, wb, M, N, K, ea);
+  return hipGetLastError();
+}
+
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
                       int64_t K, Epi epi, const EpiArgs& ea) {
-  return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
+  // the DMA path moves 16-byte chunks: rows of X and W must start 16-byte aligned
+  const bool dma_ok = K % 64 == 0 && lda % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0;
+  if (!dma_ok) return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
+  switch (epi) {
+    case EPI_F32: return launch_bt<EPI_F32>(s, x, lda, w, M, N, K, ea);
+    case EPI_BF16: return launch_bt<EPI_BF16>(s, x, lda, w, M, N, K, ea);
+    case EPI_GATE_ADD: return launch_bt<EPI_GATE_ADD>(s, x, lda, w, M, N, K, ea);
+    case EPI_SWIGLU: return launch_bt<EPI_SWIGLU>(s, x, lda, w, M, N, K, ea);
+    case EPI_GELU_BF16: return launch_bt<EPI_GELU_BF16>(s, x, lda, w, M, N, K, ea);
+    case EPI_F16: return launch_bt<EPI_F16>(s, x, lda, w, M, N, K, ea);
+  }
+  return hipErrorInvalidValue;
 }
 
 // --- the edge products in fp32 -------------------------------------------------------

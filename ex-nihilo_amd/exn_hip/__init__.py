@@ -67,6 +67,7 @@ SIGNATURES = {
     "exn_mm_gate_add": (c_int, [vp, vp, vp, c_int64, vp, c_int, c_int, c_int, vp]),
     "exn_mm_swiglu": (c_int, [vp, vp, vp, vp, c_int64]),
     "exn_weight_pairs": (c_int, [vp, vp]),
+    "exn_weight_resident": (c_int, [vp, vp, c_int]),
     "exn_ln_mod": (c_int, [vp, c_int, c_int, c_int, c_int, vp, c_int64, vp, vp, c_int]),
     "exn_rms": (c_int, [vp, c_int, c_int, c_float, vp, vp, vp, c_int]),
     "exn_gate_add": (c_int, [vp, c_int64, c_int, c_int, c_int, c_int, vp, vp, vp]),
@@ -80,6 +81,7 @@ SIGNATURES = {
     "exn_dit_set": (c_int, [vp, c_char_p, c_int, vp, c_int64, c_int64]),
     "exn_dit_synth": (c_int, [vp, c_uint64]),
     "exn_dit_check": (c_int, [vp]),
+    "exn_dit_resident": (c_int, [vp, c_int]),
     "exn_dit_velocity": (c_int, [vp, vp, c_int, vp, c_int, c_int, c_double, c_uint64, c_int, vp, c_int, c_int, vp]),
     "exn_dit_velocity_dev": (c_int, [vp, vp, c_int, vp, c_int, c_int, c_double, c_uint64, c_int, vp, c_int, c_int,
                                      vp]),
@@ -224,6 +226,11 @@ class Weight:
         call("exn_weight_pairs", self.ctx.h, self.h)
         return self
 
+    def resident(self, bf16: bool = True):
+        """Keep (or drop) the matrix's resident bf16 expansion, which products then use."""
+        call("exn_weight_resident", self.ctx.h, self.h, 1 if bf16 else 0)
+        return self
+
     def free(self):
         if getattr(self, "h", None):
             call("exn_weight_free", self.h)
@@ -263,6 +270,10 @@ class Dit:
 
     def check(self):
         call("exn_dit_check", self.h)
+
+    def resident(self, bf16: bool = True):
+        """Block matrices from resident bf16 expansions (the default) or from Q8_0."""
+        call("exn_dit_resident", self.h, 1 if bf16 else 0)
 
     def prefix_key(self, key) -> int:
         """A 64-bit key for a Lisp-style prefix key (EQUAL objects -> one key)."""

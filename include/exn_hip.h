@@ -89,6 +89,11 @@ int exn_weight_info(const exn_w* w, int64_t* rows, int64_t* cols, int* kind);
 int exn_weight_free(exn_w* w);
 /* test hook: W dequantised, fp32(d) * q into F32 and its bf16 rounding into BF16 (either may be NULL) */
 int exn_dequant(exn_ctx* ctx, const exn_w* w, float* f32, uint16_t* bf16);
+/* no reference counterpart (the reference keeps Q8_0 in 24 GB): BF16 = 1 keeps a resident
+ * bf16 expansion of a Q8_0 matrix, bf16(fp32(d) * q) -- the values its products round
+ * the weights to anyway -- and the products then stream it instead of dequantising in
+ * the kernel; 0 drops it.  Costs 2 bytes a weight on top of the 1.0625 of Q8_0. */
+int exn_weight_resident(exn_ctx* ctx, exn_w* w, int bf16);
 
 /* --- ops: the kernels of src/cuda/dit.cu and illatio's products, on device pointers ------------------ */
 
@@ -150,6 +155,11 @@ int exn_dit_synth(exn_dit* d, uint64_t seed);
 /* EXN_OK when every expected tensor is present, else EXN_ESTATE naming each missing one
  * (open-dit's check, src/weights.lisp:47-61) */
 int exn_dit_check(exn_dit* d);
+/* no reference counterpart: BF16 = 1 (the default) runs the block matrices from resident
+ * bf16 expansions (exn_weight_resident; 14 GB for the 7B model), made here for the matrices
+ * present and at the next step for any set later; 0 drops them and runs from Q8_0 with the
+ * dequantisation inside the product */
+int exn_dit_resident(exn_dit* d, int bf16);
 /* dit-velocity (src/cuda-dit.lisp:137-243): CONTEXT (P x 4096 fp32, the encoder's states),
  * LATENT (64 x H x W fp32, channel-major) -> V (64 x H x W), host memory, synchronous.
  * SIGMA is a double, as the reference's schedule (src/generate.lisp:7-9); t = 1000 sigma.

@@ -126,6 +126,27 @@ def test_edit_mode(ctx):
     d.destroy()
 
 
+def test_q8_0_and_resident_bf16_agree(ctx):
+    """The block matrices from Q8_0 (dequantised inside the products) and from their
+    resident bf16 expansions (the default) give one velocity: the operands are the same
+    bf16 values, only the fp32 summation order differs."""
+    say("q8_0 vs resident bf16 weights, 2 blocks")
+    seed, p, h, w = 8, 40, 16, 16
+    d = model(ctx, 2, seed)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    v_bf = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7)
+    d.resident(False)
+    v_q8 = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7)
+    d.resident(True)
+    v_bf2 = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7)
+    ref = xo.forward(xo.SynthWeights(seed), ctxa, lat, 0.7, layers=2)
+    e, e_ref = xo.rel_l2(v_bf, v_q8), xo.rel_l2(v_bf, ref)
+    say("resident vs q8_0 rel-L2 %.2e, vs oracle %.2e" % (e, e_ref))
+    assert e < 2e-3 and xo.rel_l2(v_bf2, v_bf) == 0.0
+    assert e_ref < 1e-2 and xo.rel_l2(v_q8, ref) < 1e-2
+    d.destroy()
+
+
 def test_device_and_host_paths_agree(ctx):
     """exn_dit_velocity (host arrays) and exn_dit_velocity_dev (device arrays) give
     the same velocity; generate's Euler loop on the device gives the host loop's

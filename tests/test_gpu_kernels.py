@@ -107,13 +107,18 @@ GEMM_CASES = [  # (M, N, K): ragged, the block shapes, proj_out's N = 64, img_in
     (4352, 12288, 4096)]
 
 
+@pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])
 @pytest.mark.parametrize("M,N,K", GEMM_CASES)
-def test_gemm_q8_bf16(ctx, M, N, K):
-    say("gemm q8", M, N, K)
+def test_gemm_q8_bf16(ctx, M, N, K, resident):
+    """Q8_0 dequantised inside the product, or streamed from the resident bf16
+    expansion (exn_weight_resident) by the LDS-DMA kernel: the same bf16 operands."""
+    say("gemm q8", M, N, K, "resident bf16" if resident else "q8_0")
     rng = np.random.default_rng(M + N + K)
     x = rng.normal(0, 1, (M, K)).astype(np.float32)
     xb = bf16(x)
     w = X.Weight.synth(ctx, 3, 200, N, K)
+    if resident:
+        w.resident()
     qs, d = xo.q8_0_synth(3, 200, N, K)
     wf = xo.dequant_q8_0(qs, d)
     dx = dev(ctx, xb)
@@ -129,12 +134,15 @@ def test_gemm_q8_bf16(ctx, M, N, K):
     assert xo.rel_l2(got[rows], want) < 1e-2
 
 
-def test_gemm_bf16_out_and_f32_in(ctx):
+@pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])
+def test_gemm_bf16_out_and_f32_in(ctx, resident):
     say("gemm f32 in, bf16 out; gemv n <= 4")
     rng = np.random.default_rng(1)
     M, N, K = 40, 256, 4096
     x = rng.normal(0, 1, (M, K)).astype(np.float32)
     w = X.Weight.synth(ctx, 4, 201, N, K)
+    if resident:
+        w.resident()
     wf = xo.dequant_q8_0(*xo.q8_0_synth(4, 201, N, K))
     dx = dev(ctx, x)
     y = X.DevBuf(ctx, (M, N), np.uint16)
@@ -165,7 +173,8 @@ def test_gemm_weight_f32_branch(ctx):
     assert xo.rel_l2(yg.get(), x[:2].astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)) < 1e-6
 
 
-def test_mm_gate_add(ctx):
+@pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])
+def test_mm_gate_add(ctx, resident):
     """x += tanh(gate[row]) * (X W^T), rows below p taking the second gate row."""
     say("mm gate_add")
     rng = np.random.default_rng(3)
@@ -174,6 +183,8 @@ def test_mm_gate_add(ctx):
     resid = rng.normal(0, 1, (M, N)).astype(np.float32)
     gate = rng.normal(0, 0.5, (2, 4 * N)).astype(np.float32)
     w = X.Weight.synth(ctx, 6, 202, N, K)
+    if resident:
+        w.resident()
     wf = xo.dequant_q8_0(*xo.q8_0_synth(6, 202, N, K))
     r = dev(ctx, resid)
     g = dev(ctx, gate)
@@ -184,12 +195,16 @@ def test_mm_gate_add(ctx):
     assert xo.rel_l2(r.get() - resid, want - resid) < 1e-5
 
 
-def test_mm_swiglu(ctx):
+@pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])
+def test_mm_swiglu(ctx, resident):
     say("mm swiglu")
     rng = np.random.default_rng(4)
     M, F, K = 150, 512, 4096
     x = rng.normal(0, 1, (M, K)).astype(np.float32)
-    w = X.Weight.synth(ctx, 7, 203, 2 * F, K).pairs()
+    w = X.Weight.synth(ctx, 7, 203, 2 * F, K)
+    if resident:           # expanded before the interleave: exn_weight_pairs re-expands it
+        w.resident()
+    w.pairs()
     wf = xo.dequant_q8_0(*xo.q8_0_synth(7, 203, 2 * F, K))
     ff = X.DevBuf(ctx, (M, F), np.uint16)
     X.call("exn_mm_swiglu", ctx.h, w.h, dev(ctx, bf16(x)).h, ff.h, M)
