@@ -36,6 +36,7 @@ P = 256                       # text rows
 LAYERS = 32
 SEED = 2
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_1024sq_traffic.json")
+PROBE_BYTES = 1 << 30         # --copy-probe 1024
 
 
 def gemm_flops_per_row():
@@ -53,16 +54,14 @@ def step_flops(cached):
     return gemm, att, gemm + att
 
 
-def cpu_baseline():
-    """The oracle's cached block at the workload's shape (4096 image rows over
-    256 kept prompt rows + themselves), one timed call, x32 blocks."""
+def cpu_baseline(blocks=5):
+    """The oracle's cached block at the workload's shape (4096 image rows over 256 kept
+    prompt rows + themselves) for blocks 0..BLOCKS-1, each timed once after its weights
+    are dequantised; the step is their mean x 32 blocks."""
     sys.path.insert(0, REPO)
     from oracle import exn_oracle as xo
     rng = np.random.default_rng(0)
-    wt = xo.SynthWeights(SEED, cache_bytes=4 << 30)
-    for slot in ("attn.to_q.weight", "attn.to_k.weight", "attn.to_v.weight", "attn.to_out.0.weight",
-                 "img_mlp.gate_up.weight", "img_mlp.out.weight"):
-        wt("transformer_blocks.0." + slot)              # dequantised before the clock starts
+    wt = xo.SynthWeights(SEED, cache_bytes=6 << 30)
     n, l = H * W, P + H * W
     x = rng.normal(0, 1, (n, 4096)).astype(np.float32)
     mod = rng.normal(0, 0.05, (n, 4 * 4096)).astype(np.float32)
@@ -71,14 +70,64 @@ def cpu_baseline():
     vf = np.zeros((l, 32, 128), np.float32)
     kf[:P] = rng.normal(0, 1, (P, 32, 128))
     vf[:P] = rng.normal(0, 1, (P, 32, 128))
-    t0 = time.perf_counter()
-    xo.block(wt, 0, x, mod, cos, sin, kf, vf, P, P, 0, 0)
-    dt = time.perf_counter() - t0
+    times = []
+    for layer in range(blocks):
+        for slot in ("attn.to_q.weight", "attn.to_k.weight", "attn.to_v.weight", "attn.to_out.0.weight",
+                     "img_mlp.gate_up.weight", "img_mlp.out.weight", "attn.norm_q.weight", "attn.norm_k.weight"):
+            wt("transformer_blocks.%d.%s" % (layer, slot))   # dequantised before the clock starts
+        t0 = time.perf_counter()
+        x = xo.block(wt, layer, x, mod, cos, sin, kf, vf, P, P, 0, 0)
+        times.append(time.perf_counter() - t0)
+    dt = float(np.mean(times))
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     threads = int(os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS") or cores)
     return {"value": round(dt * 1e3 * LAYERS, 1), "unit": "ms/step", "cores": min(cores, threads), "kind": "port",
-            "sample": "one cached block (4096 image rows over 4352 keys) of the 1024^2 step in numpy fp32, "
-                      "timed once (%.1f s), x32 blocks: an extrapolated step" % dt}
+            "sample": "blocks 0..%d of the cached 1024^2 step (4096 image rows over 4352 keys) in numpy fp32, "
+                      "%.1f s of block time (%s s each), mean x 32 blocks: an extrapolated step"
+                      % (blocks - 1, sum(times), "/".join("%.1f" % t for t in times))}
+
+
+def traffic_from(fetch_db, write_db):
+    """HBM bytes a launch of the gate_up product moves, from rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE runs (KiB a dispatch) of `bench.py --copy-probe MIB`, each counter scaled by
+    what it reads for the probe's device-to-device copy of a known size."""
+    import sqlite3
+
+    def per_kernel(db, counter):
+        c = sqlite3.connect(db)
+        rows = c.execute("select kernel_name, value from counters_collection where counter_name = ?",
+                         (counter,)).fetchall()
+        out = {}
+        for name, v in rows:
+            out.setdefault(name, []).append(float(v) * 1024.0)
+        return out
+
+    f, w = per_kernel(fetch_db, "FETCH_SIZE"), per_kernel(write_db, "WRITE_SIZE")
+    copy = [k for k in f if "copyBuffer" in k]
+    gemm = [k for k in f if "k_gemm_bt<3>" in k]
+    if not copy or not gemm:
+        sys.exit("bench.py: the databases hold no copy probe or no gate_up product")
+    big = lambda v: max(v)                                   # the probe is the largest copy
+    kc = max(copy, key=lambda k: big(f[k]))
+    rf = big(f[kc]) / PROBE_BYTES
+    wf = big(w[kc]) / PROBE_BYTES
+    fetch = float(np.median(f[gemm[0]])) / rf
+    write = float(np.median(w[gemm[0]])) / wf
+    algo = 2 * (4096 * 4096 + 24576 * 4096 + 4096 * 12288)
+    rec = {"kernel": "k_gemm_bt<3>: gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights",
+           "bytes_per_launch": round(fetch + write), "fetch_bytes": round(fetch), "write_bytes": round(write),
+           "algorithmic_bytes": algo, "copy_probe_bytes": PROBE_BYTES,
+           "fetch_factor": round(rf, 4), "write_factor": round(wf, 4),
+           "launches": len(f[gemm[0]]),
+           "commands": ["rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o p -- python3 bench.py --steps 1 "
+                        "--warmup 0 --no-cpu --copy-probe %d" % (PROBE_BYTES >> 20),
+                        "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o p -- python3 bench.py --steps 1 "
+                        "--warmup 0 --no-cpu --copy-probe %d" % (PROBE_BYTES >> 20),
+                        "python3 bench.py --traffic-from gpurun_out/pmc_fetch/p_results.db "
+                        "gpurun_out/pmc_write/p_results.db"]}
+    with open(TRAFFIC_FILE, "w") as fh:
+        json.dump(rec, fh, indent=1)
+    print(json.dumps(rec))
 
 
 def main():
@@ -87,7 +136,14 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="copy MIB MiB device to device after the set-up (the traffic counters' calibration)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
+                    help="turn two rocprofv3 --pmc databases of a --copy-probe run into " + TRAFFIC_FILE)
     a = ap.parse_args()
+    if a.traffic_from:
+        traffic_from(*a.traffic_from)
+        return
     if a.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus %d is not supported (the step shards over image "
               "rows across GPUs only by design, see DESIGN.md)" % a.gpus, file=sys.stderr)
@@ -104,6 +160,13 @@ def main():
     w_bytes, _ = d.memory()
     print("bench: synthetic 7B Q8_0 DiT on the device in %.1f s, block matrices expanded to resident bf16 in %.1f s "
           "(%.1f GB of weights)" % (t1 - t0, time.perf_counter() - t1, w_bytes / 1e9), file=sys.stderr, flush=True)
+    if a.copy_probe:
+        src = X.DevBuf(ctx, (a.copy_probe << 20,), np.uint8)
+        dst = X.DevBuf(ctx, (a.copy_probe << 20,), np.uint8)
+        X.call("exn_copy", ctx.h, dst.h, src.h, a.copy_probe << 20)
+        ctx.sync()
+        src.free()
+        dst.free()
     rng = np.random.default_rng(SEED)
     context = X.DevBuf.of(ctx, rng.normal(0, 1, (P, 4096)).astype(np.float32))
     latent = rng.normal(0, 1, (64, H, W)).astype(np.float32)
@@ -177,7 +240,7 @@ def main():
         "uncached_step_ms": round(t_uncached * 1e3, 2), "euler_8_steps_ms": round(t_8 * 1e3, 1),
         "final_latent_finite": finite, "ref_rtx3090_ms_per_step": 1187.5,
         "kernels": kernels,
-        "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, Q8_0 weights",
+        "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights (resident expansion of Q8_0)",
                      "achieved": round(achieved, 1) if achieved else None, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4) if achieved else None, "traffic": traffic,
                      "avg_launch_ms": round(gu_avg, 4)},
