@@ -1100,10 +1100,12 @@ static int ensure_kv(exn_dit* d, int64_t l, int keep_rows) {
         r = EXN_EHIP;
     }
     if (r == EXN_OK && keep_rows > 0 && i < (int)d->kc.size()) {  // carry the kept prompt rows over
+      // V^T's key columns are permuted inside aligned groups of 16 (vt_pos): whole groups move
+      const int64_t vcols = (keep_rows + 15) / 16 * 16;
       if (hipMemcpy2DAsync(kc[(size_t)i], (size_t)(lcap * EXN_HD * 2), d->kc[(size_t)i], (size_t)(d->lcap * EXN_HD * 2),
                            (size_t)(keep_rows * EXN_HD * 2), EXN_H, hipMemcpyDeviceToDevice, s) != hipSuccess ||
           hipMemcpy2DAsync(vt[(size_t)i], (size_t)(lcap * 2), d->vt[(size_t)i], (size_t)(d->lcap * 2),
-                           (size_t)(keep_rows * 2), EXN_H * EXN_HD, hipMemcpyDeviceToDevice, s) != hipSuccess)
+                           (size_t)(vcols * 2), EXN_H * EXN_HD, hipMemcpyDeviceToDevice, s) != hipSuccess)
         r = EXN_EHIP;
     }
   }

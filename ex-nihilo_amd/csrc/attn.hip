@@ -1,42 +1,52 @@
 // attn.hip -- the DiT's joint attention on gfx950's MFMA, flash style: K and
-// V tiles staged in LDS, an online softmax in fp32 (exp2 of scores in log2
-// units), Q, K, V and P in fp16 (the reference's halves), fp32 sums.  The
-// mask is the reference's xa_lim
-// (src/cuda/dit.cu:60-66): sequence row g sees keys 0..lim(g), lim(g) = l-1
-// for image rows (g >= p), b1-1 for a reference picture's rows b0..b1-1, g
-// otherwise (the prompt is causal).  lim never decreases in g, so a query
-// tile's last key is its last row's.  Replaces x_attend_mma
-// (src/cuda/dit.cu:208-336).
+// V^T tiles moved HBM/L2 -> LDS by the LDS DMA path (double-buffered, one
+// barrier a tile), an online softmax in fp32 on scores in log2 units, Q, K, V
+// and P in fp16 (the reference's halves), fp32 sums.  The mask is the
+// reference's xa_lim (src/cuda/dit.cu:60-66): sequence row g sees keys
+// 0..lim(g), lim(g) = l-1 for image rows (g >= p), b1-1 for a reference
+// picture's rows b0..b1-1, g otherwise (the prompt is causal).  lim never
+// decreases in g, so a query tile's last key is its last row's.  Replaces
+// x_attend_mma (src/cuda/dit.cu:208-336).
 //
-// Layouts: Q [32 heads][n][128] (query t = sequence row q0 + t),
-// K [32][lcap][128], V^T [32][128][lcap] (keys contiguous), all fp16;
-// out [n][4096] bf16 (the next product's input).
+// Layouts: Q [32 heads][n][128] (query t = sequence row q0 + t), pre-scaled
+// so that scores come out in log2 units; K [32][lcap][128]; V^T [32][128][lcap]
+// with the keys of every aligned group of 16 stored in the order of
+// vt_pos() below; all fp16.  out [n][4096] bf16 (the next product's input).
 //
 // The products are taken transposed so that no register shuffles are needed:
 // S^T = K Q^T puts one query in a lane's column (its 32 of a 64-key tile's
 // scores in its registers, the other 32 in lane ^ 32), and O^T += V^T P^T
-// takes that lane's P values straight as the B operand -- the contraction
-// runs over the keys in the order the accumulator holds them, and V^T's A
-// operand is read from LDS in the same order.
+// takes that lane's P values straight as the B operand.  The MFMA's k-slot
+// 8*hi + j of a 16-key step u holds key 16u + 8(j/4) + 4hi + j%4 of the
+// accumulator layout; V^T is stored so that those 8 keys are 16 contiguous
+// bytes.
+//
+// Occupancy: at most 128 VGPRs + 128 AGPRs a lane and 64 KB of LDS a
+// workgroup, so two workgroups share a CU and each SIMD interleaves one
+// wave's softmax with another's MFMAs.  The running max moves only when a
+// row's tile max exceeds it by more than 2^8 (P then stays <= 256, exact in
+// fp16 to its 11 bits), so the O rescale is rare.
 #include "exn_common.h"
 
 namespace exn {
 
 #define AQ 128          // queries a workgroup (32 a wave)
 #define AK 64           // keys a tile
-#define KS (128 + 8)    // LDS stride of a K row (fp16 values)
-#define VS (AK + 8)     // LDS stride of a V^T row (fp16 values)
+#define MAX_SLACK 8.f   // log2 units the running max may lag the true max by
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ int xa_lim(int g, int p, int l, int b0, int b1) {
   return g >= p ? l - 1 : (g >= b0 && g < b1 ? b1 - 1 : g);
 }
 
 // grid (ceil(n/128), 32 heads), block 256
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vt,
          uint16_t* __restrict__ O, int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
-  __shared__ __align__(16) uint16_t ks[AK * KS];
-  __shared__ __align__(16) uint16_t vs[128 * VS];
+  // stage s: K tile (64 keys x 256 B) at s*32 KB, V^T tile (128 dims x 128 B) at s*32 KB + 16 KB.
+  // K rows: 16-byte chunk c stored at c ^ (row % 16); V^T rows: chunk c at c ^ ((row / 2) % 8).
+  __shared__ __align__(1024) uint8_t smem[2 * 32768];
   const int h = blockIdx.y, t0 = blockIdx.x * AQ;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hi = lane >> 5, lo = lane & 31;
   const int tq = t0 + wave * 32 + lo;
@@ -52,26 +62,45 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
   const int lim = xa_lim(q0 + tqc, p, l, b0, b1);
   const int last = xa_lim(q0 + min(n, t0 + AQ) - 1, p, l, b0, b1);
   const int minlim = xa_lim(q0 + t0, p, l, b0, b1);
+  const int tiles = last / AK + 1;
+
+  const uint16_t* kbase = Kc + (int64_t)h * lcap * 128;
+  const uint16_t* vbase = Vt + (int64_t)h * 128 * lcap;
+  // DMA: round i of wave w moves K rows (4i + w)*4 .. +3 (lane: row +l/16, LDS chunk l%16)
+  // and V^T rows (4i + w)*8 .. +7 (lane: row +l/8, LDS chunk l%8)
+  auto dma = [&](int t) {
+    uint8_t* ks = smem + (t & 1) * 32768;
+    uint8_t* vs = ks + 16384;
+    const int k0 = t * AK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kr = (4 * i + wave) * 4 + (lane >> 4);
+      const int kc = (lane & 15) ^ (kr & 15);
+      __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)(k0 + kr) * 128 + 8 * kc),
+                                       (lds_void*)(ks + (4 * i + wave) * 1024), 16, 0, 0);
+      const int vr = (4 * i + wave) * 8 + (lane >> 3);
+      const int vc = (lane & 7) ^ ((vr >> 1) & 7);
+      __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)vr * lcap + k0 + 8 * vc),
+                                       (lds_void*)(vs + (4 * i + wave) * 1024), 16, 0, 0);
+    }
+  };
 
   f32x16 o[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) o[d] = f32x16{};
   float mrun = -INFINITY, lrun = 0.f;
 
-  const uint16_t* kbase = Kc + (int64_t)h * lcap * 128;
-  const uint16_t* vbase = Vt + (int64_t)h * 128 * lcap;
-
-  for (int k0 = 0; k0 <= last; k0 += AK) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int kr = c >> 4, k8 = (c & 15) * 8;
-      *(u32x4*)(ks + kr * KS + k8) = *(const u32x4*)(kbase + (int64_t)(k0 + kr) * 128 + k8);
-      const int vr = c >> 3, v8 = (c & 7) * 8;
-      *(u32x4*)(vs + vr * VS + v8) = *(const u32x4*)(vbase + (int64_t)vr * lcap + k0 + v8);
-    }
-    __syncthreads();
+  dma(0);
+  for (int t = 0; t < tiles; ++t) {
+    // tile t has landed for every wave, and every wave is done with tile t-1's stage
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + 1 < tiles) dma(t + 1);
+    const uint8_t* ks = smem + (t & 1) * 32768;
+    const uint8_t* vs = ks + 16384;
+    const int k0 = t * AK;
 
     // S^T: two 32-key blocks x this wave's 32 queries
     f32x16 s[2] = {f32x16{}, f32x16{}};
@@ -79,7 +108,8 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
     for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        const f16x8 a = *(const f16x8*)(ks + (32 * b + lo) * KS + 16 * kk + 8 * hi);
+        const int row = 32 * b + lo;
+        const f16x8 a = *(const f16x8*)(ks + row * 256 + (((2 * kk + hi) ^ (row & 15)) << 4));
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[b], 0, 0, 0);
       }
     }
@@ -98,31 +128,33 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
           if (key > lim) s[b][r] = -INFINITY;
         }
     }
-    float mx = s[0][0];
+    float mx = fmaxf(s[0][0], s[1][0]);
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(mrun, mx);
-    const float alpha = exp2f(mrun - mnew);
+    const bool grow = mx > mrun + MAX_SLACK;   // -inf + 8 = -inf: the first tile always grows
+    if (__ballot(grow)) {
+      const float mnew = grow ? mx : mrun;
+      const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+      lrun *= alpha;
+      mrun = mnew;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+    }
     float ls = 0.f;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = exp2f(s[b][r] - mnew);
+        const float e = __builtin_amdgcn_exp2f(s[b][r] - mrun);
         s[b][r] = e;
         ls += e;
       }
-    lrun = lrun * alpha + ls;
-    mrun = mnew;
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+    lrun += ls;
 
-    // O^T += V^T P^T over 4 steps of 16 keys; k-slot (hi, j) is key 16u + 8(j/4) + 4hi + j%4 of block b
+    // O^T += V^T P^T over 4 steps of 16 keys
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -132,11 +164,11 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
         const uint32_t p2 = pack_f16x2(s[b][8 * u + 4], s[b][8 * u + 5]);
         const uint32_t p3 = pack_f16x2(s[b][8 * u + 6], s[b][8 * u + 7]);
         const f16x8 pb = __builtin_bit_cast(f16x8, u32x4{p0, p1, p2, p3});
+        const int chunk = 4 * b + 2 * u + hi;   // this lane's 8 keys of the step
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          const uint16_t* vp = vs + (32 * d + lo) * VS + 32 * b + 16 * u + 4 * hi;
-          const u32x2 x0 = *(const u32x2*)vp, x1 = *(const u32x2*)(vp + 8);
-          const f16x8 a = __builtin_bit_cast(f16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
+          const int row = 32 * d + lo;
+          const f16x8 a = *(const f16x8*)(vs + row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4));
           o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[d], 0, 0, 0);
         }
       }
@@ -160,6 +192,7 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out, int n,
                   int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
   if (n <= 0) return hipSuccess;
+  // the DMA reads whole 64-key tiles: keys up to roundup(l, 64) - 1 must lie inside lcap
   if (lcap % AK || l > lcap || l <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attend, dim3((unsigned)((n + AQ - 1) / AQ), 32), dim3(256), 0, s, q, k, vt, out, n, q0, p, l,
                      lcap, b0, b1, scale);

@@ -227,7 +227,8 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
   const int tok = tid & 63;
   const int64_t t = t0 + tok;
   if (t < n) {
-    for (int d = tid >> 6; d < 128; d += 4) vt[((int64_t)h * 128 + d) * lcap + row0 + t] = tile[tok][d];
+    const int64_t col = vt_pos(row0 + t);
+    for (int d = tid >> 6; d < 128; d += 4) vt[((int64_t)h * 128 + d) * lcap + col] = tile[tok][d];
   }
 }
 

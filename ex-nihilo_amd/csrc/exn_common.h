@@ -92,6 +92,11 @@ void set_error(const char* fmt, ...);
 
 namespace exn {
 
+// V^T's column of key k: within every aligned group of 16 keys, bits 2 and 3 of the
+// index swapped.  The attention's P V^T product then finds the 8 keys a lane feeds
+// one MFMA step (16u + 8(j/4) + 4hi + j%4, j = 0..7) in 16 contiguous bytes.
+__host__ __device__ inline int64_t vt_pos(int64_t k) { return k ^ ((((k >> 2) ^ (k >> 3)) & 1) * 12); }
+
 enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_GATE_ADD = 2, EPI_SWIGLU = 3, EPI_GELU_BF16 = 4, EPI_F16 = 5 };
 
 struct EpiArgs {

@@ -128,13 +128,15 @@ int exn_silu(exn_ctx* ctx, int64_t count, float* x);
  * product: QKV fp16 rows of 3 x 4096 for tokens 0..n-1 = sequence rows ROW0..;
  * CS 128 floats a sequence row (cos, sin of 64 pairs).  Writes, fp16, Q [32][n][128]
  * scaled by log2(e)/sqrt(128), K into [32][LCAP][128] rows ROW0.., V transposed
- * into [32][128][LCAP] columns ROW0.. */
+ * into [32][128][LCAP]: key k at column k with bits 2 and 3 swapped (a permutation
+ * inside every aligned 16 keys, the order exn_attend's P V product reads them in) */
 int exn_qkv_prep(exn_ctx* ctx, const uint16_t* qkv, int64_t n, const float* wq, const float* wk, const float* cs,
                  uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap);
 /* x_attend_mma (src/cuda/dit.cu:208-336) with xa_lim's mask (:60-66): OUT [n][4096]
  * bf16 for queries = sequence rows Q0..Q0+n-1 over keys 0..l-1; Q, K, V^T fp16 in the
  * layouts exn_qkv_prep writes.  SCALE multiplies the scores, which are in log2
- * units (1 for exn_qkv_prep's Q).  LCAP % 64 == 0, V^T's columns l..LCAP-1 finite. */
+ * units (1 for exn_qkv_prep's Q).  LCAP % 64 == 0; K's rows and V^T's columns of
+ * keys l..roundup(l, 64)-1 finite (they are read, and masked). */
 int exn_attend(exn_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out, int n, int q0,
                int p, int l, int64_t lcap, int b0, int b1, float scale);
 /* the Euler update of generate's loop (src/generate.lisp:133-135): Z += DS * V */

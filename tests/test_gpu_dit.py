@@ -105,6 +105,11 @@ def test_prefix_cache(ctx):
     X.dit_release(d)
     v7 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.5, prefix_key="a")          # released: recomputed
     assert xo.rel_l2(v7, v4) < 1e-6
+    # a larger image over the kept prompt: the K/V arrays grow and carry the 20 prompt rows over
+    _, big = xo.synth_inputs(3, 20, 24, 24)
+    v8 = X.dit_velocity(d, ctxa, 20, big, 24, 24, 0.5, prefix_key="a")        # cached, 596 keys
+    v9 = X.dit_velocity(d, ctxa, 20, big, 24, 24, 0.5)
+    assert xo.rel_l2(v8, v9) < 1e-5
     d.destroy()
 
 

@@ -322,8 +322,15 @@ def test_qkv_prep(ctx):
     gotk = from_f16(gk[:, row0:row0 + n]).transpose(1, 0, 2)
     assert np.abs(gotq - wq).max() / np.abs(wq).max() < 2e-3
     assert np.abs(gotk - wk).max() / np.abs(wk).max() < 2e-3
-    gotv = from_f16(gvt[:, :, row0:row0 + n]).transpose(2, 0, 1)
+    gotv = from_f16(gvt[:, :, vt_pos(np.arange(row0, row0 + n))]).transpose(2, 0, 1)
     assert (gotv == wv).all()                                   # v only moves: bit-exact
+    assert sorted(vt_pos(np.arange(lcap))) == list(range(lcap))  # a permutation inside each 16 keys
+
+
+def vt_pos(k):
+    """V^T's column of key k (exn_qkv_prep's layout): bits 2 and 3 swapped."""
+    k = np.asarray(k)
+    return k ^ ((((k >> 2) ^ (k >> 3)) & 1) * 12)
 
 
 def _attend_case(ctx, n, q0, p, l, b0, b1, seed, heads_checked=(0, 7, 31)):
@@ -338,7 +345,7 @@ def _attend_case(ctx, n, q0, p, l, b0, b1, seed, heads_checked=(0, 7, 31)):
     kh = np.zeros((32, lcap, 128), np.uint16)
     kh[:, :l] = kb.transpose(1, 0, 2)
     vth = np.zeros((32, 128, lcap), np.uint16)
-    vth[:, :, :l] = vb.transpose(1, 2, 0)
+    vth[:, :, vt_pos(np.arange(l))] = vb.transpose(1, 2, 0)
     out = X.DevBuf(ctx, (n, 4096), np.uint16)
     X.call("exn_attend", ctx.h, dev(ctx, qh).h, dev(ctx, kh).h, dev(ctx, vth).h, out.h, n, q0, p, l, lcap, b0, b1,
            scale * math.log2(math.e))
