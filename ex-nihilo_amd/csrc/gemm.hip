@@ -263,6 +263,75 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ int chunk_swz(int r) { return (r >> 1) & 7; }
 
+// The epilogue through LDS (free once the main loop is done): a wave's 128 x 64
+// accumulators go out 32 rows at a time into its own 32 x 72-float LDS block (rows
+// 288 bytes apart: the two lane halves' rows, 4 apart, fall 32 banks apart), and come
+// back as 4 consecutive columns a lane, so every global access is 16 bytes (8 for
+// bf16/fp16) and a wave's instruction covers whole rows.  Needs N % 4 == 0, LDY % 4 == 0.
+template <int EPI, int MI, int NI>
+__device__ __forceinline__ void epilogue_lds(const f32x16 (&acc)[MI][NI], float* stage, int64_t wrow, int64_t wcol,
+                                             int lane, int64_t M, int64_t N, const EpiArgs& ea) {
+  constexpr int LS = 72;
+  const int lo = lane & 31, hi = lane >> 5;
+  // this lane's 4 columns (SwiGLU: 4 output columns of 8 lanes a row; others 16 lanes a row)
+  constexpr int LPR = EPI == EPI_SWIGLU ? 8 : 16;
+  const int c4 = (lane % LPR) * 4;
+  f32x4 g0 = {0.f, 0.f, 0.f, 0.f}, g1 = g0;
+  if constexpr (EPI == EPI_GATE_ADD) {
+    const int64_t n = wcol + c4;
+    if (n < N) {
+      const f32x4 a = *(const f32x4*)(ea.gate + n), b = *(const f32x4*)(ea.gate + ea.mstride + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        g0[e] = tanh_f(a[e]);
+        g1[e] = tanh_f(b[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) stage[(8 * (r / 4) + 4 * hi + (r % 4)) * LS + 32 * j + lo] = acc[i][j][r];
+#pragma unroll
+    for (int it = 0; it < 32 * LPR / 64; ++it) {
+      const int row = it * (64 / LPR) + lane / LPR;
+      const int64_t m = wrow + 32 * i + row;
+      if (m >= M) continue;
+      const f32x4 v = *(const f32x4*)(stage + row * LS + c4);
+      if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t col = wcol / 2 + c4;   // output column: gate at c4, up at 32 + c4 of the LDS row
+        if (2 * (col - c4) >= N) continue;
+        const f32x4 u = *(const f32x4*)(stage + row * LS + 32 + c4);
+        uint16_t* y = (uint16_t*)ea.y + m * ea.ldy + col;
+        *(u32x2*)y = u32x2{pack_bf16x2(silu_f(v[0]) * u[0], silu_f(v[1]) * u[1]),
+                           pack_bf16x2(silu_f(v[2]) * u[2], silu_f(v[3]) * u[3])};
+      } else {
+        const int64_t n = wcol + c4;
+        if (n >= N) continue;
+        if constexpr (EPI == EPI_F32) {
+          *(f32x4*)((float*)ea.y + m * ea.ldy + n) = v;
+        } else if constexpr (EPI == EPI_BF16) {
+          *(u32x2*)((uint16_t*)ea.y + m * ea.ldy + n) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        } else if constexpr (EPI == EPI_F16) {
+          *(u32x2*)((uint16_t*)ea.y + m * ea.ldy + n) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+        } else if constexpr (EPI == EPI_GELU_BF16) {
+          *(u32x2*)((uint16_t*)ea.y + m * ea.ldy + n) =
+              u32x2{pack_bf16x2(gelu_tanh_f(v[0]), gelu_tanh_f(v[1])), pack_bf16x2(gelu_tanh_f(v[2]), gelu_tanh_f(v[3]))};
+        } else if constexpr (EPI == EPI_GATE_ADD) {
+          const f32x4 g = (ea.n0 + m < ea.p) ? g1 : g0;
+          f32x4* x = (f32x4*)(ea.resid + m * ea.ldy + n);
+          f32x4 xv = *x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xv[e] = xv[e] + g[e] * v[e];
+          *x = xv;
+        }
+      }
+    }
+  }
+}
+
 template <int EPI>
 __global__ void __launch_bounds__(512)
 k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB, int64_t M, int64_t N,
@@ -350,7 +419,8 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); SGB(0x020, 2); }
     SGB(0x008, NMF - NRD);
   }
-  epilogue<EPI, MI, NI>(acc, m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
+  // every wave is past its last LDS read (the last step's barrier) and no DMA is in flight
+  epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * 72), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
 template <int EPI>
@@ -372,7 +442,10 @@ static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
                       int64_t K, Epi epi, const EpiArgs& ea) {
   // the DMA path moves 16-byte chunks: rows of X and W must start 16-byte aligned
-  const bool dma_ok = K % 64 == 0 && lda % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0;
+  // and the epilogue stores 4 columns at once: N, the output's row stride and base aligned to 4 values
+  const bool dma_ok = K % 64 == 0 && lda % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+                      N % 4 == 0 && ea.ldy % 4 == 0 && ((uintptr_t)ea.y & 15) == 0 && ((uintptr_t)ea.resid & 15) == 0 &&
+                      ((uintptr_t)ea.gate & 15) == 0 && ea.mstride % 4 == 0;
   if (!dma_ok) return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
   switch (epi) {
     case EPI_F32: return launch_bt<EPI_F32>(s, x, lda, w, M, N, K, ea);
