@@ -21,12 +21,17 @@
 // accumulator layout; V^T is stored so that those 8 keys are 16 contiguous
 // bytes.
 //
-// Occupancy: at most 128 VGPRs + 128 AGPRs a lane and 64 KB of LDS a
-// workgroup, so two workgroups share a CU and each SIMD interleaves one
-// wave's softmax with another's MFMAs.  The running max moves only when a
-// row's tile max exceeds it by more than 2^8 (P then stays <= 256, exact in
-// fp16 to its 11 bits), so the O rescale is rare.
+// Occupancy: at most 256 registers a lane and 64 KB of LDS a workgroup, so two
+// workgroups share a CU and each SIMD interleaves one wave's softmax with
+// another's MFMAs.  The running max moves only when a row's tile max exceeds
+// it by more than 2^8 (P then stays <= 256, exact in fp16 to its 11 bits), so
+// the O rescale is rare; the S product starts from -max, so the common tile
+// needs no subtraction before exp2, and the row sums come from v_dot2 on the
+// packed fp16 P.  The tile body is specialised per LDS stage, so every
+// fragment read is a per-lane base plus an immediate offset.
 #include "exn_common.h"
+
+#include <type_traits>
 
 namespace exn {
 
@@ -85,39 +90,54 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
     }
   };
 
+  // per-lane LDS offsets: K row 32b + lo, chunk (2kk + hi) ^ (lo % 16); V^T row 32d + lo,
+  // chunk (4b + 2u + hi) ^ ((lo / 2) % 8).  Stage, b and d are immediate offsets.
+  int kofs[8], vofs[4];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) kofs[kk] = lo * 256 + (((2 * kk + hi) ^ (lo & 15)) << 4);
+#pragma unroll
+  for (int bu = 0; bu < 4; ++bu) vofs[bu] = 16384 + lo * 128 + (((2 * bu + hi) ^ ((lo >> 1) & 7)) << 4);
+
   f32x16 o[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) o[d] = f32x16{};
-  float mrun = -INFINITY, lrun = 0.f;
+  // mrun: the reference the scores are taken relative to (the row's running max, lagging
+  // it by at most MAX_SLACK); the S product starts from -mrun so its output is already
+  // relative (exact scale 1 only; another scale multiplies first and subtracts after)
+  float mrun = 0.f, lrun = 0.f;
+  const bool unit = scale == 1.f;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 ones = {(_Float16)1.f, (_Float16)1.f};
 
-  dma(0);
-  for (int t = 0; t < tiles; ++t) {
+  auto tile = [&](auto stage_c, int t) {
+    constexpr int ST = decltype(stage_c)::value;
     // tile t has landed for every wave, and every wave is done with tile t-1's stage
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // vmcnt(0) lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (t + 1 < tiles) dma(t + 1);
-    const uint8_t* ks = smem + (t & 1) * 32768;
-    const uint8_t* vs = ks + 16384;
     const int k0 = t * AK;
+    const float mref = t == 0 ? 0.f : mrun;
+    const float c0 = unit ? -mref : 0.f;
 
-    // S^T: two 32-key blocks x this wave's 32 queries
-    f32x16 s[2] = {f32x16{}, f32x16{}};
+    // S^T - mref: two 32-key blocks x this wave's 32 queries
+    f32x16 s[2];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int b = 0; b < 2; ++b) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int row = 32 * b + lo;
-        const f16x8 a = *(const f16x8*)(ks + row * 256 + (((2 * kk + hi) ^ (row & 15)) << 4));
+      for (int r = 0; r < 16; ++r) s[b][r] = c0;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const f16x8 a = *(const f16x8*)(smem + kofs[kk] + (ST * 32768 + b * 8192));
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[b], 0, 0, 0);
       }
     }
-    if (scale != 1.f) {
+    if (!unit) {
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[b][r] *= scale;
+        for (int r = 0; r < 16; ++r) s[b][r] = s[b][r] * scale - mref;
     }
     if (k0 + AK - 1 > minlim) {   // some key of this tile is hidden from some query
 #pragma unroll
@@ -128,50 +148,56 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
           if (key > lim) s[b][r] = -INFINITY;
         }
     }
-    float mx = fmaxf(s[0][0], s[1][0]);
+    float mx = fmaxf(s[0][0], s[0][1]);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+    for (int r = 2; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[0][r]), s[0][r + 1]);
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[1][r]), s[1][r + 1]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const bool grow = mx > mrun + MAX_SLACK;   // -inf + 8 = -inf: the first tile always grows
-    if (__ballot(grow)) {
-      const float mnew = grow ? mx : mrun;
-      const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-      lrun *= alpha;
-      mrun = mnew;
+    // the first tile always sets the reference (its key 0 is visible to every row)
+    const bool move = t == 0 || mx > MAX_SLACK;
+    if (__ballot(move)) {
+      const float shift = move ? mx : 0.f;
+      if (t > 0) {
+        const float alpha = __builtin_amdgcn_exp2f(-shift);
+        lrun *= alpha;
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
+        for (int d = 0; d < 4; ++d)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
-    }
-    float ls = 0.f;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = __builtin_amdgcn_exp2f(s[b][r] - mrun);
-        s[b][r] = e;
-        ls += e;
+          for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
       }
-    lrun += ls;
+      mrun = mref + shift;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[b][r] -= shift;
+    }
 
-    // O^T += V^T P^T over 4 steps of 16 keys
+    // P = exp2(S^T - mrun) in fp16; O^T += V^T P^T over 4 steps of 16 keys; the row sum
+    // adds the fp16 P values the product uses
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const uint32_t p0 = pack_f16x2(s[b][8 * u + 0], s[b][8 * u + 1]);
-        const uint32_t p1 = pack_f16x2(s[b][8 * u + 2], s[b][8 * u + 3]);
-        const uint32_t p2 = pack_f16x2(s[b][8 * u + 4], s[b][8 * u + 5]);
-        const uint32_t p3 = pack_f16x2(s[b][8 * u + 6], s[b][8 * u + 7]);
-        const f16x8 pb = __builtin_bit_cast(f16x8, u32x4{p0, p1, p2, p3});
-        const int chunk = 4 * b + 2 * u + hi;   // this lane's 8 keys of the step
+        uint32_t pk[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pk[e] = pack_f16x2(__builtin_amdgcn_exp2f(s[b][8 * u + 2 * e]), __builtin_amdgcn_exp2f(s[b][8 * u + 2 * e + 1]));
+          lrun = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[e]), ones, lrun, false);
+        }
+        const f16x8 pb = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          const int row = 32 * d + lo;
-          const f16x8 a = *(const f16x8*)(vs + row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4));
+          const f16x8 a = *(const f16x8*)(smem + vofs[2 * b + u] + (ST * 32768 + d * 4096));
           o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[d], 0, 0, 0);
         }
       }
+  };
+
+  dma(0);
+  for (int t = 0; t < tiles; t += 2) {
+    tile(std::integral_constant<int, 0>(), t);
+    if (t + 1 < tiles) tile(std::integral_constant<int, 1>(), t + 1);
   }
 
   const float ltot = lrun + __shfl_xor(lrun, 32, 64);
