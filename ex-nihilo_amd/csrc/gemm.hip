@@ -244,11 +244,11 @@ hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* 
 
 // --- bf16 weights: the pipelined kernel ----------------------------------------------
 // 256 x 256 tiles, 8 waves of 128 x 64, BK = 64.  Both tiles go HBM/L2 -> LDS by the
-// LDS DMA path (global_load_lds_dwordx4: no VGPR staging, no ds_write), two stages.
+// LDS DMA path (buffer_load_dwordx4 ... lds: no VGPR staging, no ds_write), two stages.
 // Inside a step the wave's fragment registers are double-buffered: the ds_reads of
-// slice kk+1 are interleaved with the MFMAs of slice kk (sched_group_barrier), and the
-// step's one barrier sits before the last slice, so the next step's DMA and first
-// fragment reads overlap that slice's MFMAs.
+// slice kk+1 are interleaved with the MFMAs of slice kk, and the step's one barrier sits
+// before the last slice, so the DMA of the step after next and the next step's first
+// fragment reads are spread over that slice's MFMAs, one of each an MFMA.
 // LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by (row/2)%8: the
 // fragment reads of 32 rows x 16 bytes are bank-conflict free.
 typedef __attribute__((address_space(3))) void lds_void;
@@ -332,94 +332,96 @@ __device__ __forceinline__ void epilogue_lds(const f32x16 (&acc)[MI][NI], float*
   }
 }
 
+// One 16-byte DMA lane of a tile: the buffer's extent makes rows past the matrix read as zeros.
+__device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
+
 template <int EPI>
 __global__ void __launch_bounds__(512)
 k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB, int64_t M, int64_t N,
           int64_t K, EpiArgs ea) {
   constexpr int NW = 8, WM = 128, WN = 64, MI = WM / 32, NI = WN / 32, ROUNDS = 256 / (NW * 8);
-  constexpr int NMF = MI * NI, NRD = MI + NI;
+  constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = 2 * ROUNDS;
   extern __shared__ __align__(1024) uint8_t smem[];   // 2 stages x (X tile 32 KB | W tile 32 KB)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS bases stay scalar
   const int wm = wave / (256 / WN), wn = wave % (256 / WN);
   const int64_t m0 = (int64_t)blockIdx.y * 256, n0 = (int64_t)blockIdx.x * 256;
   const int KT = (int)(K / 64);
-  // DMA: round i of wave w moves rows (i*8 + w)*8 .. +7, lane l row +l/8, LDS chunk l%8
-  const uint16_t* a_src[ROUNDS];
-  const uint16_t* w_src[ROUNDS];
+  // DMA: round i of wave w moves rows (i*8 + w)*8 .. +7 of a tile, lane l row +l/8, LDS chunk l%8
+  // (global chunk (l%8) ^ swizzle); the k-step is the scalar offset
+  const uint16_t* xbase = X + m0 * lda;
+  const uint16_t* wbase = WB + n0 * K;
+  const uint32_t xext = (uint32_t)((M - m0) * lda * 2), wext = (uint32_t)(max((int64_t)0, N - n0) * K * 2);
+  uint32_t xoff[ROUNDS], woff[ROUNDS];
 #pragma unroll
   for (int i = 0; i < ROUNDS; ++i) {
     const int row = (i * NW + wave) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ chunk_swz(row);
-    a_src[i] = X + min(m0 + row, M - 1) * lda + 8 * c;
-    w_src[i] = WB + min(n0 + row, N - 1) * K + 8 * c;
+    xoff[i] = (uint32_t)((row * lda + 8 * c) * 2);
+    woff[i] = (uint32_t)((row * K + 8 * c) * 2);
   }
-  auto dma = [&](int t) {
-    uint8_t* a = smem + (t & 1) * 65536;
-    uint8_t* b = a + 32768;
-#pragma unroll
-    for (int i = 0; i < ROUNDS; ++i) {
-      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + (int64_t)t * 64), (lds_void*)(a + (i * NW + wave) * 1024),
-                                       16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + (int64_t)t * 64), (lds_void*)(b + (i * NW + wave) * 1024),
-                                       16, 0, 0);
-    }
+  auto dma_part = [&](int t, int stage, int p) {   // part p < ROUNDS: X round p, else W round p - ROUNDS
+    uint8_t* dst = smem + stage * 65536 + (p < ROUNDS ? 0 : 32768) + ((p % ROUNDS) * NW + wave) * 1024;
+    if (p < ROUNDS) tile_dma(xbase, xext, (lds_void*)dst, xoff[p % ROUNDS], t * 128);
+    else tile_dma(wbase, wext, (lds_void*)dst, woff[p % ROUNDS], t * 128);
   };
   const int lo = lane & 31, hi = lane >> 5, fs = chunk_swz(lo);
   const uint8_t* a_rd = smem + (wm * WM + lo) * 128;
   const uint8_t* b_rd = smem + 32768 + (wn * WN + lo) * 128;
   struct Frag {
-    bf16x8 a[MI], b[NI];
+    bf16x8 v[NRD];   // X fragments 0..MI-1, W fragments MI..
   };
-  auto rd = [&](Frag& f, int stage, int kk) {
+  auto rd1 = [&](Frag& f, int stage, int kk, int q) {
     const int off = stage * 65536 + (((2 * kk + hi) ^ fs) << 4);
-#pragma unroll
-    for (int i = 0; i < MI; ++i) f.a[i] = *(const bf16x8*)(a_rd + off + i * 32 * 128);
-#pragma unroll
-    for (int j = 0; j < NI; ++j) f.b[j] = *(const bf16x8*)(b_rd + off + j * 32 * 128);
+    if (q < MI) f.v[q] = *(const bf16x8*)(a_rd + off + q * 32 * 128);
+    else f.v[q] = *(const bf16x8*)(b_rd + off + (q - MI) * 32 * 128);
   };
   f32x16 acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
-  auto mma = [&](const Frag& f) {
+  // A slice of 16 k: NMF MFMAs on F in a fixed order -- after each, one fragment read of
+  // the next slice into G (the first NRD of them) and, on the DMA slice, one DMA part --
+  // with scheduling fences between, so the DMA and the reads never bunch up.
+  auto slice = [&](const Frag& F, Frag& G, int rstage, int rkk, bool dma, int dt, int dstage) {
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int x = 0; x < NMF; ++x) {
+      acc[x / NI][x % NI] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.v[x / NI], F.v[MI + x % NI], acc[x / NI][x % NI], 0, 0, 0);
+      if (x < NRD) rd1(G, rstage, rkk, x);
+      if (dma) {
 #pragma unroll
-      for (int j = 0; j < NI; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+        for (int p = (x * NDMA) / NMF; p < ((x + 1) * NDMA) / NMF; ++p) dma_part(dt, dstage, p);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   Frag F0, F1;
-  dma(0);
+#pragma unroll
+  for (int p = 0; p < NDMA; ++p) dma_part(0, 0, p);
   LDS_VMCNT0_BARRIER();
-  if (KT > 1) dma(1);
-  rd(F0, 0, 0);
+  if (KT > 1) {
+#pragma unroll
+    for (int p = 0; p < NDMA; ++p) dma_part(1, 1, p);
+  }
+#pragma unroll
+  for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
   for (int t = 0; t < KT; ++t) {
     const int cur = t & 1;
-    rd(F1, cur, 1);
-    mma(F0);
-#pragma unroll
-    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); }
-    SGB(0x008, NMF - NRD);
-    rd(F0, cur, 2);
-    mma(F1);
-#pragma unroll
-    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); }
-    SGB(0x008, NMF - NRD);
-    rd(F1, cur, 3);
-    mma(F0);
-#pragma unroll
-    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); }
-    SGB(0x008, NMF - NRD);
+    slice(F0, F1, cur, 1, false, 0, 0);
+    slice(F1, F0, cur, 2, false, 0, 0);
+    slice(F0, F1, cur, 3, false, 0, 0);
     // every wave has its slice-3 fragments and its DMA of step t+1 has landed: stage cur is free
     LDS_VMCNT0_BARRIER();
-    if (t + 2 < KT) dma(t + 2);
-    if (t + 1 < KT) rd(F0, cur ^ 1, 0);
-    mma(F1);
-#pragma unroll
-    for (int g = 0; g < NRD; ++g) { SGB(0x008, 1); SGB(0x100, 1); SGB(0x020, 2); }
-    SGB(0x008, NMF - NRD);
+    // the step after next into stage cur (past the end: the last step again, never read), the
+    // next step's first fragments from the other stage -- no branch, so the order holds
+    slice(F1, F0, cur ^ 1, 0, true, min(t + 2, KT - 1), cur);
   }
-  // every wave is past its last LDS read (the last step's barrier) and no DMA is in flight
+  LDS_VMCNT0_BARRIER();   // the last DMA has landed before the epilogue takes the LDS over
   epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * 72), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
@@ -443,7 +445,9 @@ hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint1
                       int64_t K, Epi epi, const EpiArgs& ea) {
   // the DMA path moves 16-byte chunks: rows of X and W must start 16-byte aligned
   // and the epilogue stores 4 columns at once: N, the output's row stride and base aligned to 4 values
+  // and the buffer extents (bytes from a tile's first row to the matrix's end) fit 31 bits
   const bool dma_ok = K % 64 == 0 && lda % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+                      M * lda < (int64_t)1 << 30 && N * K < (int64_t)1 << 30 &&
                       N % 4 == 0 && ea.ldy % 4 == 0 && ((uintptr_t)ea.y & 15) == 0 && ((uintptr_t)ea.resid & 15) == 0 &&
                       ((uintptr_t)ea.gate & 15) == 0 && ea.mstride % 4 == 0;
   if (!dma_ok) return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
