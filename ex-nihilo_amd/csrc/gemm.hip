@@ -243,12 +243,13 @@ hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* 
 }
 
 // --- bf16 weights: the pipelined kernel ----------------------------------------------
-// 256 x 256 tiles, 8 waves of 128 x 64, BK = 64.  Both tiles go HBM/L2 -> LDS by the
+// 256 x 256 tiles, 8 waves of 128 x 64 (8 x 4 tiles of v_mfma_f32_16x16x32_bf16), BK = 64
+// in two slices of 32.  Both tiles go HBM/L2 -> LDS by the
 // LDS DMA path (buffer_load_dwordx4 ... lds: no VGPR staging, no ds_write), two stages.
 // Inside a step the wave's fragment registers are double-buffered: the ds_reads of
-// slice kk+1 are interleaved with the MFMAs of slice kk, and the step's one barrier sits
-// before the last slice, so the DMA of the step after next and the next step's first
-// fragment reads are spread over that slice's MFMAs, one of each an MFMA.
+// slice 1 are interleaved with the MFMAs of slice 0, and the step's one barrier sits
+// before slice 1, so the DMA of the step after next and the next step's first fragment
+// reads are spread over that slice's MFMAs.
 // LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by (row/2)%8: the
 // fragment reads of 32 rows x 16 bytes are bank-conflict free.
 typedef __attribute__((address_space(3))) void lds_void;
@@ -264,15 +265,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ int chunk_swz(int r) { return (r >> 1) & 7; }
 
 // The epilogue through LDS (free once the main loop is done): a wave's 128 x 64
-// accumulators go out 32 rows at a time into its own 32 x 72-float LDS block (rows
-// 288 bytes apart: the two lane halves' rows, 4 apart, fall 32 banks apart), and come
-// back as 4 consecutive columns a lane, so every global access is 16 bytes (8 for
-// bf16/fp16) and a wave's instruction covers whole rows.  Needs N % 4 == 0, LDY % 4 == 0.
+// accumulators go out 32 rows at a time into its own 32 x 72-float LDS block (rows 288
+// bytes apart), and come back as 4 consecutive columns a lane, so every global access
+// is 16 bytes (8 for bf16/fp16) and a wave's instruction covers whole rows.  Needs
+// N % 4 == 0, LDY % 4 == 0.
 template <int EPI, int MI, int NI>
-__device__ __forceinline__ void epilogue_lds(const f32x16 (&acc)[MI][NI], float* stage, int64_t wrow, int64_t wcol,
+__device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* stage, int64_t wrow, int64_t wcol,
                                              int lane, int64_t M, int64_t N, const EpiArgs& ea) {
   constexpr int LS = 72;
-  const int lo = lane & 31, hi = lane >> 5;
   // this lane's 4 columns (SwiGLU: 4 output columns of 8 lanes a row; others 16 lanes a row)
   constexpr int LPR = EPI == EPI_SWIGLU ? 8 : 16;
   const int c4 = (lane % LPR) * 4;
@@ -288,16 +288,20 @@ __device__ __forceinline__ void epilogue_lds(const f32x16 (&acc)[MI][NI], float*
       }
     }
   }
+  // accumulators of v_mfma_f32_16x16x32: lane l holds column l%16, rows 4*(l/16) + r
+  const int c16 = lane & 15, q4 = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < MI; ++i) {
+  for (int i2 = 0; i2 < MI / 2; ++i2) {
 #pragma unroll
-    for (int j = 0; j < NI; ++j)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) stage[(8 * (r / 4) + 4 * hi + (r % 4)) * LS + 32 * j + lo] = acc[i][j][r];
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) stage[(16 * h + 4 * q4 + r) * LS + 16 * j + c16] = acc[2 * i2 + h][j][r];
 #pragma unroll
     for (int it = 0; it < 32 * LPR / 64; ++it) {
       const int row = it * (64 / LPR) + lane / LPR;
-      const int64_t m = wrow + 32 * i + row;
+      const int64_t m = wrow + 32 * i2 + row;
       if (m >= M) continue;
       const f32x4 v = *(const f32x4*)(stage + row * LS + c4);
       if constexpr (EPI == EPI_SWIGLU) {
@@ -342,7 +346,7 @@ template <int EPI>
 __global__ void __launch_bounds__(512)
 k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB, int64_t M, int64_t N,
           int64_t K, EpiArgs ea) {
-  constexpr int NW = 8, WM = 128, WN = 64, MI = WM / 32, NI = WN / 32, ROUNDS = 256 / (NW * 8);
+  constexpr int NW = 8, WM = 128, WN = 64, MI = WM / 16, NI = WN / 16, ROUNDS = 256 / (NW * 8);
   constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = 2 * ROUNDS;
   extern __shared__ __align__(1024) uint8_t smem[];   // 2 stages x (X tile 32 KB | W tile 32 KB)
   const int tid = threadIdx.x, lane = tid & 63;
@@ -368,30 +372,31 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     if (p < ROUNDS) tile_dma(xbase, xext, (lds_void*)dst, xoff[p % ROUNDS], t * 128);
     else tile_dma(wbase, wext, (lds_void*)dst, woff[p % ROUNDS], t * 128);
   };
-  const int lo = lane & 31, hi = lane >> 5, fs = chunk_swz(lo);
+  // v_mfma_f32_16x16x32_bf16 operands: lane l holds row l%16, k = 8*(l/16) .. +7 of a slice of 32
+  const int lo = lane & 15, q4 = lane >> 4, fs = chunk_swz(lo);
   const uint8_t* a_rd = smem + (wm * WM + lo) * 128;
   const uint8_t* b_rd = smem + 32768 + (wn * WN + lo) * 128;
   struct Frag {
     bf16x8 v[NRD];   // X fragments 0..MI-1, W fragments MI..
   };
   auto rd1 = [&](Frag& f, int stage, int kk, int q) {
-    const int off = stage * 65536 + (((2 * kk + hi) ^ fs) << 4);
-    if (q < MI) f.v[q] = *(const bf16x8*)(a_rd + off + q * 32 * 128);
-    else f.v[q] = *(const bf16x8*)(b_rd + off + (q - MI) * 32 * 128);
+    const int off = stage * 65536 + (((4 * kk + q4) ^ fs) << 4);
+    if (q < MI) f.v[q] = *(const bf16x8*)(a_rd + off + q * 16 * 128);
+    else f.v[q] = *(const bf16x8*)(b_rd + off + (q - MI) * 16 * 128);
   };
-  f32x16 acc[MI][NI];
+  f32x4 acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
-  // A slice of 16 k: NMF MFMAs on F in a fixed order -- after each, one fragment read of
+    for (int j = 0; j < NI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // A slice of 32 k: NMF MFMAs on F in a fixed order -- after each, one fragment read of
   // the next slice into G (the first NRD of them) and, on the DMA slice, one DMA part --
   // with scheduling fences between, so the DMA and the reads never bunch up.
   auto slice = [&](const Frag& F, Frag& G, int rstage, int rkk, bool dma, int dt, int dstage) {
 #pragma unroll
     for (int x = 0; x < NMF; ++x) {
       acc[x / NI][x % NI] =
-          __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.v[x / NI], F.v[MI + x % NI], acc[x / NI][x % NI], 0, 0, 0);
+          __builtin_amdgcn_mfma_f32_16x16x32_bf16(F.v[x / NI], F.v[MI + x % NI], acc[x / NI][x % NI], 0, 0, 0);
       if (x < NRD) rd1(G, rstage, rkk, x);
       if (dma) {
 #pragma unroll
@@ -413,9 +418,7 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   for (int t = 0; t < KT; ++t) {
     const int cur = t & 1;
     slice(F0, F1, cur, 1, false, 0, 0);
-    slice(F1, F0, cur, 2, false, 0, 0);
-    slice(F0, F1, cur, 3, false, 0, 0);
-    // every wave has its slice-3 fragments and its DMA of step t+1 has landed: stage cur is free
+    // every wave has its slice-1 fragments and its DMA of step t+1 has landed: stage cur is free
     LDS_VMCNT0_BARRIER();
     // the step after next into stage cur (past the end: the last step again, never read), the
     // next step's first fragments from the other stage -- no branch, so the order holds
