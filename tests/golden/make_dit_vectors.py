@@ -4,7 +4,8 @@ minutes of CPU).  These are the oracle's outputs (oracle/exn_oracle.py,
 itself pinned against the reference's ref_dit.py vectors), cached:
 
     python tests/golden/make_dit_vectors.py small      # dit_depth32_small.npz
-    python tests/golden/make_dit_vectors.py cfg2       # dit_cfg2_8step.npz (about half an hour)
+    python tests/golden/make_dit_vectors.py cfg2       # dit_cfg2_8step.npz (about 1.5 hours)
+    python tests/golden/make_dit_vectors.py full2      # dit_full_shapes_2blocks.npz (a few minutes)
 
 small: 32 blocks of the real shape, synthetic Q8_0 weights (seed 1), 32 text
 rows, an 8 x 8 latent: the velocity of each of the 8 Turbo steps (the first
@@ -46,9 +47,37 @@ def run(seed, p, h, w, out, half=False):
     print("wrote", out)
 
 
+# the workloads' full shapes, two blocks deep: (seed, text rows, h, w, (a, rh, rw) or None, sigma)
+FULL_CASES = {
+    "cfg2_1024sq": (2, 256, 64, 64, None, 0.978453),
+    "cfg3_1536x1024": (6, 256, 96, 64, None, 0.95418),
+    "cfg4_edit_1024sq": (7, 512, 64, 64, (8, 64, 64), 0.926626),
+}
+
+
+def full_shapes(out):
+    arrays = {}
+    for name, (seed, p, h, w, ref, sigma) in FULL_CASES.items():
+        t0 = time.time()
+        if ref is None:
+            ctx, lat = xo.synth_inputs(seed, p, h, w)
+            oref = None
+        else:
+            a, rh, rw = ref
+            ctx, lat, rl = xo.synth_inputs(seed, p, h, w, ref_hw=(rh, rw))
+            oref = (a, rl)
+        v = xo.forward(xo.SynthWeights(seed, cache_bytes=0), ctx, lat, sigma, ref=oref, layers=2)
+        arrays[name] = v.astype(np.float16)
+        print("%s: |v| %.4f, %.0fs" % (name, float(np.sqrt((v * v).mean())), time.time() - t0), flush=True)
+    np.savez_compressed(os.path.join(HERE, out), **arrays)
+    print("wrote", out)
+
+
 if __name__ == "__main__":
     which = sys.argv[1] if len(sys.argv) > 1 else "small"
     if which == "small":
         run(1, 32, 8, 8, "dit_depth32_small.npz")
     elif which == "cfg2":
         run(2, 256, 64, 64, "dit_cfg2_8step.npz", half=True)
+    elif which == "full2":
+        full_shapes("dit_full_shapes_2blocks.npz")

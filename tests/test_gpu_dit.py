@@ -207,3 +207,38 @@ def test_full_depth_steps_against_oracle(ctx):
     X.call("exn_dit_generate_dev", d.h, cd.h, p, zd.h, h, w, X.ptr(sg), len(sg), 0, None, 0, 0)
     assert xo.rel_l2(zd.get(), z) < 1e-5
     d.destroy()
+
+
+# --- the workloads' full shapes, two blocks deep -------------------------------------------
+
+FULL_CASES = {  # name: (seed, text rows, image h, w, reference picture (a, rh, rw) or None, sigma)
+    "cfg2_1024sq": (2, 256, 64, 64, None, 0.978453),
+    "cfg3_1536x1024": (6, 256, 96, 64, None, 0.95418),
+    "cfg4_edit_1024sq": (7, 512, 64, 64, (8, 64, 64), 0.926626),
+}
+
+
+@pytest.mark.parametrize("case", list(FULL_CASES))
+def test_full_shapes_two_blocks(ctx, case):
+    """Every kernel at a workload's real sizes (4096 or 6144 image rows; 256 text rows, or
+    512 text rows plus a 64 x 64 reference picture = 8704 keys), two blocks deep: the
+    uncached pass and then the cached pass against the oracle's velocity (<= 1e-2; the
+    oracle's results cached in tests/golden/dit_full_shapes_2blocks.npz as float16), and
+    against each other (the kept K/V give the same velocity)."""
+    seed, p, h, w, ref, sigma = FULL_CASES[case]
+    say(case, "p", p, "image", h, "x", w, "ref", ref)
+    want = np.load(os.path.join(GOLDEN, "dit_full_shapes_2blocks.npz"))[case].astype(np.float32)
+    d = model(ctx, 2, seed)
+    if ref is None:
+        ctxa, lat = xo.synth_inputs(seed, p, h, w)
+        refarg = None
+    else:
+        a, rh, rw = ref
+        ctxa, lat, rl = xo.synth_inputs(seed, p, h, w, ref_hw=(rh, rw))
+        refarg = (a, rl, rh, rw)
+    v0 = X.dit_velocity(d, ctxa, p, lat, h, w, sigma, prefix_key="k", ref=refarg)     # uncached, keeps K/V
+    v1 = X.dit_velocity(d, ctxa, p, lat, h, w, sigma, prefix_key="k", ref=refarg)     # cached
+    e0, e1, e01 = xo.rel_l2(v0, want), xo.rel_l2(v1, want), xo.rel_l2(v1, v0)
+    say("velocity rel-L2: uncached %.2e, cached %.2e, cached vs uncached %.2e" % (e0, e1, e01))
+    assert e0 < 1e-2 and e1 < 1e-2 and e01 < 1e-5
+    d.destroy()
