@@ -666,7 +666,7 @@ struct exn_dit {
     hipEvent_t a, b;
     double flops, bytes;
   };
-  bool prof = false;
+  unsigned prof = 0;   // bit per kernel class recorded
   std::vector<Rec> recs;
   std::vector<hipEvent_t> pool;
   size_t pool_used = 0;
@@ -688,7 +688,7 @@ struct ProfScope {
   double flops, bytes;
   hipEvent_t a = nullptr;
   ProfScope(exn_dit* d_, int c, double f, double b) : d(d_), cls(c), flops(f), bytes(b) {
-    if (d->prof && (a = prof_event(d))) (void)hipEventRecord(a, d->ctx->stream);
+    if ((d->prof >> cls & 1u) && (a = prof_event(d))) (void)hipEventRecord(a, d->ctx->stream);
   }
   ~ProfScope() {
     if (!a) return;
@@ -811,7 +811,7 @@ int exn_dit_profile(exn_dit* d, int on) {
     d->recs.clear();
     d->pool_used = 0;
   }
-  d->prof = on != 0;
+  d->prof = on < 0 ? (1u << EXN_PROF_CLASSES) - 1u : (unsigned)on & ((1u << EXN_PROF_CLASSES) - 1u);
   return EXN_OK;
 }
 

@@ -70,6 +70,13 @@ __device__ __forceinline__ float tanh_f(float x) { return tanhf(x); }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
 
+// SiLU for a value rounded to bf16 next: x / (1 + 2^(-x log2 e)) with the hardware exp2
+// and reciprocal (about 1 ulp each); -0 once 2^(-x log2 e) overflows (x below about -88),
+// x itself once it vanishes against 1 (x above about 17).
+__device__ __forceinline__ float silu_bf16out(float x) {
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
 __device__ __forceinline__ float gelu_tanh_f(float v) {
   return 0.5f * v * (1.f + tanh_f(0.7978845608028654f * (v + 0.044715f * v * v * v)));
 }

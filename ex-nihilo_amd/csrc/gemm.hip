@@ -309,8 +309,8 @@ __device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* 
         if (2 * (col - c4) >= N) continue;
         const f32x4 u = *(const f32x4*)(stage + row * LS + 32 + c4);
         uint16_t* y = (uint16_t*)ea.y + m * ea.ldy + col;
-        *(u32x2*)y = u32x2{pack_bf16x2(silu_f(v[0]) * u[0], silu_f(v[1]) * u[1]),
-                           pack_bf16x2(silu_f(v[2]) * u[2], silu_f(v[3]) * u[3])};
+        *(u32x2*)y = u32x2{pack_bf16x2(silu_bf16out(v[0]) * u[0], silu_bf16out(v[1]) * u[1]),
+                           pack_bf16x2(silu_bf16out(v[2]) * u[2], silu_bf16out(v[3]) * u[3])};
       } else {
         const int64_t n = wcol + c4;
         if (n >= N) continue;
@@ -352,7 +352,18 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS bases stay scalar
   const int wm = wave / (256 / WN), wn = wave % (256 / WN);
-  const int64_t m0 = (int64_t)blockIdx.y * 256, n0 = (int64_t)blockIdx.x * 256;
+  // tile order: workgroups go to the 8 XCDs in turn, so XCD x takes the x-th eighth of a
+  // tile order that walks 4 row tiles at a time -- its concurrent tiles share W and X in its L2
+  int bm = blockIdx.y, bn = blockIdx.x;
+  {
+    const int gx = gridDim.x, gy = gridDim.y, G = gx * gy, b = blockIdx.y * gx + blockIdx.x;
+    const int L = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
+    constexpr int GM = 4;
+    const int grp = L / (GM * gx), first = grp * GM, sz = min(gy - first, GM), in = L % (GM * gx);
+    bm = first + in % sz;
+    bn = in / sz;
+  }
+  const int64_t m0 = (int64_t)bm * 256, n0 = (int64_t)bn * 256;
   const int KT = (int)(K / 64);
   // DMA: round i of wave w moves rows (i*8 + w)*8 .. +7 of a tile, lane l row +l/8, LDS chunk l%8
   // (global chunk (l%8) ^ swizzle); the k-step is the scalar offset

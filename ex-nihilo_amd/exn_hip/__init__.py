@@ -290,8 +290,12 @@ class Dit:
 
     PROFILE_CLASSES = ("qkv", "attend", "out", "gate_up", "down", "ln_mod", "qkv_prep", "edge")
 
-    def profile(self, on: bool):
-        call("exn_dit_profile", self.h, 1 if on else 0)
+    def profile(self, on, classes=None):
+        """Record HIP event pairs around the step's launches: all classes, or those named."""
+        mask = 0
+        if on:
+            mask = -1 if classes is None else sum(1 << self.PROFILE_CLASSES.index(c) for c in classes)
+        call("exn_dit_profile", self.h, mask)
 
     def profile_read(self):
         """{class: (ms, launches, flops, bytes)} over the recorded launches."""

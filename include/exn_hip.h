@@ -183,10 +183,11 @@ int exn_dit_generate_dev(exn_dit* d, const float* context, int p, float* z, int 
  * NULL turns it off */
 int exn_dit_trace(exn_dit* d, float* buf, int64_t cap);
 /* EXN_PROFILE's per-kernel GPU time (src/tenant.lisp:53-62), on the context's stream:
- * exn_dit_profile(d, 1) clears and starts recording a HIP event pair around every
- * launch of the step, by kernel class; (d, 0) stops.  exn_dit_profile_read gives a
- * class's summed milliseconds, launches, and algorithmic FLOPs and HBM bytes (one
- * read of each input, one write of each output) over the recorded launches. */
+ * exn_dit_profile(d, ON) clears and starts recording a HIP event pair around every
+ * launch of the step of the kernel classes in the bit mask ON (1 << EXN_PROF_...; -1
+ * for all); (d, 0) stops.  exn_dit_profile_read gives a class's summed milliseconds,
+ * launches, and algorithmic FLOPs and HBM bytes (one read of each input, one write of
+ * each output) over the recorded launches. */
 #define EXN_PROF_QKV 0      /* LayerNormed rows x to_q|to_k|to_v, Q8_0 */
 #define EXN_PROF_ATTEND 1   /* attention */
 #define EXN_PROF_OUT 2      /* attention rows x to_out.0, gated residual fused */
