@@ -1,5 +1,5 @@
 // attn.hip -- the DiT's joint attention on gfx950's MFMA, flash style: K and
-// V^T tiles moved HBM/L2 -> LDS by the LDS DMA path (double-buffered, one
+// V^T tiles moved HBM/L2 -> LDS by buffer loads to LDS (double-buffered, one
 // barrier a tile), an online softmax in fp32 on scores in log2 units, Q, K, V
 // and P in fp16 (the reference's halves), fp32 sums.  The mask is the
 // reference's xa_lim (src/cuda/dit.cu:60-66): sequence row g sees keys
@@ -41,6 +41,12 @@ namespace exn {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// one 16-byte DMA lane of a K or V^T tile
+__device__ __forceinline__ void kv_dma(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
+
 __device__ __forceinline__ int xa_lim(int g, int p, int l, int b0, int b1) {
   return g >= p ? l - 1 : (g >= b0 && g < b1 ? b1 - 1 : g);
 }
@@ -53,7 +59,8 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
   // K rows: 16-byte chunk c stored at c ^ (row % 16); V^T rows: chunk c at c ^ ((row / 2) % 8).
   __shared__ __align__(1024) uint8_t smem[2 * 32768];
   const int h = blockIdx.y, t0 = blockIdx.x * AQ;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hi = lane >> 5, lo = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, hi = lane >> 5, lo = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS bases stay scalar
   const int tq = t0 + wave * 32 + lo;
   const int tqc = min(tq, n - 1);
 
@@ -71,22 +78,26 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 
   const uint16_t* kbase = Kc + (int64_t)h * lcap * 128;
   const uint16_t* vbase = Vt + (int64_t)h * 128 * lcap;
+  const uint32_t kvext = (uint32_t)(lcap * 128 * 2);   // a head's K, and its V^T, in bytes
   // DMA: round i of wave w moves K rows (4i + w)*4 .. +3 (lane: row +l/16, LDS chunk l%16)
-  // and V^T rows (4i + w)*8 .. +7 (lane: row +l/8, LDS chunk l%8)
+  // and V^T rows (4i + w)*8 .. +7 (lane: row +l/8, LDS chunk l%8); the lane's byte offsets
+  // are fixed, the tile's key offset is scalar
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kr = (4 * i + wave) * 4 + (lane >> 4);
+    koff[i] = (uint32_t)((kr * 128 + 8 * ((lane & 15) ^ (kr & 15))) * 2);
+    const int vr = (4 * i + wave) * 8 + (lane >> 3);
+    voff[i] = (uint32_t)((vr * lcap + 8 * ((lane & 7) ^ ((vr >> 1) & 7))) * 2);
+  }
   auto dma = [&](int t) {
     uint8_t* ks = smem + (t & 1) * 32768;
     uint8_t* vs = ks + 16384;
     const int k0 = t * AK;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int kr = (4 * i + wave) * 4 + (lane >> 4);
-      const int kc = (lane & 15) ^ (kr & 15);
-      __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)(k0 + kr) * 128 + 8 * kc),
-                                       (lds_void*)(ks + (4 * i + wave) * 1024), 16, 0, 0);
-      const int vr = (4 * i + wave) * 8 + (lane >> 3);
-      const int vc = (lane & 7) ^ ((vr >> 1) & 7);
-      __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)vr * lcap + k0 + 8 * vc),
-                                       (lds_void*)(vs + (4 * i + wave) * 1024), 16, 0, 0);
+      kv_dma(kbase, kvext, (lds_void*)(ks + (4 * i + wave) * 1024), koff[i], k0 * 256);
+      kv_dma(vbase, kvext, (lds_void*)(vs + (4 * i + wave) * 1024), voff[i], k0 * 2);
     }
   };
 
@@ -219,7 +230,8 @@ hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uin
                   int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
   if (n <= 0) return hipSuccess;
   // the DMA reads whole 64-key tiles: keys up to roundup(l, 64) - 1 must lie inside lcap
-  if (lcap % AK || l > lcap || l <= 0) return hipErrorInvalidValue;
+  // and a head's K (or V^T) is one buffer of lcap * 256 bytes
+  if (lcap % AK || l > lcap || l <= 0 || lcap > (1 << 22)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attend, dim3((unsigned)((n + AQ - 1) / AQ), 32), dim3(256), 0, s, q, k, vt, out, n, q0, p, l,
                      lcap, b0, b1, scale);
   return hipGetLastError();
