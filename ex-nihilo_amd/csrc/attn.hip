@@ -1,7 +1,9 @@
 // attn.hip -- the DiT's joint attention on gfx950's MFMA, flash style: K and
-// V^T tiles moved HBM/L2 -> LDS by buffer loads to LDS (double-buffered, one
-// barrier a tile), an online softmax in fp32 on scores in log2 units, Q, K, V
-// and P in fp16 (the reference's halves), fp32 sums.  The mask is the
+// V^T tiles moved HBM/L2 -> LDS by buffer loads to LDS (two rings of two
+// stages, one barrier a tile), an online softmax in fp32 on scores in log2
+// units, Q, K, V and P in fp16 (the reference's halves), fp32 sums.  Each
+// wave's step is software-pipelined: the S product of the next tile runs on
+// the MFMA pipe while the VALU takes this tile's exp2.  The mask is the
 // reference's xa_lim (src/cuda/dit.cu:60-66): sequence row g sees keys
 // 0..lim(g), lim(g) = l-1 for image rows (g >= p), b1-1 for a reference
 // picture's rows b0..b1-1, g otherwise (the prompt is causal).  lim never
@@ -51,14 +53,38 @@ __device__ __forceinline__ int xa_lim(int g, int p, int l, int b0, int b1) {
   return g >= p ? l - 1 : (g >= b0 && g < b1 ? b1 - 1 : g);
 }
 
+// max and sum over lanes l and l ^ 32: v_permlane32_swap exchanges the upper half of one
+// register with the lower half of another, so two copies of v come back as (own, partner)
+// in either order.  Written as inline asm: given the same value twice, the compiler's
+// builtin for it returns what it treats as one value, and the pair's max or sum folds away.
+__device__ __forceinline__ void xswap32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float xmax32(float v) {
+  float a = v, b = v;
+  xswap32(a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xsum32(float v) {
+  float a = v, b = v;
+  xswap32(a, b);
+  return a + b;
+}
+
 // grid (ceil(n/128), 32 heads), block 256
 __global__ void __launch_bounds__(256, 2)
 k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vt,
          uint16_t* __restrict__ O, int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
-  // stage s: K tile (64 keys x 256 B) at s*32 KB, V^T tile (128 dims x 128 B) at s*32 KB + 16 KB.
+  // Two rings, one tile apart: K stage s (64 keys x 256 B) at s * 16 KB, V^T stage s (128 dims x
+  // 128 B) at 32 KB + s * 16 KB.  Step t reads K of tile t+1 and V^T of tile t, so the DMA of K
+  // t+2 and V^T t+1 go into the stages step t-1 read.
   // K rows: 16-byte chunk c stored at c ^ (row % 16); V^T rows: chunk c at c ^ ((row / 2) % 8).
-  __shared__ __align__(1024) uint8_t smem[2 * 32768];
-  const int h = blockIdx.y, t0 = blockIdx.x * AQ;
+  __shared__ __align__(1024) uint8_t smem[4 * 16384];
+  // Workgroups go to the 8 XCDs in turn (linear id mod 8).  XCD x takes whole heads x, x + 8,
+  // .. in order, so the query tiles that stream one head's K and V^T share that XCD's L2:
+  // two heads in flight an XCD, 4.4 MB at 4352 keys, instead of a sixteenth of each of 16.
+  const int QT = gridDim.x, lin = blockIdx.y * QT + blockIdx.x, slot = lin / 8;
+  const int h = lin % 8 + 8 * (slot / QT), t0 = slot % QT * AQ;
   const int tid = threadIdx.x, lane = tid & 63, hi = lane >> 5, lo = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS bases stay scalar
   const int tq = t0 + wave * 32 + lo;
@@ -90,15 +116,15 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
     const int vr = (4 * i + wave) * 8 + (lane >> 3);
     voff[i] = (uint32_t)((vr * lcap + 8 * ((lane & 7) ^ ((vr >> 1) & 7))) * 2);
   }
-  auto dma = [&](int t) {
-    uint8_t* ks = smem + (t & 1) * 32768;
-    uint8_t* vs = ks + 16384;
-    const int k0 = t * AK;
+  auto dma_k = [&](int t) {
+    uint8_t* ks = smem + (t & 1) * 16384;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kv_dma(kbase, kvext, (lds_void*)(ks + (4 * i + wave) * 1024), koff[i], k0 * 256);
-      kv_dma(vbase, kvext, (lds_void*)(vs + (4 * i + wave) * 1024), voff[i], k0 * 2);
-    }
+    for (int i = 0; i < 4; ++i) kv_dma(kbase, kvext, (lds_void*)(ks + (4 * i + wave) * 1024), koff[i], t * AK * 256);
+  };
+  auto dma_v = [&](int t) {
+    uint8_t* vs = smem + 32768 + (t & 1) * 16384;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kv_dma(vbase, kvext, (lds_void*)(vs + (4 * i + wave) * 1024), voff[i], t * AK * 2);
   };
 
   // per-lane LDS offsets: K row 32b + lo, chunk (2kk + hi) ^ (lo % 16); V^T row 32d + lo,
@@ -107,48 +133,50 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) kofs[kk] = lo * 256 + (((2 * kk + hi) ^ (lo & 15)) << 4);
 #pragma unroll
-  for (int bu = 0; bu < 4; ++bu) vofs[bu] = 16384 + lo * 128 + (((2 * bu + hi) ^ ((lo >> 1) & 7)) << 4);
+  for (int bu = 0; bu < 4; ++bu) vofs[bu] = 32768 + lo * 128 + (((2 * bu + hi) ^ ((lo >> 1) & 7)) << 4);
+  // S product i = 2kk + b: K fragment of 32-key block b, dims 16kk ..; O product j = 4bu + d:
+  // V^T fragment of dims 32d .., keys 16bu ..
+  auto kfrag = [&](auto ks_c, int i) {
+    return *(const f16x8*)(smem + kofs[i / 2] + (decltype(ks_c)::value * 16384 + (i % 2) * 8192));
+  };
+  auto vfrag = [&](auto vs_c, int j) {
+    return *(const f16x8*)(smem + vofs[j / 4] + (decltype(vs_c)::value * 16384 + (j % 4) * 4096));
+  };
 
   f32x16 o[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) o[d] = f32x16{};
   // mrun: the reference the scores are taken relative to (the row's running max, lagging
-  // it by at most MAX_SLACK); the S product starts from -mrun so its output is already
-  // relative (exact scale 1 only; another scale multiplies first and subtracts after)
+  // it by at most MAX_SLACK).  A tile's S product starts from -mrun (exact scale 1 only;
+  // another scale multiplies first and subtracts after): it is issued after the previous
+  // tile's max update, the last one before its own softmax.
   float mrun = 0.f, lrun = 0.f;
   const bool unit = scale == 1.f;
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const h2 ones = {(_Float16)1.f, (_Float16)1.f};
+  f32x16 sc[2];   // S^T - mrun of the tile in hand: two 32-key blocks x this wave's 32 queries
 
-  auto tile = [&](auto stage_c, int t) {
-    constexpr int ST = decltype(stage_c)::value;
-    // tile t has landed for every wave, and every wave is done with tile t-1's stage
+  // Step t: the softmax of tile t, then the S product of tile t+1 interleaved with tile t's
+  // exp2 (the VALU works while the MFMA pipe runs), then O^T += V^T P^T of tile t.
+  auto step = [&](auto st_c, auto last_c, int t) {
+    constexpr int ST = decltype(st_c)::value;
+    constexpr bool LAST = decltype(last_c)::value;
+    // K of tile t+1 and V^T of tile t have landed for every wave, and every wave is done
+    // with K of tile t and V^T of tile t-1
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // vmcnt(0) lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (t + 1 < tiles) dma(t + 1);
-    const int k0 = t * AK;
-    const float mref = t == 0 ? 0.f : mrun;
-    const float c0 = unit ? -mref : 0.f;
-
-    // S^T - mref: two 32-key blocks x this wave's 32 queries
-    f32x16 s[2];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[b][r] = c0;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const f16x8 a = *(const f16x8*)(smem + kofs[kk] + (ST * 32768 + b * 8192));
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[b], 0, 0, 0);
-      }
+    if constexpr (!LAST) {
+      if (t + 2 < tiles) dma_k(t + 2);
+      dma_v(t + 1);
     }
+    const int k0 = t * AK;
     if (!unit) {
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[b][r] = s[b][r] * scale - mref;
+        for (int r = 0; r < 16; ++r) sc[b][r] = sc[b][r] * scale - mrun;
     }
     if (k0 + AK - 1 > minlim) {   // some key of this tile is hidden from some query
 #pragma unroll
@@ -156,15 +184,19 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 32 * b + 8 * (r >> 2) + 4 * hi + (r & 3);
-          if (key > lim) s[b][r] = -INFINITY;
+          if (key > lim) sc[b][r] = -INFINITY;
         }
     }
-    float mx = fmaxf(s[0][0], s[0][1]);
+    float m4[4];
 #pragma unroll
-    for (int r = 2; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[0][r]), s[0][r + 1]);
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[1][r]), s[1][r + 1]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    for (int c = 0; c < 4; ++c) {
+      const int b = c / 2, r0 = (c % 2) * 8;
+      float m = fmaxf(fmaxf(sc[b][r0], sc[b][r0 + 1]), sc[b][r0 + 2]);
+      m = fmaxf(fmaxf(m, sc[b][r0 + 3]), sc[b][r0 + 4]);
+      m = fmaxf(fmaxf(m, sc[b][r0 + 5]), sc[b][r0 + 6]);
+      m4[c] = fmaxf(m, sc[b][r0 + 7]);
+    }
+    const float mx = xmax32(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
     // the first tile always sets the reference (its key 0 is visible to every row)
     const bool move = t == 0 || mx > MAX_SLACK;
     if (__ballot(move)) {
@@ -177,42 +209,95 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
       }
-      mrun = mref + shift;
+      mrun += shift;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[b][r] -= shift;
+        for (int r = 0; r < 16; ++r) sc[b][r] -= shift;
     }
 
-    // P = exp2(S^T - mrun) in fp16; O^T += V^T P^T over 4 steps of 16 keys; the row sum
-    // adds the fp16 P values the product uses
+    // S of tile t+1 from K stage ST^1, one MFMA a slot, with one pair of tile t's P values
+    // (two exp2, an fp16 pack, and the row sum of the fp16 values the product uses) a slot
+    f32x16 sn[2];
+    uint32_t pk[16];   // pair i: keys of S element (i / 8, 2 (i % 8)) and the next
+    f16x8 ka, kb;
+    if constexpr (!LAST) {
+      const float c0 = unit ? -mrun : 0.f;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        uint32_t pk[4];
+        for (int r = 0; r < 16; ++r) sn[b][r] = c0;
+      ka = kfrag(std::integral_constant<int, ST ^ 1>(), 0);
+      kb = kfrag(std::integral_constant<int, ST ^ 1>(), 1);
+    }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pk[e] = pack_f16x2(__builtin_amdgcn_exp2f(s[b][8 * u + 2 * e]), __builtin_amdgcn_exp2f(s[b][8 * u + 2 * e + 1]));
-          lrun = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[e]), ones, lrun, false);
-        }
-        const f16x8 pb = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const f16x8 a = *(const f16x8*)(smem + vofs[2 * b + u] + (ST * 32768 + d * 4096));
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[d], 0, 0, 0);
-        }
+    for (int i = 0; i < 16; ++i) {
+      if constexpr (!LAST) {
+        f16x8 kn = {};
+        if (i + 2 < 16) kn = kfrag(std::integral_constant<int, ST ^ 1>(), i + 2);
+        sn[i % 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[i / 2], sn[i % 2], 0, 0, 0);
+        ka = kb;
+        kb = kn;
       }
+      const int b = i / 8, r = 2 * (i % 8);
+      pk[i] = pack_f16x2(__builtin_amdgcn_exp2f(sc[b][r]), __builtin_amdgcn_exp2f(sc[b][r + 1]));
+      lrun = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[i]), ones, lrun, false);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // O^T += V^T P^T of tile t over 4 steps of 16 keys (step bu: block bu / 2, rows 8 (bu % 2) ..)
+    f16x8 va = vfrag(std::integral_constant<int, ST>(), 0), vb = vfrag(std::integral_constant<int, ST>(), 1);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      f16x8 vn = {};
+      if (j + 2 < 16) vn = vfrag(std::integral_constant<int, ST>(), j + 2);
+      const int bu = j / 4;
+      const f16x8 pb = __builtin_bit_cast(f16x8, u32x4{pk[4 * bu], pk[4 * bu + 1], pk[4 * bu + 2], pk[4 * bu + 3]});
+      o[j % 4] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[j % 4], 0, 0, 0);
+      va = vb;
+      vb = vn;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (!LAST) {
+      sc[0] = sn[0];
+      sc[1] = sn[1];
+    }
+    // the row sum is complete here: its v_dot2 chain stays in the slots above instead of
+    // sinking into the next step's max (its first use)
+    asm volatile("" : "+v"(lrun));
   };
 
-  dma(0);
-  for (int t = 0; t < tiles; t += 2) {
-    tile(std::integral_constant<int, 0>(), t);
-    if (t + 1 < tiles) tile(std::integral_constant<int, 1>(), t + 1);
+  // prologue: K of tile 0, then S of tile 0 (reference 0) while V^T 0 and K 1 move
+  dma_k(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  dma_v(0);
+  if (tiles > 1) dma_k(1);
+#pragma unroll
+  for (int b = 0; b < 2; ++b) sc[b] = f32x16{};
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    sc[i % 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kfrag(std::integral_constant<int, 0>(), i), qf[i / 2], sc[i % 2], 0, 0, 0);
+
+  typedef std::integral_constant<int, 0> S0;
+  typedef std::integral_constant<int, 1> S1;
+  typedef std::integral_constant<bool, false> More;
+  typedef std::integral_constant<bool, true> Last;
+  int t = 0;
+  for (; t + 2 < tiles; t += 2) {
+    step(S0(), More(), t);
+    step(S1(), More(), t + 1);
+  }
+  if (t + 1 < tiles) {
+    step(S0(), More(), t);
+    step(S1(), Last(), t + 1);
+  } else {
+    step(S0(), Last(), t);
   }
 
-  const float ltot = lrun + __shfl_xor(lrun, 32, 64);
-  const float inv = 1.f / ltot;
+  const float inv = 1.f / xsum32(lrun);
   if (tq < n) {
     uint16_t* orow = O + (int64_t)tq * 4096 + h * 128 + 4 * hi;
 #pragma unroll

@@ -333,13 +333,19 @@ def vt_pos(k):
     return k ^ ((((k >> 2) ^ (k >> 3)) & 1) * 12)
 
 
-def _attend_case(ctx, n, q0, p, l, b0, b1, seed, heads_checked=(0, 7, 31)):
+def _attend_case(ctx, n, q0, p, l, b0, b1, seed, heads_checked=(0, 7, 31), prescaled=False):
+    """prescaled: q is stored times log2(e)/sqrt(128), as exn_qkv_prep leaves it for the
+    DiT, and the kernel's own scale is 1."""
     rng = np.random.default_rng(seed)
     lcap = (l + 63) // 64 * 64
     q = rng.uniform(-2, 2, (n, 32, 128)).astype(np.float32)
     k = rng.uniform(-2, 2, (l, 32, 128)).astype(np.float32)
     v = rng.uniform(-1, 1, (l, 32, 128)).astype(np.float32)
     scale = 1 / math.sqrt(128)
+    kscale = scale * math.log2(math.e)
+    if prescaled:
+        q = q * np.float32(kscale)
+        scale, kscale = 1 / math.log2(math.e), 1.0
     qb, kb, vb = f16(q), f16(k), f16(v)
     qh = np.ascontiguousarray(qb.transpose(1, 0, 2))                         # [32][n][128]
     kh = np.zeros((32, lcap, 128), np.uint16)
@@ -348,7 +354,7 @@ def _attend_case(ctx, n, q0, p, l, b0, b1, seed, heads_checked=(0, 7, 31)):
     vth[:, :, vt_pos(np.arange(l))] = vb.transpose(1, 2, 0)
     out = X.DevBuf(ctx, (n, 4096), np.uint16)
     X.call("exn_attend", ctx.h, dev(ctx, qh).h, dev(ctx, kh).h, dev(ctx, vth).h, out.h, n, q0, p, l, lcap, b0, b1,
-           scale * math.log2(math.e))
+           kscale)
     got = from_bf16(out.get()).reshape(n, 32, 128)
     qf, kf, vf = (from_f16(a).astype(np.float64) for a in (qb, kb, vb))
     want = np.zeros((n, len(heads_checked), 128))
@@ -377,4 +383,16 @@ def test_attention_longer(ctx):
     """Image queries after a cached prompt over several key tiles, every head."""
     say("attend 300 queries over 556 keys")
     got, want = _attend_case(ctx, 300, 256, 256, 556, 0, 0, 5, heads_checked=tuple(range(0, 32, 3)))
+    assert xo.rel_l2(got, want) < 3e-3
+
+
+@pytest.mark.parametrize("n,q0,p,l,b0,b1", [(300, 256, 256, 556, 0, 0), (90, 0, 40, 90, 12, 30),
+                                            (200, 0, 72, 200, 0, 0), (64, 64, 64, 128, 0, 0)])
+def test_attention_prescaled(ctx, n, q0, p, l, b0, b1):
+    """The DiT's call: q already in log2 units (times log2(e)/sqrt(128)) and scale 1, the
+    path where each tile's product starts from minus the running max.  Tile counts odd
+    and even, one and several."""
+    say("attend prescaled", n, q0, p, l, b0, b1)
+    got, want = _attend_case(ctx, n, q0, p, l, b0, b1, 7 + n, prescaled=True)
+    assert np.abs(got - want).max() < 3e-3 + 2 ** -9
     assert xo.rel_l2(got, want) < 3e-3
