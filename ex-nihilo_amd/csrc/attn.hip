@@ -53,13 +53,7 @@ __device__ __forceinline__ int xa_lim(int g, int p, int l, int b0, int b1) {
   return g >= p ? l - 1 : (g >= b0 && g < b1 ? b1 - 1 : g);
 }
 
-// max and sum over lanes l and l ^ 32: v_permlane32_swap exchanges the upper half of one
-// register with the lower half of another, so two copies of v come back as (own, partner)
-// in either order.  Written as inline asm: given the same value twice, the compiler's
-// builtin for it returns what it treats as one value, and the pair's max or sum folds away.
-__device__ __forceinline__ void xswap32(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
+// max and sum over lanes l and l ^ 32 (xswap32 hands each lane its partner's value)
 __device__ __forceinline__ float xmax32(float v) {
   float a = v, b = v;
   xswap32(a, b);

@@ -22,7 +22,7 @@ static inline unsigned grid_of(int64_t n, int b) { return (unsigned)((n + b - 1)
 
 // sum over a 256-thread block; RED must hold 4 floats and not be reused until a barrier
 __device__ __forceinline__ float block_sum256(float v, float* red) {
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   return red[0] + red[1] + red[2] + red[3];
@@ -189,27 +189,62 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
   __shared__ uint16_t tile[64][128 + 2];
   const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * 64;
-  const float wq0 = wq[2 * lane], wq1 = wq[2 * lane + 1], wk0 = wk[2 * lane], wk1 = wk[2 * lane + 1];
-  for (int tt = 0; tt < 16; ++tt) {
-    const int64_t t = t0 + wave * 16 + tt;
-    if (t >= n) break;
-    const uint16_t* rq = qkv + t * (3 * 4096) + h * 128;
-    const uint32_t uq = *(const uint32_t*)(rq + 2 * lane);
-    const uint32_t uk = *(const uint32_t*)(rq + 4096 + 2 * lane);
-    const float2 c = *(const float2*)(cs + (row0 + t) * 128 + 2 * lane);
-    {
-      const float a = f16_lo(uq), b = f16_hi(uq);
-      const float inv = rsqrtf(wave_sum(a * a + b * b) * (1.f / 128.f) + 1e-6f);
-      const float an = a * inv * wq0, bn = b * inv * wq1;
-      *(uint32_t*)(q + ((int64_t)h * n + t) * 128 + 2 * lane) =
-          pack_f16x2((an * c.x - bn * c.y) * qscale, (an * c.y + bn * c.x) * qscale);
+  // q and k: 16 lanes a token, lane holding dims d8 .. d8+7 (its 4 rotation pairs) as one
+  // 16-byte load and store; a wave takes 4 tokens a round, its 16 tokens in 4 rounds whose
+  // loads are all issued first.  The RMS sum is a reduction over the 16 lanes.
+  const int sub = lane >> 4, d8 = (lane & 15) * 8;
+  float wqv[8], wkv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    wqv[j] = wq[d8 + j];
+    wkv[j] = wk[d8 + j];
+  }
+  u32x4 uq[4], uk[4];
+  f32x4 ca[4], cb[4];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int64_t tc = min(t0 + wave * 16 + it * 4 + sub, n - 1);   // rows past n: loaded, not stored
+    const uint16_t* rq = qkv + tc * (3 * 4096) + h * 128 + d8;
+    uq[it] = *(const u32x4*)rq;
+    uk[it] = *(const u32x4*)(rq + 4096);
+    const float* cr = cs + (row0 + tc) * 128 + d8;   // cos, sin of pairs d8/2 .. d8/2 + 3
+    ca[it] = *(const f32x4*)cr;
+    cb[it] = *(const f32x4*)(cr + 4);
+  }
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int64_t t = t0 + wave * 16 + it * 4 + sub;
+    const float c[8] = {ca[it][0], ca[it][1], ca[it][2], ca[it][3], cb[it][0], cb[it][1], cb[it][2], cb[it][3]};
+    float a[8], ssq = 0.f, ssk = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[2 * e] = f16_lo(uq[it][e]);
+      a[2 * e + 1] = f16_hi(uq[it][e]);
     }
-    {
-      const float a = f16_lo(uk), b = f16_hi(uk);
-      const float inv = rsqrtf(wave_sum(a * a + b * b) * (1.f / 128.f) + 1e-6f);
-      const float an = a * inv * wk0, bn = b * inv * wk1;
-      *(uint32_t*)(kc + ((int64_t)h * lcap + row0 + t) * 128 + 2 * lane) =
-          pack_f16x2(an * c.x - bn * c.y, an * c.y + bn * c.x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ssq += a[j] * a[j];
+    float b[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      b[2 * e] = f16_lo(uk[it][e]);
+      b[2 * e + 1] = f16_hi(uk[it][e]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ssk += b[j] * b[j];
+    const float invq = rsqrtf(row16_sum(ssq) * (1.f / 128.f) + 1e-6f);
+    const float invk = rsqrtf(row16_sum(ssk) * (1.f / 128.f) + 1e-6f);
+    u32x4 oq, ok;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float cx = c[2 * e], cy = c[2 * e + 1];
+      const float an = a[2 * e] * invq * wqv[2 * e], bn = a[2 * e + 1] * invq * wqv[2 * e + 1];
+      oq[e] = pack_f16x2((an * cx - bn * cy) * qscale, (an * cy + bn * cx) * qscale);
+      const float ak = b[2 * e] * invk * wkv[2 * e], bk = b[2 * e + 1] * invk * wkv[2 * e + 1];
+      ok[e] = pack_f16x2(ak * cx - bk * cy, ak * cy + bk * cx);
+    }
+    if (t < n) {
+      *(u32x4*)(q + ((int64_t)h * n + t) * 128 + d8) = oq;
+      *(u32x4*)(kc + ((int64_t)h * lcap + row0 + t) * 128 + d8) = ok;
     }
   }
   // v: 64 tokens x 128 dims through LDS, out as 128 rows of 64 consecutive keys

@@ -59,6 +59,48 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// v from the lane the DPP control names (quad_perm 0x00-0xFF, row_mirror 0x140,
+// row_half_mirror 0x141), within rows of 16 lanes
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// The sum of v over each row of 16 lanes, in every lane of the row: pairs (xor 1), quads
+// (xor 2), then the two quads of each half (half mirror) and the two halves (mirror).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);   // row_half_mirror: lane i <-> 7 - i of each half row
+  v += dpp_f<0x140>(v);   // row_mirror: lane i <-> 15 - i
+  return v;
+}
+
+// gfx950's v_permlane16_swap / v_permlane32_swap on two copies of a value: a and b come back
+// holding the lane's own value and its partner's (lane ^ 16, lane ^ 32), in either order.
+// Written as inline asm: given the same value twice, the compiler's builtins return what it
+// treats as one value, and a sum or max over the pair folds away.  The s_nop covers the
+// VALU write -> permlane read hazard of the copies.
+__device__ __forceinline__ void xswap16(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void xswap32(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// The sum of v over the wave, in every lane, without LDS: rows of 16 by DPP, then the row
+// pairs and the halves by lane swaps.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = row16_sum(v);
+  float a = v, b = v;
+  xswap16(a, b);
+  v = a + b;
+  a = v;
+  b = v;
+  xswap32(a, b);
+  return a + b;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
