@@ -192,4 +192,17 @@ hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float d
 hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out,
                   int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale);
 
+// the VAE decoder (vae.hip).  vae_conv: out 0 fp32 (+ bias, + res), 1 bf16 (+ bias), 2 fp32
+// (+ bias) clamped to -1 .. 1; taps 9 or 1; up: the input is the half-size picture
+hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
+                    const float* bias, const float* res, void* y, int h, int w, int c, int cout, int kp);
+hipError_t vae_rms_silu(hipStream_t s, int64_t P, int C, const float* x, const float* gamma, uint16_t* y, int silu);
+hipError_t vae_dupup_add(hipStream_t s, int cin, int cout, int ft, int h, int w, const float* x, float* y);
+hipError_t vae_latent_pixels(hipStream_t s, int64_t P, int C, const float* z, uint16_t* y);
+hipError_t vae_split_qkv(hipStream_t s, int64_t n, int64_t np, int c, const float* qkv, uint16_t* q, uint16_t* k,
+                         uint16_t* vt);
+hipError_t vae_softmax_rows(hipStream_t s, int n, int np, float scale, const float* S, uint16_t* P);
+hipError_t vae_pack_conv(hipStream_t s, int64_t o, int ci, int taps, int kp, const float* src, uint16_t* dst);
+hipError_t vae_round_bf16(hipStream_t s, int64_t n, float* x);
+
 }  // namespace exn

@@ -1,0 +1,385 @@
+// vae.hip -- the VAE decoder's kernels on gfx950 (Qwen-Image-2.1's decoder,
+// Wan 2.2's, on one frame): replaces src/cuda/vae.cu and the products and
+// norms src/cuda-vae.lisp:94-136 takes from illatio.
+//
+// Activations are channels last: a picture of H x W pixels is H*W rows of C
+// values, fp32 between blocks (the residual stream and the convolutions'
+// outputs), bf16 where they feed a product.
+//
+// Convolutions (3 x 3 'same', and 1 x 1) are implicit products on the bf16
+// MFMA, Y[pixel][o] = sum over k of A[pixel][k] Wt[o][k] with k = tap * C + c:
+// the A tile is gathered straight from the input picture by LDS-DMA (buffer
+// loads to LDS), each lane's 16 bytes (8 channels of one tap) from its
+// pixel's neighbour, taps off the picture and K past 9C as out-of-range
+// offsets, which the buffer load reads as zeros.  With UP the input is the
+// half-size picture and the neighbour's pixel is halved: the nearest x2
+// upsampling (x_up2) folded into the resample convolution's loads.
+//
+// Tiles: 256 pixels x 144 output channels a workgroup (144 divides every
+// width of the decoder: 1152, 576, 288, 144), 8 waves of 32 pixels x 144,
+// each a 2 x 9 grid of v_mfma_f32_16x16x32_bf16; K 64 a step, three LDS
+// stages (50 KB each) so that a step's DMA has two steps to land.
+#include "exn_common.h"
+
+namespace exn {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+static inline unsigned grid_of(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
+
+// one 16-byte DMA lane; a byte offset at or past EXTENT reads as zeros
+__device__ __forceinline__ void conv_dma(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
+
+#define VBM 256
+#define VBN 144
+#define VSTAGE (VBM * 128 + VBN * 128)   // A rows | B rows, 64 bf16 of K each: 51200 bytes
+#define VOFF_NONE 0x80000000u            // past any extent: the load reads zeros
+
+// OUT: 0 fp32 (+ bias, + res when given), 1 bf16 (+ bias), 2 fp32 (+ bias) clamped to -1 .. 1
+template <int TAPS, int UP, int OUT>
+__global__ void __launch_bounds__(512)
+k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
+       const float* __restrict__ res, void* __restrict__ Y, int H, int W, int C, int cout, int Kp) {
+  extern __shared__ __align__(1024) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int P = H * W;
+  const int m0 = blockIdx.x * VBM, n0 = blockIdx.y * VBN;
+  const int KT = Kp / 64;
+  const int Hs = UP ? H >> 1 : H, Ws = UP ? W >> 1 : W;
+  const uint32_t xext = (uint32_t)((int64_t)Hs * Ws * C * 2);
+  const uint16_t* wbase = Wt + (int64_t)n0 * Kp;
+  const uint32_t wext = (uint32_t)((int64_t)max(0, cout - n0) * Kp * 2);
+
+  // A: round i moves tile rows (8i + wave) * 8 + lane / 8; LDS chunk lane % 8 of a row holds
+  // K chunk (lane % 8) ^ swizzle(row).  The chunk's tap and channel move 64 K a step.
+  int py[4], px[4], cc[4], tp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (8 * i + wave) * 8 + (lane >> 3);
+    const int m = m0 + r;
+    const int y = m / W;
+    py[i] = m < P ? y : -0x40000000;   // a row past the picture: every neighbour off it
+    px[i] = m - y * W;
+    const int k = 8 * ((lane & 7) ^ ((r >> 1) & 7));
+    tp[i] = k / C;
+    cc[i] = k - tp[i] * C;
+  }
+  // B: rounds 0 and 1 move rows 64 rd + 8 wave + lane / 8, round 2 rows 128 + 2 wave + lane / 8
+  // (lanes 0..15): 144 rows, the same three DMA instructions in every wave
+  uint32_t boff[3];
+#pragma unroll
+  for (int rd = 0; rd < 3; ++rd) {
+    const int row = rd < 2 ? 64 * rd + 8 * wave + (lane >> 3) : 128 + 2 * wave + ((lane >> 3) & 1);
+    boff[rd] = (uint32_t)((row * Kp + 8 * ((lane & 7) ^ ((row >> 1) & 7))) * 2);
+  }
+  // issue the next k-step's tiles into stage s (the A chunks' positions then move on)
+  auto dma = [&](int t, int s) {
+    uint8_t* st = smem + s * VSTAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tap = tp[i];
+      int dy = 0, dx = 0;
+      if constexpr (TAPS == 9) {
+        const int q = (tap * 11) >> 5;   // tap / 3 for tap < 9
+        dy = q - 1;
+        dx = tap - 3 * q - 1;
+      }
+      int sy = py[i] + dy, sx = px[i] + dx;
+      const bool ok = tap < TAPS && sy >= 0 && sy < H && sx >= 0 && sx < W;
+      if constexpr (UP) {
+        sy >>= 1;
+        sx >>= 1;
+      }
+      const uint32_t off = ok ? (uint32_t)(((sy * Ws + sx) * C + cc[i]) * 2) : VOFF_NONE;
+      conv_dma(X, xext, (lds_void*)(st + (8 * i + wave) * 1024), off, 0);
+      cc[i] += 64;
+      if (cc[i] >= C) {   // C >= 64: one wrap at most
+        cc[i] -= C;
+        tp[i] += 1;
+      }
+    }
+    conv_dma(wbase, wext, (lds_void*)(st + 32768 + wave * 1024), boff[0], t * 128);
+    conv_dma(wbase, wext, (lds_void*)(st + 32768 + 8192 + wave * 1024), boff[1], t * 128);
+    if (lane < 16) conv_dma(wbase, wext, (lds_void*)(st + 32768 + 16384 + wave * 256), boff[2], t * 128);
+  };
+
+  // fragments: lane holds row lo of a 16-row block, K 8 q4 .. of a slice of 32
+  const int lo = lane & 15, q4 = lane >> 4, fs = (lo >> 1) & 7;
+  const int a_rd = (32 * wave + lo) * 128, b_rd = 32768 + lo * 128;
+  f32x4 acc[2][9];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 9; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  dma(0, 0);
+  dma(min(1, KT - 1), 1);   // every step issues seven DMA instructions a wave, so vmcnt(7) below
+  int s = 0;
+  for (int t = 0; t < KT; ++t) {
+    // step t has landed for every wave, and every wave is done with stage (t + 2) % 3
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((7 & 0xF) | (0x7 << 4) | (0x0 << 8));   // vmcnt(7) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int s2 = s >= 1 ? s - 1 : 2;   // (t + 2) % 3
+    dma(min(t + 2, KT - 1), s2);         // past the end: a harmless reload, never read
+    const uint8_t* st = smem + s * VSTAGE;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int co = ((4 * kk + q4) ^ fs) << 4;
+      bf16x8 a[2], b[9];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *(const bf16x8*)(st + a_rd + i * 2048 + co);
+#pragma unroll
+      for (int j = 0; j < 9; ++j) b[j] = *(const bf16x8*)(st + b_rd + j * 2048 + co);
+#pragma unroll
+      for (int j = 0; j < 9; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    s = s == 2 ? 0 : s + 1;
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // no DMA left in flight
+  asm volatile("" ::: "memory");
+
+  // lane holds rows 4 q4 .. +3 of each 16 x 16 tile, column lo
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const int n = n0 + 16 * j + lo;
+    if (n >= cout) continue;
+    const float bn = bias[n];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 32 * wave + 16 * i + 4 * q4 + r;
+        if (m >= P) continue;
+        const int64_t at = (int64_t)m * cout + n;
+        float v = acc[i][j][r] + bn;
+        if constexpr (OUT == 0) {
+          if (res) v += res[at];
+          ((float*)Y)[at] = v;
+        } else if constexpr (OUT == 1) {
+          ((uint16_t*)Y)[at] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
+        } else {
+          ((float*)Y)[at] = fminf(1.f, fmaxf(-1.f, v));
+        }
+      }
+  }
+}
+
+template <int TAPS, int UP, int OUT>
+static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const float* res,
+                              void* y, int h, int w, int c, int cout, int kp) {
+  auto kern = k_conv<TAPS, UP, OUT>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 3 * VSTAGE);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid(grid_of((int64_t)h * w, VBM), grid_of(cout, VBN));
+  hipLaunchKernelGGL(kern, grid, dim3(512), 3 * VSTAGE, s, x, wt, bias, res, y, h, w, c, cout, kp);
+  return hipGetLastError();
+}
+
+hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt, const float* bias,
+                    const float* res, void* y, int h, int w, int c, int cout, int kp) {
+  // the loads move 8 channels at once and each k-step moves a chunk's tap at most once;
+  // every offset and extent fits 31 bits
+  if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || h <= 0 || w <= 0 || (up && (h % 2 || w % 2)) ||
+      ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || (int64_t)h * w * c * 2 >= ((int64_t)1 << 31) ||
+      (int64_t)cout * kp * 2 >= ((int64_t)1 << 31))
+    return hipErrorInvalidValue;
+  if (taps == 9 && !up && out == 0) return launch_conv<9, 0, 0>(s, x, wt, bias, res, y, h, w, c, cout, kp);
+  if (taps == 9 && !up && out == 1) return launch_conv<9, 0, 1>(s, x, wt, bias, res, y, h, w, c, cout, kp);
+  if (taps == 9 && !up && out == 2) return launch_conv<9, 0, 2>(s, x, wt, bias, res, y, h, w, c, cout, kp);
+  if (taps == 9 && up && out == 0) return launch_conv<9, 1, 0>(s, x, wt, bias, res, y, h, w, c, cout, kp);
+  if (taps == 1 && !up && out == 0) return launch_conv<1, 0, 0>(s, x, wt, bias, res, y, h, w, c, cout, kp);
+  if (taps == 1 && !up && out == 1) return launch_conv<1, 0, 1>(s, x, wt, bias, res, y, h, w, c, cout, kp);
+  return hipErrorInvalidValue;
+}
+
+// --- the bandwidth kernels ----------------------------------------------------------
+
+// y = x / max(|x|, 1e-12) * sqrt(C) * gamma over each pixel's C channels (src/cuda-vae.lisp's
+// v_rms with eps 1e-12; inspect/ref_vae.py:50-52), then SiLU when SILU; bf16 out.  LP lanes a
+// pixel (16 or 64), C a multiple of 4.
+template <int LP, int SILU>
+__global__ void __launch_bounds__(256)
+k_rms_silu(int64_t P, int C, const float* __restrict__ x, const float* __restrict__ gamma, uint16_t* __restrict__ y) {
+  const int64_t p = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LP;
+  const int sub = threadIdx.x % LP;
+  const bool live = p < P;
+  const float* r = x + (live ? p : 0) * C;
+  float ss = 0.f;
+  for (int c = 4 * sub; c < C; c += 4 * LP) {
+    const f32x4 v = *(const f32x4*)(r + c);
+    ss += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+  }
+  ss = LP == 64 ? wave_sum_dpp(ss) : row16_sum(ss);   // every lane of the group takes part
+  const float inv = sqrtf((float)C) / fmaxf(sqrtf(ss), 1e-12f);
+  if (!live) return;
+  uint16_t* o = y + p * C;
+  for (int c = 4 * sub; c < C; c += 4 * LP) {
+    const f32x4 v = *(const f32x4*)(r + c), g = *(const f32x4*)(gamma + c);
+    float e[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      e[q] = v[q] * inv * g[q];
+      if constexpr (SILU) e[q] = silu_bf16out(e[q]);
+    }
+    *(u32x2*)(o + c) = u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])};
+  }
+}
+
+hipError_t vae_rms_silu(hipStream_t s, int64_t P, int C, const float* x, const float* gamma, uint16_t* y, int silu) {
+  if (C % 4 || P <= 0) return P == 0 ? hipSuccess : hipErrorInvalidValue;
+  if (C <= 512) {
+    const unsigned g = grid_of(P * 16, 256);
+    if (silu) hipLaunchKernelGGL((k_rms_silu<16, 1>), dim3(g), dim3(256), 0, s, P, C, x, gamma, y);
+    else hipLaunchKernelGGL((k_rms_silu<16, 0>), dim3(g), dim3(256), 0, s, P, C, x, gamma, y);
+  } else {
+    const unsigned g = grid_of(P * 64, 256);
+    if (silu) hipLaunchKernelGGL((k_rms_silu<64, 1>), dim3(g), dim3(256), 0, s, P, C, x, gamma, y);
+    else hipLaunchKernelGGL((k_rms_silu<64, 0>), dim3(g), dim3(256), 0, s, P, C, x, gamma, y);
+  }
+  return hipGetLastError();
+}
+
+// y (2H x 2W x cout, fp32) += DupUp3D(x) (H x W x cin), frame ft - 1 of ft: channel c of pixel
+// (Y, X) adds channel j / rep of pixel (Y/2, X/2), j = ((c ft + ft - 1) 2 + Y%2) 2 + X%2,
+// rep = cout ft 4 / cin (src/cuda/vae.cu's x_dupup_add, the index of inspect/ref_vae.py:79-85)
+__global__ void k_dupup_add(int cin, int cout, int ft, int H, int W, const float* __restrict__ x,
+                            float* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 4LL * H * W * cout) return;
+  const int c = (int)(i % cout);
+  const int64_t p = i / cout;
+  const int yy = (int)(p / (2 * W)), xx = (int)(p % (2 * W));
+  const int rep = cout * ft * 4 / cin;
+  const int j = ((c * ft + ft - 1) * 2 + (yy & 1)) * 2 + (xx & 1);
+  y[i] += x[((int64_t)(yy >> 1) * W + (xx >> 1)) * cin + j / rep];
+}
+
+hipError_t vae_dupup_add(hipStream_t s, int cin, int cout, int ft, int h, int w, const float* x, float* y) {
+  if ((int64_t)cout * ft * 4 % cin) return hipErrorInvalidValue;
+  const int64_t n = 4LL * h * w * cout;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_dupup_add, dim3(grid_of(n, 256)), dim3(256), 0, s, cin, cout, ft, h, w, x, y);
+  return hipGetLastError();
+}
+
+// the latent (64 x P fp32, channel-major) as pixel rows of 64 bf16
+__global__ void k_latent_pixels(int64_t P, int C, const float* __restrict__ z, uint16_t* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P * C) return;
+  const int64_t p = i / C;
+  const int c = (int)(i % C);
+  y[i] = (uint16_t)(pack_bf16x2(z[c * P + p], 0.f) & 0xFFFFu);
+}
+
+hipError_t vae_latent_pixels(hipStream_t s, int64_t P, int C, const float* z, uint16_t* y) {
+  if (P * C == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_latent_pixels, dim3(grid_of(P * C, 256)), dim3(256), 0, s, P, C, z, y);
+  return hipGetLastError();
+}
+
+// the attention's q|k|v rows (n x 3c fp32) apart: q, k as n x c bf16 and v transposed, c x np
+// bf16, columns n .. np - 1 zero (the second product's K is np, a multiple of 64)
+__global__ void k_split_qkv(int64_t n, int64_t np, int c, const float* __restrict__ qkv, uint16_t* __restrict__ q,
+                            uint16_t* __restrict__ k, uint16_t* __restrict__ vt) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= np * c) return;
+  const int64_t t = i / c;
+  const int j = (int)(i % c);
+  if (t < n) {
+    const float* r = qkv + t * 3 * c;
+    q[i] = (uint16_t)(pack_bf16x2(r[j], 0.f) & 0xFFFFu);
+    k[i] = (uint16_t)(pack_bf16x2(r[c + j], 0.f) & 0xFFFFu);
+    vt[(int64_t)j * np + t] = (uint16_t)(pack_bf16x2(r[2 * c + j], 0.f) & 0xFFFFu);
+  } else {
+    vt[(int64_t)j * np + t] = 0;
+  }
+}
+
+hipError_t vae_split_qkv(hipStream_t s, int64_t n, int64_t np, int c, const float* qkv, uint16_t* q, uint16_t* k,
+                         uint16_t* vt) {
+  if (np < n || np * c == 0) return np < n ? hipErrorInvalidValue : hipSuccess;
+  hipLaunchKernelGGL(k_split_qkv, dim3(grid_of(np * c, 256)), dim3(256), 0, s, n, np, c, qkv, q, k, vt);
+  return hipGetLastError();
+}
+
+// each row of S (n x np fp32, the first n columns the scores): softmax of the scores times
+// SCALE as bf16 P, columns n .. np - 1 zero (src/cuda/vae.cu's x_softmax_rows)
+__global__ void __launch_bounds__(256)
+k_softmax_rows(int n, int np, float scale, const float* __restrict__ S, uint16_t* __restrict__ P) {
+  __shared__ float red[8];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const float* r = S + (int64_t)row * np;
+  uint16_t* o = P + (int64_t)row * np;
+  float mx = -INFINITY;
+  for (int c = tid; c < n; c += 256) mx = fmaxf(mx, r[c]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float sum = 0.f;
+  for (int c = tid; c < n; c += 256) sum += expf((r[c] - mx) * scale);
+  sum = wave_sum_dpp(sum);
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = sum;
+  __syncthreads();
+  const float inv = 1.f / (red[4] + red[5] + red[6] + red[7]);
+  for (int c = tid; c < np; c += 256) {
+    const float p = c < n ? expf((r[c] - mx) * scale) * inv : 0.f;
+    o[c] = (uint16_t)(pack_bf16x2(p, 0.f) & 0xFFFFu);
+  }
+}
+
+hipError_t vae_softmax_rows(hipStream_t s, int n, int np, float scale, const float* S, uint16_t* P) {
+  if (n <= 0 || np < n) return n == 0 ? hipSuccess : hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_softmax_rows, dim3(n), dim3(256), 0, s, n, np, scale, S, P);
+  return hipGetLastError();
+}
+
+// a tensor as the file holds it (fp32 values; a convolution (o, i, [1,] k, k)) -> the device
+// form: a convolution's weights as bf16 rows of (tap, channel), K padded with zeros to kp
+__global__ void k_pack_conv(int64_t o, int ci, int taps, int kp, const float* __restrict__ src,
+                            uint16_t* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= o * kp) return;
+  const int64_t r = i / kp;
+  const int k = (int)(i % kp);
+  float v = 0.f;
+  if (k < taps * ci) {
+    const int tap = k / ci, c = k % ci;
+    v = src[(r * ci + c) * taps + tap];
+  }
+  dst[i] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
+}
+
+hipError_t vae_pack_conv(hipStream_t s, int64_t o, int ci, int taps, int kp, const float* src, uint16_t* dst) {
+  if (kp < taps * ci || o * kp == 0) return kp < taps * ci ? hipErrorInvalidValue : hipSuccess;
+  hipLaunchKernelGGL(k_pack_conv, dim3(grid_of(o * kp, 256)), dim3(256), 0, s, o, ci, taps, kp, src, dst);
+  return hipGetLastError();
+}
+
+// fp32 values rounded through bf16 (a tensor the file ships as bf16, kept as fp32)
+__global__ void k_round_bf16(int64_t n, float* __restrict__ x) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = bf16_to_f32((uint16_t)(pack_bf16x2(x[i], 0.f) & 0xFFFFu));
+}
+
+hipError_t vae_round_bf16(hipStream_t s, int64_t n, float* x) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_round_bf16, dim3(grid_of(n, 256)), dim3(256), 0, s, n, x);
+  return hipGetLastError();
+}
+
+}  // namespace exn

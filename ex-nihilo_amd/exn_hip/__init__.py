@@ -93,6 +93,18 @@ SIGNATURES = {
     "exn_dit_release": (c_int, [vp]),
     "exn_dit_destroy": (c_int, [vp]),
     "exn_dit_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
+    "exn_vae_create": (c_int, [vp, POINTER(vp)]),
+    "exn_vae_set": (c_int, [vp, c_char_p, c_int, vp, POINTER(c_int64), c_int]),
+    "exn_vae_synth": (c_int, [vp, c_uint64]),
+    "exn_vae_check": (c_int, [vp]),
+    "exn_vae_decode": (c_int, [vp, vp, c_int, c_int, vp]),
+    "exn_vae_decode_dev": (c_int, [vp, vp, c_int, c_int, vp]),
+    "exn_vae_release": (c_int, [vp]),
+    "exn_vae_destroy": (c_int, [vp]),
+    "exn_vae_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
+    "exn_vae_conv": (c_int, [vp, c_int, c_int, c_int, vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int]),
+    "exn_vae_rms_silu": (c_int, [vp, c_int64, c_int, vp, vp, vp, c_int]),
+    "exn_vae_dupup_add": (c_int, [vp, c_int, c_int, c_int, c_int, c_int, vp, vp]),
 }
 
 
@@ -365,3 +377,69 @@ def generate_latent(d: Dit, context: np.ndarray, p: int, z: np.ndarray, h: int, 
         v = dit_velocity(d, context, p, z, h, w, s, prefix_key=prefix_key, ref=ref)
         z = z + np.float32(s2 - s) * v
     return z
+
+
+# --- the VAE decoder: upload-vae, vae-decode, vae-release (src/cuda-vae.lisp) -------------
+
+class Vae:
+    """The decoder on the device: its tensors and scratch (gvae)."""
+
+    def __init__(self, ctx: Context):
+        h = vp()
+        call("exn_vae_create", ctx.h, ctypes.byref(h))
+        self.ctx, self.h = ctx, h
+
+    def set(self, name: str, kind: int, data: np.ndarray, shape):
+        """One tensor by its safetensors name and shape (BF16 bit patterns as uint16, or F32)."""
+        dims = (c_int64 * len(shape))(*shape)
+        call("exn_vae_set", self.h, name.encode(), kind, ptr(np.ascontiguousarray(data)), dims, len(shape))
+
+    def synth(self, seed: int):
+        call("exn_vae_synth", self.h, seed)
+
+    def check(self):
+        call("exn_vae_check", self.h)
+
+    def memory(self):
+        w, s = c_int64(), c_int64()
+        call("exn_vae_memory", self.h, ctypes.byref(w), ctypes.byref(s))
+        return w.value, s.value
+
+    def release(self):
+        call("exn_vae_release", self.h)
+
+    def destroy(self):
+        if self.h:
+            call("exn_vae_destroy", self.h)
+            self.h = None
+
+
+def upload_vae(tensors=None, *, device: int = 0, seed: int | None = None, ctx=None) -> Vae:
+    """upload-vae (src/cuda-vae.lisp:15-26): TENSORS an iterable of (name, kind,
+    data, shape) as read from the safetensors, or SEED: the synthetic decoder made
+    on the device.  Checked against the decoder's tensor list before return."""
+    ctx = ctx or Context(device)
+    v = Vae(ctx)
+    if seed is not None:
+        v.synth(seed)
+    for name, kind, data, shape in tensors or ():
+        v.set(name, kind, data, shape)
+    v.check()
+    return v
+
+
+def vae_decode(v: Vae, latent: np.ndarray, h: int, w: int):
+    """vae-decode (src/cuda-vae.lisp:94-136): LATENT (64 x H x W floats,
+    channel-major, denormalized) -> (the picture as 16H x 16W x 4 floats, RGBA
+    in -1..1, channels last; its height; its width)."""
+    lat = np.ascontiguousarray(latent, dtype=np.float32).reshape(-1)
+    if lat.size != 64 * h * w:
+        raise ExnError(EINVAL, "latent of %d floats for %d x %d" % (lat.size, h, w))
+    px = np.empty((16 * h, 16 * w, 4), np.float32)
+    call("exn_vae_decode", v.h, ptr(lat), h, w, ptr(px))
+    return px, 16 * h, 16 * w
+
+
+def vae_release(v: Vae):
+    """vae-release (src/cuda-vae.lisp:28-33): the scratch freed."""
+    v.release()

@@ -1,0 +1,188 @@
+"""The VAE decoder on the GPU through the C ABI, against the oracle
+(oracle/exn_vae_oracle.py) and the reference script's own pictures
+(tests/golden/ref_vae_tiny.npz).  The picture's bar is the reference's for its
+half-precision decoder against the decoder in floats: within 3 of 255
+(README.md:130-132), so max |difference| <= 6/255 on -1..1; and relative L2 <=
+1e-2.  Needs an MI355X."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import exn_hip as X
+from oracle import exn_oracle as xo
+from oracle import exn_vae_oracle as vo
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+PICTURE_MAX = 6.0 / 255.0
+
+
+def say(*a):
+    print("[gpu]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = X.Context(0)
+    yield c
+    c.close()
+
+
+_KEEP = []
+
+
+def dev(ctx, a):
+    """A device copy of A kept alive for the module: a temporary freed at once could hand
+    its memory to the next upload before the kernel reads it."""
+    b = X.DevBuf.of(ctx, np.ascontiguousarray(a))
+    _KEEP.append(b)
+    return b
+
+
+def pack_conv(w, kp):
+    """(o, i, [1,] k, k) -> bf16 rows of (tap, channel), K padded to kp: the device form."""
+    o, i = w.shape[0], w.shape[1]
+    k = w.shape[-1]
+    rows = w.reshape(o, i, k * k).transpose(0, 2, 1).reshape(o, k * k * i)
+    out = np.zeros((o, kp), np.uint16)
+    out[:, :rows.shape[1]] = xo.bf16_bits(rows)
+    return out
+
+
+CONV_CASES = [  # (h, w, c, cout, taps, up, out, with res)
+    (5, 7, 64, 144, 9, 0, 0, False),
+    (16, 16, 144, 288, 9, 0, 0, True),
+    (6, 10, 288, 144, 9, 0, 1, False),
+    (3, 4, 1152, 1152, 9, 0, 0, True),
+    (9, 9, 144, 4, 9, 0, 2, False),
+    (8, 6, 576, 576, 9, 1, 0, False),
+    (20, 18, 288, 288, 9, 1, 0, False),
+    (7, 9, 1152, 3456, 1, 0, 0, False),
+    (11, 5, 288, 144, 1, 0, 0, True),
+    (4, 4, 64, 64, 1, 0, 1, False),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv_against_float64(ctx, case):
+    """The implicit-GEMM convolution: partial pixel and channel tiles, K not a
+    multiple of 64 (144, 288 wide), the upsampling fold, the three outputs."""
+    h, w, c, cout, taps, up, out, with_res = case
+    say("conv", case)
+    rng = np.random.default_rng(h * 1000 + c + cout)
+    hs, ws = (h // 2, w // 2) if up else (h, w)
+    x = xo.bf16_round(rng.standard_normal((hs, ws, c)).astype(np.float32))
+    k = 3 if taps == 9 else 1
+    wt = xo.bf16_round((rng.standard_normal((cout, c, 1, k, k)) / np.sqrt(c * taps)).astype(np.float32))
+    b = rng.standard_normal(cout).astype(np.float32) * 0.1
+    kp = (taps * c + 63) // 64 * 64
+    res = rng.standard_normal((h * w, cout)).astype(np.float32) if with_res else None
+    xin = np.repeat(np.repeat(x, 2, 0), 2, 1) if up else x
+    want = vo.conv(xin.astype(np.float64), wt.astype(np.float64), b.astype(np.float64), k).reshape(h * w, cout)
+    if with_res:
+        want = want + res
+    if out == 2:
+        want = np.clip(want, -1, 1)
+    y = X.DevBuf(ctx, (h * w, cout), np.uint16 if out == 1 else np.float32)
+    rbuf = dev(ctx, res) if with_res else None
+    X.call("exn_vae_conv", ctx.h, taps, up, out, dev(ctx, xo.bf16_bits(x)).h, dev(ctx, pack_conv(wt, kp)).h,
+           dev(ctx, b).h, rbuf.h if rbuf else None, y.h, h, w, c, cout, kp)
+    got = y.get()
+    if out == 1:
+        got = xo.bf16_to_f32(got)
+        assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max() + 1e-6
+    else:
+        assert np.abs(got - want).max() < 1e-4 * max(1.0, np.abs(want).max())
+
+
+def test_conv_rejects_bad_shapes(ctx):
+    with pytest.raises(X.ExnError) as e:
+        X.call("exn_vae_conv", ctx.h, 9, 0, 0, dev(ctx, np.zeros(64, np.uint16)).h, dev(ctx, np.zeros(64, np.uint16)).h,
+               dev(ctx, np.zeros(4, np.float32)).h, None, dev(ctx, np.zeros(64, np.float32)).h, 1, 1, 40, 4, 384)
+    assert e.value.code == X.EINVAL
+
+
+@pytest.mark.parametrize("c,silu", [(144, 1), (288, 1), (576, 1), (1152, 1), (1152, 0)])
+def test_rms_silu(ctx, c, silu):
+    rng = np.random.default_rng(c + silu)
+    n = 777
+    x = (rng.standard_normal((n, c)) * 3 + 0.5).astype(np.float32)
+    x[5] = 0.0                                   # the 1e-12 floor
+    g = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    want = vo.rms(x.reshape(1, n, c), g).reshape(n, c)
+    if silu:
+        want = vo.silu(want)
+    y = X.DevBuf(ctx, (n, c), np.uint16)
+    X.call("exn_vae_rms_silu", ctx.h, n, c, dev(ctx, x).h, dev(ctx, g).h, y.h, silu)
+    got = xo.bf16_to_f32(y.get())
+    assert np.abs(got - want).max() <= 2 ** -8 * np.abs(want).max()
+    assert np.all(got[5] == 0)
+
+
+@pytest.mark.parametrize("cin,cout,ft", [(1152, 1152, 2), (1152, 576, 2), (576, 288, 1)])
+def test_dupup_add(ctx, cin, cout, ft):
+    rng = np.random.default_rng(cin + cout)
+    h, w = 3, 5
+    x = rng.standard_normal((h, w, cin)).astype(np.float32)
+    y0 = rng.standard_normal((2 * h, 2 * w, cout)).astype(np.float32)
+    y = dev(ctx, y0)
+    X.call("exn_vae_dupup_add", ctx.h, cin, cout, ft, h, w, dev(ctx, x).h, y.h)
+    assert np.array_equal(y.get(), y0 + vo.dupup(x, cout, ft))
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(os.path.join(GOLDEN, "ref_vae_tiny.npz"))
+
+
+@pytest.fixture(scope="module")
+def vae(ctx, golden):
+    v = X.upload_vae(seed=int(golden["seed"][0]), ctx=ctx)
+    yield v
+    v.destroy()
+
+
+@pytest.mark.parametrize("case", [0, 1])
+def test_decode_against_reference_script(vae, golden, case):
+    """The whole decoder on the synthetic weights, against the pictures the
+    reference's inspect/ref_vae.py made from the same weights and latents."""
+    z = golden["latent_%d" % case]
+    h, w = z.shape[1:]
+    want = golden["picture_%d" % case]
+    got, ph, pw = X.vae_decode(vae, z, h, w)
+    assert (ph, pw) == (16 * h, 16 * w)
+    e, m = xo.rel_l2(got, want), float(np.abs(got - want).max())
+    say("decode %d x %d: rel-L2 %.2e, max |diff| %.4f (%.2f of 255)" % (h, w, e, m, m * 127.5))
+    assert e < 1e-2 and m <= PICTURE_MAX
+
+
+def test_decode_square_against_oracle(vae, golden):
+    """A 4 x 4 latent (a 64 x 64 picture: every stage with several tiles of
+    pixels), against the oracle on the same weights."""
+    z = vo.synth_latent(21, 4, 4)
+    got, _, _ = X.vae_decode(vae, z, 4, 4)
+    want = vo.decode(vo.SynthVae(int(golden["seed"][0])), z)
+    e, m = xo.rel_l2(got, want), float(np.abs(got - want).max())
+    say("decode 4 x 4: rel-L2 %.2e, max |diff| %.4f (%.2f of 255)" % (e, m, m * 127.5))
+    assert e < 1e-2 and m <= PICTURE_MAX
+    # a second decode on the same scratch gives the same picture
+    again, _, _ = X.vae_decode(vae, z, 4, 4)
+    assert np.array_equal(again, got)
+
+
+def test_vae_set_and_check_errors(ctx):
+    v = X.Vae(ctx)
+    with pytest.raises(X.ExnError) as e:
+        v.check()
+    assert e.value.code == X.ESTATE and "missing conv2.weight" in str(e.value)
+    with pytest.raises(X.ExnError) as e:
+        v.set("decoder.conv1.weight", X.F32, np.zeros(10, np.float32), (1152, 64, 3, 3))
+    assert e.value.code == X.EINVAL and "not (1152 64 1 3 3)" in str(e.value)
+    with pytest.raises(X.ExnError) as e:
+        v.set("decoder.nothing", X.F32, np.zeros(1, np.float32), (1,))
+    assert e.value.code == X.EINVAL
+    v.set("decoder.head.2.bias", X.BF16, xo.bf16_bits(np.array([0.5, -0.25, 0, 1], np.float32)), (4,))
+    v.destroy()
