@@ -242,3 +242,25 @@ def test_full_shapes_two_blocks(ctx, case):
     say("velocity rel-L2: uncached %.2e, cached %.2e, cached vs uncached %.2e" % (e0, e1, e01))
     assert e0 < 1e-2 and e1 < 1e-2 and e01 < 1e-5
     d.destroy()
+
+
+def test_cfg2_eight_steps_full_depth(ctx):
+    """The 1024^2 workload end to end: 32 blocks, 4096 image rows over 256 text rows, the
+    first step's velocity (uncached, <= 1e-2) and the final latent after the 8 Turbo steps
+    of the device Euler loop (<= 2e-2), against the oracle's run cached as float16 in
+    tests/golden/dit_cfg2_8step.npz (about 75 minutes of numpy)."""
+    g = np.load(os.path.join(GOLDEN, "dit_cfg2_8step.npz"))
+    seed, p, h, w = (int(v) for v in g["meta"])
+    say("cfg2: 32 blocks, p", p, "image", h, "x", w, "8 steps")
+    d = model(ctx, 32, seed)
+    d.resident(True)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    v0 = X.dit_velocity(d, ctxa, p, lat, h, w, xo.TURBO_SIGMAS[0])
+    e0 = xo.rel_l2(v0, g["v_step0"].astype(np.float32))
+    zd, cd = X.DevBuf.of(ctx, lat), X.DevBuf.of(ctx, ctxa)
+    sg = np.array(xo.TURBO_SIGMAS, np.float64)
+    X.call("exn_dit_generate_dev", d.h, cd.h, p, zd.h, h, w, X.ptr(sg), len(sg), 0, None, 0, 0)
+    ez = xo.rel_l2(zd.get(), g["z_final"].astype(np.float32))
+    say("cfg2: step-0 velocity rel-L2 %.2e, final latent rel-L2 %.2e" % (e0, ez))
+    assert e0 < 1e-2 and ez < 2e-2
+    d.destroy()
