@@ -16,6 +16,9 @@ WRITE_SIZE (profiles/), or null.
 
 cpu_baseline: the oracle (oracle/exn_oracle.py, numpy fp32) timed on this
 host for one cached block of the same workload, x32 blocks (extrapolated).
+
+vae_decode_1024sq: the VAE decoder (synthetic bf16 weights) on the 8-step loop's
+final latent, 64 x 64 -> a 1024 x 1024 RGBA picture, the mean of 5 decodes.
 """
 import argparse
 import json
@@ -37,6 +40,7 @@ LAYERS = 32
 SEED = 2
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_1024sq_traffic.json")
 PROBE_BYTES = 1 << 30         # --copy-probe 1024
+VAE_FLOP = 17.03e12           # one decode of a 64 x 64 latent: every convolution and the attention's products
 
 
 def gemm_flops_per_row():
@@ -236,6 +240,23 @@ def main():
     zf = z.get()
     finite = bool(np.isfinite(zf).all())
 
+    # the picture: the VAE decoder (synthetic bf16 weights) on the loop's final latent,
+    # 64 x 64 -> 1024 x 1024 RGBA, with the latent and the picture in HBM
+    vae = X.upload_vae(seed=SEED, ctx=ctx)
+    pic = X.DevBuf(ctx, (16 * H, 16 * W, 4), np.float32)
+    for i in range(2):
+        X.call("exn_vae_decode_dev", vae.h, z.h, H, W, pic.h)
+    ctx.sync()
+    VAE_REPS = 5
+    t0 = time.perf_counter()
+    for i in range(VAE_REPS):
+        X.call("exn_vae_decode_dev", vae.h, z.h, H, W, pic.h)
+    ctx.sync()
+    t_vae = (time.perf_counter() - t0) / VAE_REPS
+    px = pic.get()
+    vae_w, vae_s = vae.memory()
+    vae.destroy()
+
     gemm_f, att_f, tot_f = step_flops(True)
     tflops = tot_f / (ms * 1e-3) / 1e12
     gu_ms, gu_n, gu_f, gu_b = gu_timed
@@ -266,6 +287,12 @@ def main():
         "host_boundary_velocity_ms": round(t_host, 3),
         "final_latent_finite": finite, "ref_rtx3090_ms_per_step": 1187.5,
         "kernels": kernels,
+        "vae_decode_1024sq": {"ms": round(t_vae * 1e3, 2), "tflop": round(VAE_FLOP / 1e12, 2),
+                              "tflops": round(VAE_FLOP / t_vae / 1e12, 1),
+                              "mfma_peak_frac": round(VAE_FLOP / t_vae / 1e12 / PEAK_TFLOPS, 4),
+                              "picture_finite": bool(np.isfinite(px).all()),
+                              "weights_gb": round(vae_w / 1e9, 3), "scratch_gb": round(vae_s / 1e9, 2),
+                              "ref_rtx3090_ms": 1500.0},
         "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights (resident expansion of Q8_0)",
                      "achieved": round(achieved, 1) if achieved else None, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4) if achieved else None, "traffic": traffic,
