@@ -1620,11 +1620,13 @@ int exn_vae_memory(exn_vae* v, int64_t* weights, int64_t* scratch) {
 // one convolution of the decoder: NAME's weights and bias over X (bf16 pixel rows, h x w of the
 // output), RES added when given
 static int vae_conv_named(exn_vae* v, const std::string& name, int up, int out, const uint16_t* x, const float* res,
-                          void* y, int h, int w) {
+                          void* y, int h, int w, const float* keep = nullptr, int kcin = 0, int ft = 0,
+                          uint16_t* y2 = nullptr) {
   const VT* wt = vae_t(v, name + ".weight");
   const VT* b = vae_t(v, name + ".bias");
   if (!wt || !b) FAIL(EXN_ESTATE, "decoder: missing %s", name.c_str());
-  HIPCHK(vae_conv(v->ctx->stream, wt->taps, up, out, x, (const uint16_t*)wt->p, (const float*)b->p, res, y, h, w,
+  const VaeEpi ep{res, keep, kcin, ft, y2};
+  HIPCHK(vae_conv(v->ctx->stream, wt->taps, up, out, x, (const uint16_t*)wt->p, (const float*)b->p, ep, y, h, w,
                   wt->ci, (int)wt->o, wt->kp));
   return EXN_OK;
 }
@@ -1635,21 +1637,27 @@ static const float* vae_vec(const exn_vae* v, const std::string& name) {
 }
 
 // OUT = conv(silu(norm(conv(silu(norm(X)))))) + (X, or its 1 x 1 shortcut): src/cuda-vae.lisp's
-// resblock, inspect/ref_vae.py:59-65.  T1/U bf16 scratch, T2 fp32 scratch.
-static int vae_resblock(exn_vae* v, const std::string& p, const float* x, float* out, int i, int o, int h, int w,
-                        uint16_t* t1, float* t2, uint16_t* u) {
+// resblock, inspect/ref_vae.py:59-65.  OUT fp32, or bf16 when OUT_BF16 (a product's input next);
+// XB: X in bf16 when the caller has it (the shortcut's input), else cast here.  T1/U bf16
+// scratch, T2 fp32 scratch.
+static int vae_resblock(exn_vae* v, const std::string& p, const float* x, const uint16_t* xb, void* out, bool out_bf16,
+                        int i, int o, int h, int w, uint16_t* t1, float* t2, uint16_t* u) {
   hipStream_t s = v->ctx->stream;
   const int64_t n = (int64_t)h * w;
   const float* g0 = vae_vec(v, p + ".residual.0.gamma");
   const float* g3 = vae_vec(v, p + ".residual.3.gamma");
   if (!g0 || !g3) FAIL(EXN_ESTATE, "decoder: missing %s gammas", p.c_str());
+  const int oo = out_bf16 ? VAE_BF16 : VAE_F32;
   HIPCHK(vae_rms_silu(s, n, i, x, g0, t1, 1));
-  TRY(vae_conv_named(v, p + ".residual.2", 0, 0, t1, nullptr, t2, h, w));
+  TRY(vae_conv_named(v, p + ".residual.2", 0, VAE_F32, t1, nullptr, t2, h, w));
   HIPCHK(vae_rms_silu(s, n, o, t2, g3, t1, 1));
-  if (i == o) return vae_conv_named(v, p + ".residual.6", 0, 0, t1, x, out, h, w);
-  HIPCHK(f32_to_bf16(s, x, u, n * i));
-  TRY(vae_conv_named(v, p + ".shortcut", 0, 0, u, nullptr, t2, h, w));
-  return vae_conv_named(v, p + ".residual.6", 0, 0, t1, t2, out, h, w);
+  if (i == o) return vae_conv_named(v, p + ".residual.6", 0, oo, t1, x, out, h, w);
+  if (!xb) {
+    HIPCHK(f32_to_bf16(s, x, u, n * i));
+    xb = u;
+  }
+  TRY(vae_conv_named(v, p + ".shortcut", 0, VAE_F32, xb, nullptr, t2, h, w));
+  return vae_conv_named(v, p + ".residual.6", 0, oo, t1, t2, out, h, w);
 }
 
 // one head over the n pixels, c wide (inspect/ref_vae.py:68-76): OUT = proj(softmax(q k^T /
@@ -1700,41 +1708,49 @@ static int vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba
     }
   }
   float *A, *B, *C, *t2;
-  uint16_t *t1, *u;
+  uint16_t *t1, *u, *xs;
   TRY(vae_buf(v, "A", (size_t)most * 4, (void**)&A));
   TRY(vae_buf(v, "B", (size_t)most * 4, (void**)&B));
   TRY(vae_buf(v, "C", (size_t)most * 4, (void**)&C));
   TRY(vae_buf(v, "t2", (size_t)most * 4, (void**)&t2));
   TRY(vae_buf(v, "t1", (size_t)most * 2, (void**)&t1));
   TRY(vae_buf(v, "u", (size_t)most * 2, (void**)&u));
+  TRY(vae_buf(v, "xs", (size_t)most * 2, (void**)&xs));
   int hh = h, ww = w;
   const int64_t n0 = (int64_t)h * w;
   // the latent's pixels, conv2 (1 x 1), decoder.conv1 (3 x 3 to the top width)
   HIPCHK(vae_latent_pixels(s, n0, kVaeZ, latent, t1));
-  TRY(vae_conv_named(v, "conv2", 0, 1, t1, nullptr, u, hh, ww));
-  TRY(vae_conv_named(v, "decoder.conv1", 0, 0, u, nullptr, A, hh, ww));
-  TRY(vae_resblock(v, "decoder.middle.0", A, B, top, top, hh, ww, t1, t2, u));
+  TRY(vae_conv_named(v, "conv2", 0, VAE_BF16, t1, nullptr, u, hh, ww));
+  TRY(vae_conv_named(v, "decoder.conv1", 0, VAE_F32, u, nullptr, A, hh, ww));
+  TRY(vae_resblock(v, "decoder.middle.0", A, nullptr, B, false, top, top, hh, ww, t1, t2, u));
   TRY(vae_attention(v, "decoder.middle.1", B, C, hh, ww, top, t1));
-  TRY(vae_resblock(v, "decoder.middle.2", C, A, top, top, hh, ww, t1, t2, u));
+  TRY(vae_resblock(v, "decoder.middle.2", C, nullptr, A, false, top, top, hh, ww, t1, t2, u));
   char p[96];
+  const uint16_t* a_bf16 = nullptr;   // A in bf16, when the step that wrote A kept a copy
   for (int si = 0; si < 5; ++si) {
     const VStage& st = kVaeStages[si];
-    // A holds the stage's input, kept for DupUp3D
+    // A holds the stage's input, kept for DupUp3D; the last block of an upsampling stage
+    // writes bf16 straight for the resample convolution
     snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.0", si);
-    TRY(vae_resblock(v, p, A, B, st.in, st.out, hh, ww, t1, t2, u));
+    TRY(vae_resblock(v, p, A, a_bf16, B, false, st.in, st.out, hh, ww, t1, t2, u));
     snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.1", si);
-    TRY(vae_resblock(v, p, B, C, st.out, st.out, hh, ww, t1, t2, u));
+    TRY(vae_resblock(v, p, B, nullptr, C, false, st.out, st.out, hh, ww, t1, t2, u));
     snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.2", si);
-    TRY(vae_resblock(v, p, C, B, st.out, st.out, hh, ww, t1, t2, u));
     if (st.up) {
-      HIPCHK(f32_to_bf16(s, B, u, (int64_t)hh * ww * st.out));
+      TRY(vae_resblock(v, p, C, nullptr, u, true, st.out, st.out, hh, ww, t1, t2, u));
+      // nearest x2 folded into the convolution's loads, DupUp3D of the stage's input into its
+      // store, and a bf16 copy when the next stage's first block takes a 1 x 1 shortcut of it
+      const bool copy = si + 1 < 5 && kVaeStages[si + 1].in != kVaeStages[si + 1].out;
       snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.3.resample.1", si);
-      TRY(vae_conv_named(v, p, 1, 0, u, nullptr, C, 2 * hh, 2 * ww));
-      HIPCHK(vae_dupup_add(s, st.in, st.out, st.tup ? 2 : 1, hh, ww, A, C));
+      TRY(vae_conv_named(v, p, 1, VAE_DUPUP, u, nullptr, C, 2 * hh, 2 * ww, A, st.in, st.tup ? 2 : 1,
+                         copy ? xs : nullptr));
+      a_bf16 = copy ? xs : nullptr;
       hh *= 2;
       ww *= 2;
       std::swap(A, C);
     } else {
+      TRY(vae_resblock(v, p, C, nullptr, B, false, st.out, st.out, hh, ww, t1, t2, u));
+      a_bf16 = nullptr;
       std::swap(A, B);
     }
   }
@@ -1742,7 +1758,7 @@ static int vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba
   const float* g = vae_vec(v, "decoder.head.0.gamma");
   if (!g) FAIL(EXN_ESTATE, "decoder: missing decoder.head.0.gamma");
   HIPCHK(vae_rms_silu(s, (int64_t)hh * ww, kVaeStages[4].out, A, g, t1, 1));
-  return vae_conv_named(v, "decoder.head.2", 0, 2, t1, nullptr, rgba, hh, ww);
+  return vae_conv_named(v, "decoder.head.2", 0, VAE_CLAMP, t1, nullptr, rgba, hh, ww);
 }
 
 extern "C" {
@@ -1778,7 +1794,8 @@ int exn_vae_conv(exn_ctx* ctx, int taps, int up, int outdt, const uint16_t* x, c
   TRY(use(ctx));
   if (!x || !wt || !bias || !y || (taps != 1 && taps != 9) || outdt < 0 || outdt > 2)
     FAIL(EXN_EINVAL, "vae conv arguments");
-  const hipError_t e = vae_conv(ctx->stream, taps, up, outdt, x, wt, bias, res, y, h, w, c, cout, kp);
+  const VaeEpi ep{res, nullptr, 0, 0, nullptr};
+  const hipError_t e = vae_conv(ctx->stream, taps, up, outdt, x, wt, bias, ep, y, h, w, c, cout, kp);
   if (e == hipErrorInvalidValue)
     FAIL(EXN_EINVAL, "vae conv: taps %d up %d out %d, %d x %d x %d -> %d, kp %d", taps, up, outdt, h, w, c, cout, kp);
   HIPCHK(e);

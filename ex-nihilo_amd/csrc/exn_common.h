@@ -192,10 +192,18 @@ hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float d
 hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out,
                   int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale);
 
-// the VAE decoder (vae.hip).  vae_conv: out 0 fp32 (+ bias, + res), 1 bf16 (+ bias), 2 fp32
-// (+ bias) clamped to -1 .. 1; taps 9 or 1; up: the input is the half-size picture
+// the VAE decoder (vae.hip).  vae_conv's outputs: fp32 (+ bias, + res when given), bf16 (+ bias,
+// + res when given), fp32 (+ bias) clamped to -1 .. 1, fp32 (+ bias, + DupUp3D of keep: kcin
+// channels at half size, frame ft - 1 of ft); taps 9 or 1; up: the input is the half-size picture
+enum VaeOut { VAE_F32 = 0, VAE_BF16 = 1, VAE_CLAMP = 2, VAE_DUPUP = 3 };
+struct VaeEpi {
+  const float* res;    // VAE_F32 / VAE_BF16: added when not null (the output's layout)
+  const float* keep;   // VAE_DUPUP: the stage's input, pixel rows of kcin
+  int kcin, ft;
+  uint16_t* y2;        // VAE_F32 / VAE_DUPUP: when not null, a bf16 copy of the output too
+};
 hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
-                    const float* bias, const float* res, void* y, int h, int w, int c, int cout, int kp);
+                    const float* bias, const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp);
 hipError_t vae_rms_silu(hipStream_t s, int64_t P, int C, const float* x, const float* gamma, uint16_t* y, int silu);
 hipError_t vae_dupup_add(hipStream_t s, int cin, int cout, int ft, int h, int w, const float* x, float* y);
 hipError_t vae_latent_pixels(hipStream_t s, int64_t P, int C, const float* z, uint16_t* y);

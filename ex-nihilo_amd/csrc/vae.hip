@@ -34,20 +34,36 @@ __device__ __forceinline__ void conv_dma(const void* base, uint32_t extent, lds_
 }
 
 #define VBM 256
-#define VBN 144
-#define VSTAGE (VBM * 128 + VBN * 128)   // A rows | B rows, 64 bf16 of K each: 51200 bytes
-#define VOFF_NONE 0x80000000u            // past any extent: the load reads zeros
+#define VOFF_NONE 0x80000000u   // past any extent: the load reads zeros
+#define VEPI_LDS (8 * 32 * 148 * 4)   // the epilogue's staging: 8 waves x 32 pixels x 148 floats
 
-// OUT: 0 fp32 (+ bias, + res when given), 1 bf16 (+ bias), 2 fp32 (+ bias) clamped to -1 .. 1
-template <int TAPS, int UP, int OUT>
+// Tiles of 256 pixels x BN output channels, BN = 144 (3 LDS stages) or 288 (2 stages; the
+// widths that 288 divides): 8 waves of WM pixels x 144 channels, each a (WM/16) x 9 grid of
+// v_mfma_f32_16x16x32_bf16 -- 0.61 fragment reads an MFMA at BN 144, 0.36 at BN 288.
+template <int BN>
+struct ConvTile {
+  static constexpr int NWN = BN / 144, NWM = 8 / NWN, WM = VBM / NWM, MI = WM / 16;
+  static constexpr int STAGE = VBM * 128 + BN * 128;   // A rows | B rows, 64 bf16 of K each
+  static constexpr int NST = BN == 144 ? 3 : 2;
+  static constexpr int BFULL = BN * 8 / 512;           // full B DMA rounds a step
+  static constexpr int BREM = (BN * 8 - 512 * BFULL) / 8;   // lanes a wave in the partial round
+  static constexpr int NDMA = 4 + BFULL + 1;           // DMA instructions a wave a step
+  static constexpr int LDS = NST * STAGE > VEPI_LDS ? NST * STAGE : VEPI_LDS;
+};
+
+// OUT: VAE_F32 fp32 (+ bias, + res when given), VAE_BF16 bf16 (+ bias, + res when given),
+// VAE_CLAMP fp32 (+ bias) clamped to -1 .. 1, VAE_DUPUP fp32 (+ bias, + DupUp3D of keep)
+template <int BN, int TAPS, int UP, int OUT>
 __global__ void __launch_bounds__(512)
 k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
-       const float* __restrict__ res, void* __restrict__ Y, int H, int W, int C, int cout, int Kp) {
+       VaeEpi ep, void* __restrict__ Y, int H, int W, int C, int cout, int Kp) {
+  typedef ConvTile<BN> T;
   extern __shared__ __align__(1024) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % T::NWM, wn = wave / T::NWM;
   const int P = H * W;
-  const int m0 = blockIdx.x * VBM, n0 = blockIdx.y * VBN;
+  const int m0 = blockIdx.x * VBM, n0 = blockIdx.y * BN;
   const int KT = Kp / 64;
   const int Hs = UP ? H >> 1 : H, Ws = UP ? W >> 1 : W;
   const uint32_t xext = (uint32_t)((int64_t)Hs * Ws * C * 2);
@@ -68,17 +84,19 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
     tp[i] = k / C;
     cc[i] = k - tp[i] * C;
   }
-  // B: rounds 0 and 1 move rows 64 rd + 8 wave + lane / 8, round 2 rows 128 + 2 wave + lane / 8
-  // (lanes 0..15): 144 rows, the same three DMA instructions in every wave
-  uint32_t boff[3];
+  // B: full rounds move rows 64 rd + 8 wave + lane / 8; the partial round rows
+  // 64 BFULL + (BREM / 8) wave + lane / 8 for the first BREM lanes: every wave issues the same
+  // number of DMA instructions
+  uint32_t boff[T::BFULL + 1];
 #pragma unroll
-  for (int rd = 0; rd < 3; ++rd) {
-    const int row = rd < 2 ? 64 * rd + 8 * wave + (lane >> 3) : 128 + 2 * wave + ((lane >> 3) & 1);
+  for (int rd = 0; rd <= T::BFULL; ++rd) {
+    const int row = rd < T::BFULL ? 64 * rd + 8 * wave + (lane >> 3)
+                                  : 64 * T::BFULL + (T::BREM / 8) * wave + ((lane >> 3) % (T::BREM / 8));
     boff[rd] = (uint32_t)((row * Kp + 8 * ((lane & 7) ^ ((row >> 1) & 7))) * 2);
   }
   // issue the next k-step's tiles into stage s (the A chunks' positions then move on)
   auto dma = [&](int t, int s) {
-    uint8_t* st = smem + s * VSTAGE;
+    uint8_t* st = smem + s * T::STAGE;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tap = tp[i];
@@ -102,114 +120,188 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
         tp[i] += 1;
       }
     }
-    conv_dma(wbase, wext, (lds_void*)(st + 32768 + wave * 1024), boff[0], t * 128);
-    conv_dma(wbase, wext, (lds_void*)(st + 32768 + 8192 + wave * 1024), boff[1], t * 128);
-    if (lane < 16) conv_dma(wbase, wext, (lds_void*)(st + 32768 + 16384 + wave * 256), boff[2], t * 128);
+#pragma unroll
+    for (int rd = 0; rd < T::BFULL; ++rd)
+      conv_dma(wbase, wext, (lds_void*)(st + 32768 + rd * 8192 + wave * 1024), boff[rd], t * 128);
+    if (lane < T::BREM)
+      conv_dma(wbase, wext, (lds_void*)(st + 32768 + T::BFULL * 8192 + wave * T::BREM * 16), boff[T::BFULL], t * 128);
   };
 
   // fragments: lane holds row lo of a 16-row block, K 8 q4 .. of a slice of 32
   const int lo = lane & 15, q4 = lane >> 4, fs = (lo >> 1) & 7;
-  const int a_rd = (32 * wave + lo) * 128, b_rd = 32768 + lo * 128;
-  f32x4 acc[2][9];
+  const int a_rd = (T::WM * wm + lo) * 128, b_rd = 32768 + (144 * wn + lo) * 128;
+  f32x4 acc[T::MI][9];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < T::MI; ++i)
 #pragma unroll
     for (int j = 0; j < 9; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  dma(0, 0);
-  dma(min(1, KT - 1), 1);   // every step issues seven DMA instructions a wave, so vmcnt(7) below
-  int s = 0;
-  for (int t = 0; t < KT; ++t) {
-    // step t has landed for every wave, and every wave is done with stage (t + 2) % 3
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((7 & 0xF) | (0x7 << 4) | (0x0 << 8));   // vmcnt(7) lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    const int s2 = s >= 1 ? s - 1 : 2;   // (t + 2) % 3
-    dma(min(t + 2, KT - 1), s2);         // past the end: a harmless reload, never read
-    const uint8_t* st = smem + s * VSTAGE;
+  auto step = [&](const uint8_t* st) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int co = ((4 * kk + q4) ^ fs) << 4;
-      bf16x8 a[2], b[9];
+      bf16x8 a[T::MI];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = *(const bf16x8*)(st + a_rd + i * 2048 + co);
+      for (int i = 0; i < T::MI; ++i) a[i] = *(const bf16x8*)(st + a_rd + i * 2048 + co);
 #pragma unroll
-      for (int j = 0; j < 9; ++j) b[j] = *(const bf16x8*)(st + b_rd + j * 2048 + co);
+      for (int j = 0; j < 9; ++j) {
+        const bf16x8 b = *(const bf16x8*)(st + b_rd + j * 2048 + co);
 #pragma unroll
-      for (int j = 0; j < 9; ++j)
-#pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < T::MI; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][j], 0, 0, 0);
+      }
     }
-    s = s == 2 ? 0 : s + 1;
+  };
+
+  if constexpr (T::NST == 3) {
+    dma(0, 0);
+    dma(min(1, KT - 1), 1);   // every step issues NDMA instructions a wave, so vmcnt(NDMA) below
+    int s = 0;
+    for (int t = 0; t < KT; ++t) {
+      // step t has landed for every wave, and every wave is done with stage (t + 2) % 3
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt((T::NDMA & 0xF) | (0x7 << 4) | (0x0 << 8));   // vmcnt(NDMA) lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      dma(min(t + 2, KT - 1), s >= 1 ? s - 1 : 2);   // into (t + 2) % 3; past the end a reload, never read
+      step(smem + s * T::STAGE);
+      s = s == 2 ? 0 : s + 1;
+    }
+  } else {
+    dma(0, 0);
+    for (int t = 0; t < KT; ++t) {
+      // step t has landed for every wave, and every wave is done with the other stage
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // vmcnt(0) lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      dma(min(t + 1, KT - 1), (t + 1) & 1);   // past the end a reload, never read
+      step(smem + (t & 1) * T::STAGE);
+    }
   }
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // no DMA left in flight
   asm volatile("" ::: "memory");
 
-  // lane holds rows 4 q4 .. +3 of each 16 x 16 tile, column lo
+  // The epilogue through LDS (free now), 32 of the wave's pixels at a time: the wave stages its
+  // 32 x 144 block (row stride 148 floats), then moves it as 16-byte chunks, 4 channels of one
+  // pixel a lane: bias, and the residual or the DupUp3D gather, loaded for a batch of chunks
+  // before any of their stores.
+  float* stg = (float*)smem + wave * (32 * 148);
+  const float winv = 1.f / (float)W;
+  const int rsh = OUT == VAE_DUPUP ? __builtin_ctz((unsigned)(cout * ep.ft * 4 / ep.kcin)) : 0;
 #pragma unroll
-  for (int j = 0; j < 9; ++j) {
-    const int n = n0 + 16 * j + lo;
-    if (n >= cout) continue;
-    const float bn = bias[n];
+  for (int half = 0; half < T::MI / 2; ++half) {
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 9; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 32 * wave + 16 * i + 4 * q4 + r;
-        if (m >= P) continue;
-        const int64_t at = (int64_t)m * cout + n;
-        float v = acc[i][j][r] + bn;
-        if constexpr (OUT == 0) {
-          if (res) v += res[at];
-          ((float*)Y)[at] = v;
-        } else if constexpr (OUT == 1) {
-          ((uint16_t*)Y)[at] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
-        } else {
-          ((float*)Y)[at] = fminf(1.f, fmaxf(-1.f, v));
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) stg[(16 * i + 4 * q4 + r) * 148 + 16 * j + lo] = acc[2 * half + i][j][r];
+    __syncthreads();
+    // 18 chunks a lane, in batches of 6 (3 at BN 288, where half the accumulators are still live)
+    constexpr int CH = BN == 144 ? 6 : (OUT == VAE_DUPUP ? 2 : 3);
+#pragma unroll
+    for (int bt = 0; bt < 18 / CH; ++bt) {
+      f32x4 v[CH], add[CH];
+      int at[CH];
+      bool ok[CH];
+#pragma unroll
+      for (int q = 0; q < CH; ++q) {
+        const int k = (bt * CH + q) * 64 + lane, row = k / 36, c4 = k - row * 36;
+        const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + 144 * wn + 4 * c4;
+        ok[q] = m < P && n < cout;
+        const int mc = min(m, P - 1), nc = min(n, cout - 4);   // in bounds for the loads either way
+        at[q] = mc * cout + nc;
+        v[q] = *(const f32x4*)(stg + row * 148 + 4 * c4) + *(const f32x4*)(bias + nc);
+        add[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (OUT == VAE_DUPUP) {
+          // channel c of pixel (yy, xx) adds keep's channel j / rep of pixel (yy/2, xx/2),
+          // j = ((c ft + ft - 1) 2 + yy%2) 2 + xx%2, rep = cout ft 4 / kcin (a power of two)
+          int yy = (int)(((float)mc + 0.5f) * winv);   // mc / W, corrected to exact below
+          yy -= yy * W > mc;
+          yy += (yy + 1) * W <= mc;
+          const int xx = mc - yy * W;
+          const float* kr = ep.keep + (((yy >> 1) * (W >> 1) + (xx >> 1)) * ep.kcin);
+          const int j0 = ((nc * ep.ft + ep.ft - 1) * 2 + (yy & 1)) * 2 + (xx & 1);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) add[q][e] = kr[(j0 + 4 * ep.ft * e) >> rsh];
+        } else if constexpr (OUT == VAE_F32 || OUT == VAE_BF16) {
+          if (ep.res) add[q] = *(const f32x4*)(ep.res + at[q]);
         }
       }
+#pragma unroll
+      for (int q = 0; q < CH; ++q) {
+        if (!ok[q]) continue;
+        const f32x4 o = v[q] + add[q];
+        if constexpr (OUT == VAE_BF16) {
+          *(u32x2*)((uint16_t*)Y + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        } else if constexpr (OUT == VAE_CLAMP) {
+          f32x4 c;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) c[e] = fminf(1.f, fmaxf(-1.f, o[e]));
+          *(f32x4*)((float*)Y + at[q]) = c;
+        } else {
+          *(f32x4*)((float*)Y + at[q]) = o;
+          if constexpr (OUT == VAE_F32 || OUT == VAE_DUPUP) {
+            if (ep.y2) *(u32x2*)(ep.y2 + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          }
+        }
+      }
+    }
   }
 }
 
-template <int TAPS, int UP, int OUT>
-static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const float* res,
+template <int BN, int TAPS, int UP, int OUT>
+static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const VaeEpi& ep,
                               void* y, int h, int w, int c, int cout, int kp) {
-  auto kern = k_conv<TAPS, UP, OUT>;
+  auto kern = k_conv<BN, TAPS, UP, OUT>;
+  constexpr int lds = ConvTile<BN>::LDS;
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 3 * VSTAGE);
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  dim3 grid(grid_of((int64_t)h * w, VBM), grid_of(cout, VBN));
-  hipLaunchKernelGGL(kern, grid, dim3(512), 3 * VSTAGE, s, x, wt, bias, res, y, h, w, c, cout, kp);
+  dim3 grid(grid_of((int64_t)h * w, VBM), grid_of(cout, BN));
+  hipLaunchKernelGGL(kern, grid, dim3(512), lds, s, x, wt, bias, ep, y, h, w, c, cout, kp);
   return hipGetLastError();
 }
 
-hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt, const float* bias,
-                    const float* res, void* y, int h, int w, int c, int cout, int kp) {
-  // the loads move 8 channels at once and each k-step moves a chunk's tap at most once;
-  // every offset and extent fits 31 bits
-  if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || h <= 0 || w <= 0 || (up && (h % 2 || w % 2)) ||
-      ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || (int64_t)h * w * c * 2 >= ((int64_t)1 << 31) ||
-      (int64_t)cout * kp * 2 >= ((int64_t)1 << 31))
-    return hipErrorInvalidValue;
-  if (taps == 9 && !up && out == 0) return launch_conv<9, 0, 0>(s, x, wt, bias, res, y, h, w, c, cout, kp);
-  if (taps == 9 && !up && out == 1) return launch_conv<9, 0, 1>(s, x, wt, bias, res, y, h, w, c, cout, kp);
-  if (taps == 9 && !up && out == 2) return launch_conv<9, 0, 2>(s, x, wt, bias, res, y, h, w, c, cout, kp);
-  if (taps == 9 && up && out == 0) return launch_conv<9, 1, 0>(s, x, wt, bias, res, y, h, w, c, cout, kp);
-  if (taps == 1 && !up && out == 0) return launch_conv<1, 0, 0>(s, x, wt, bias, res, y, h, w, c, cout, kp);
-  if (taps == 1 && !up && out == 1) return launch_conv<1, 0, 1>(s, x, wt, bias, res, y, h, w, c, cout, kp);
+template <int BN>
+static hipError_t conv_bn(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
+                          const float* bias, const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp) {
+  if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (taps == 9 && !up && out == VAE_BF16) return launch_conv<BN, 9, 0, VAE_BF16>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (taps == 9 && !up && out == VAE_CLAMP) return launch_conv<BN, 9, 0, VAE_CLAMP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (taps == 9 && up && out == VAE_F32) return launch_conv<BN, 9, 1, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (taps == 9 && up && out == VAE_DUPUP) return launch_conv<BN, 9, 1, VAE_DUPUP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (taps == 1 && !up && out == VAE_F32) return launch_conv<BN, 1, 0, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (taps == 1 && !up && out == VAE_BF16) return launch_conv<BN, 1, 0, VAE_BF16>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
   return hipErrorInvalidValue;
+}
+
+hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt, const float* bias,
+                    const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp) {
+  // the loads move 8 channels at once and each k-step moves a chunk's tap at most once; the
+  // epilogue moves 4 channels at once; every offset and extent fits 31 bits
+  if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || cout % 4 || h <= 0 || w <= 0 ||
+      (up && (h % 2 || w % 2)) || ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || ((uintptr_t)y & 15) ||
+      ((uintptr_t)bias & 15) || ((uintptr_t)ep.res & 15) || ((uintptr_t)ep.y2 & 7) ||
+      (int64_t)h * w * c * 2 >= ((int64_t)1 << 31) || (int64_t)cout * kp * 2 >= ((int64_t)1 << 31) ||
+      (int64_t)h * w * cout >= ((int64_t)1 << 31) ||
+      (out == VAE_DUPUP && (!ep.keep || ep.ft < 1 || ep.kcin <= 0 || (int64_t)cout * ep.ft * 4 % ep.kcin || h % 2 ||
+                            w % 2 || ((cout * ep.ft * 4 / ep.kcin) & (cout * ep.ft * 4 / ep.kcin - 1)))))
+    return hipErrorInvalidValue;
+  // the wide tile where 288 divides the width (1152, 576, 288 and the 3456 of q|k|v)
+  if (cout % 288 == 0) return conv_bn<288>(s, taps, up, out, x, wt, bias, ep, y, h, w, c, cout, kp);
+  return conv_bn<144>(s, taps, up, out, x, wt, bias, ep, y, h, w, c, cout, kp);
 }
 
 // --- the bandwidth kernels ----------------------------------------------------------
 
 // y = x / max(|x|, 1e-12) * sqrt(C) * gamma over each pixel's C channels (src/cuda-vae.lisp's
 // v_rms with eps 1e-12; inspect/ref_vae.py:50-52), then SiLU when SILU; bf16 out.  LP lanes a
-// pixel (16 or 64), C a multiple of 4.
+// pixel, C a multiple of 4.
 template <int LP, int SILU>
 __global__ void __launch_bounds__(256)
 k_rms_silu(int64_t P, int C, const float* __restrict__ x, const float* __restrict__ gamma, uint16_t* __restrict__ y) {
@@ -238,8 +330,71 @@ k_rms_silu(int64_t P, int C, const float* __restrict__ x, const float* __restric
   }
 }
 
+// the sum of v over each group of LP lanes (4, 8, 16 or 32 aligned lanes), in every lane of it
+template <int LP>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f<0xB1>(v);                       // pairs
+  v += dpp_f<0x4E>(v);                       // quads
+  if constexpr (LP >= 8) v += dpp_f<0x141>(v);   // the two quads of a half row
+  if constexpr (LP >= 16) v += dpp_f<0x140>(v);  // the two halves of a row
+  if constexpr (LP >= 32) {
+    float a = v, b = v;
+    xswap16(a, b);
+    v = a + b;
+  }
+  return v;
+}
+
+// the decoder's widths, C = 36 LP (144, 288, 576, 1152): a lane holds 9 chunks of 4 channels in
+// registers, so x is read once
+template <int LP, int SILU>
+__global__ void __launch_bounds__(256)
+k_rms_silu9(int64_t P, const float* __restrict__ x, const float* __restrict__ gamma, uint16_t* __restrict__ y) {
+  constexpr int C = 36 * LP;
+  const int64_t p = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LP;
+  const int sub = threadIdx.x % LP;
+  const bool live = p < P;
+  const float* r = x + (live ? p : 0) * C;
+  f32x4 v[9];
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 9; ++q) {
+    v[q] = *(const f32x4*)(r + 4 * (sub + LP * q));
+    ss += (v[q][0] * v[q][0] + v[q][1] * v[q][1]) + (v[q][2] * v[q][2] + v[q][3] * v[q][3]);
+  }
+  ss = group_sum<LP>(ss);
+  const float inv = sqrtf((float)C) / fmaxf(sqrtf(ss), 1e-12f);
+  if (!live) return;
+  uint16_t* o = y + p * C;
+#pragma unroll
+  for (int q = 0; q < 9; ++q) {
+    const int c = 4 * (sub + LP * q);
+    const f32x4 g = *(const f32x4*)(gamma + c);
+    float e[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      e[k] = v[q][k] * inv * g[k];
+      if constexpr (SILU) e[k] = silu_bf16out(e[k]);
+    }
+    *(u32x2*)(o + c) = u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])};
+  }
+}
+
+template <int LP>
+static void launch_rms9(hipStream_t s, int64_t P, const float* x, const float* gamma, uint16_t* y, int silu) {
+  const unsigned g = grid_of(P * LP, 256);
+  if (silu) hipLaunchKernelGGL((k_rms_silu9<LP, 1>), dim3(g), dim3(256), 0, s, P, x, gamma, y);
+  else hipLaunchKernelGGL((k_rms_silu9<LP, 0>), dim3(g), dim3(256), 0, s, P, x, gamma, y);
+}
+
 hipError_t vae_rms_silu(hipStream_t s, int64_t P, int C, const float* x, const float* gamma, uint16_t* y, int silu) {
   if (C % 4 || P <= 0) return P == 0 ? hipSuccess : hipErrorInvalidValue;
+  switch (C) {
+    case 144: launch_rms9<4>(s, P, x, gamma, y, silu); return hipGetLastError();
+    case 288: launch_rms9<8>(s, P, x, gamma, y, silu); return hipGetLastError();
+    case 576: launch_rms9<16>(s, P, x, gamma, y, silu); return hipGetLastError();
+    case 1152: launch_rms9<32>(s, P, x, gamma, y, silu); return hipGetLastError();
+  }
   if (C <= 512) {
     const unsigned g = grid_of(P * 16, 256);
     if (silu) hipLaunchKernelGGL((k_rms_silu<16, 1>), dim3(g), dim3(256), 0, s, P, C, x, gamma, y);
