@@ -19,6 +19,11 @@ host for one cached block of the same workload, x32 blocks (extrapolated).
 
 vae_decode_1024sq: the VAE decoder (synthetic bf16 weights) on the 8-step loop's
 final latent, 64 x 64 -> a 1024 x 1024 RGBA picture, the mean of 5 decodes.
+
+    python bench.py --vae-only [--steps K] [--warmup W]
+
+times the VAE decoder alone on a seeded 64 x 64 latent (K decodes after W) and
+prints its own JSON line.
 """
 import argparse
 import json
@@ -134,12 +139,44 @@ def traffic_from(fetch_db, write_db):
     print(json.dumps(rec))
 
 
+def vae_only(steps, warmup):
+    """The VAE decoder alone: a seeded 64 x 64 latent in HBM -> a 1024 x 1024 RGBA picture."""
+    import exn_hip as X
+    rng = np.random.default_rng(SEED)
+    ctx = X.Context(0)
+    vae = X.upload_vae(seed=SEED, ctx=ctx)
+    z = X.DevBuf.of(ctx, rng.normal(0, 1, (64, H, W)).astype(np.float32))
+    pic = X.DevBuf(ctx, (16 * H, 16 * W, 4), np.float32)
+    for i in range(warmup):
+        X.call("exn_vae_decode_dev", vae.h, z.h, H, W, pic.h)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        X.call("exn_vae_decode_dev", vae.h, z.h, H, W, pic.h)
+    ctx.sync()
+    t = (time.perf_counter() - t0) / steps
+    px = pic.get()
+    vae_w, vae_s = vae.memory()
+    vae.destroy()
+    ctx.close()
+    print(json.dumps({"metric": "VAE decode ms @1024² (64x64x64 latent -> 1024x1024 RGBA), 1 GPU",
+                      "value": round(t * 1e3, 3), "unit": "ms/decode", "n_gpus": 1, "steps": steps,
+                      "warmup": warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+                      "config": {"workload": "vae-decode-64x64-latent", "weights": "bf16 synthetic", "seed": SEED},
+                      "tflop": round(VAE_FLOP / 1e12, 2), "tflops": round(VAE_FLOP / t / 1e12, 1),
+                      "mfma_peak_frac": round(VAE_FLOP / t / 1e12 / PEAK_TFLOPS, 4),
+                      "picture_finite": bool(np.isfinite(px).all()),
+                      "weights_gb": round(vae_w / 1e9, 3), "scratch_gb": round(vae_s / 1e9, 2),
+                      "ref_rtx3090_ms": 1500.0}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--vae-only", action="store_true", help="time the VAE decoder alone")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="copy MIB MiB device to device after the set-up (the traffic counters' calibration)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
@@ -152,6 +189,9 @@ def main():
         print("bench.py: this build measures one GPU; --gpus %d is not supported (the step shards over image "
               "rows across GPUs only by design, see DESIGN.md)" % a.gpus, file=sys.stderr)
         sys.exit(2)
+    if a.vae_only:
+        vae_only(a.steps, a.warmup)
+        return
 
     import exn_hip as X
     ctx = X.Context(0)
