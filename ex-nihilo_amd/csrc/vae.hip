@@ -15,10 +15,12 @@
 // half-size picture and the neighbour's pixel is halved: the nearest x2
 // upsampling (x_up2) folded into the resample convolution's loads.
 //
-// Tiles: 256 pixels x 144 output channels a workgroup (144 divides every
-// width of the decoder: 1152, 576, 288, 144), 8 waves of 32 pixels x 144,
-// each a 2 x 9 grid of v_mfma_f32_16x16x32_bf16; K 64 a step, three LDS
-// stages (50 KB each) so that a step's DMA has two steps to land.
+// Tiles: 256 pixels x 288 output channels a workgroup where 288 divides the
+// width (1152, 576, 288), else 256 x 144 (144 divides every width of the
+// decoder); 8 waves of 144 channels each, v_mfma_f32_16x16x32_bf16; K 64 a
+// step, two LDS stages (72 KB each) at 288, three (50 KB each) at 144.  The
+// epilogue stages each wave's accumulators through LDS 32 pixels at a time,
+// so that bias, residual, DupUp3D and clamp are applied to 16-byte rows.
 #include "exn_common.h"
 
 namespace exn {
