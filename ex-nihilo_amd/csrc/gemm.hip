@@ -264,17 +264,16 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ int chunk_swz(int r) { return (r >> 1) & 7; }
 
-// The epilogue through LDS (free once the main loop is done): a wave's 128 x 64
-// accumulators go out 32 rows at a time into its own 32 x 72-float LDS block (rows 288
-// bytes apart), and come back as 4 consecutive columns a lane, so every global access
-// is 16 bytes (8 for bf16/fp16) and a wave's instruction covers whole rows.  Needs
-// N % 4 == 0, LDY % 4 == 0.
+// The epilogue through LDS (free once the main loop is done): a wave's (16 MI) x (16 NI)
+// accumulators go out 32 rows at a time into its own 32 x (16 NI + 8)-float LDS block, and
+// come back as 4 consecutive columns a lane, so every global access is 16 bytes (8 for
+// bf16/fp16) and a wave's instruction covers whole rows.  Needs N % 4 == 0, LDY % 4 == 0.
 template <int EPI, int MI, int NI>
 __device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* stage, int64_t wrow, int64_t wcol,
                                              int lane, int64_t M, int64_t N, const EpiArgs& ea) {
-  constexpr int LS = 72;
-  // this lane's 4 columns (SwiGLU: 4 output columns of 8 lanes a row; others 16 lanes a row)
-  constexpr int LPR = EPI == EPI_SWIGLU ? 8 : 16;
+  constexpr int LS = 16 * NI + 8;
+  // this lane's 4 columns (SwiGLU: 4 output columns, 8 NI / 4 lanes a row; others 16 NI / 4)
+  constexpr int LPR = EPI == EPI_SWIGLU ? 2 * NI : 4 * NI;
   const int c4 = (lane % LPR) * 4;
   f32x4 g0 = {0.f, 0.f, 0.f, 0.f}, g1 = g0;
   if constexpr (EPI == EPI_GATE_ADD) {
@@ -303,17 +302,20 @@ __device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* 
       const int row = it * (64 / LPR) + lane / LPR;
       const int64_t m = wrow + 32 * i2 + row;
       if (m >= M) continue;
-      const f32x4 v = *(const f32x4*)(stage + row * LS + c4);
       if constexpr (EPI == EPI_SWIGLU) {
-        const int64_t col = wcol / 2 + c4;   // output column: gate at c4, up at 32 + c4 of the LDS row
+        // output column wcol/2 + c4: its gate at 64 (c4/32) + c4%32 of the LDS row, its up 32 on
+        const int64_t col = wcol / 2 + c4;
         if (2 * (col - c4) >= N) continue;
-        const f32x4 u = *(const f32x4*)(stage + row * LS + 32 + c4);
+        const int gc = 64 * (c4 >> 5) + (c4 & 31);
+        const f32x4 v = *(const f32x4*)(stage + row * LS + gc);
+        const f32x4 u = *(const f32x4*)(stage + row * LS + gc + 32);
         uint16_t* y = (uint16_t*)ea.y + m * ea.ldy + col;
         *(u32x2*)y = u32x2{pack_bf16x2(silu_bf16out(v[0]) * u[0], silu_bf16out(v[1]) * u[1]),
                            pack_bf16x2(silu_bf16out(v[2]) * u[2], silu_bf16out(v[3]) * u[3])};
       } else {
         const int64_t n = wcol + c4;
         if (n >= N) continue;
+        const f32x4 v = *(const f32x4*)(stage + row * LS + c4);
         if constexpr (EPI == EPI_F32) {
           *(f32x4*)((float*)ea.y + m * ea.ldy + n) = v;
         } else if constexpr (EPI == EPI_BF16) {
@@ -342,11 +344,14 @@ __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
 }
 
-template <int EPI>
-__global__ void __launch_bounds__(512)
+// NW waves of 128 x (512 / NW) a 256 x 256 tile.  The launch uses 8 waves of 128 x 64, two a
+// SIMD.  4 waves of 128 x 128 (one a SIMD, a third less LDS read a FLOP) were slower under the
+// one-barrier schedule and spill their 256 accumulators under this one.
+template <int EPI, int NW>
+__global__ void __launch_bounds__(NW * 64)
 k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB, int64_t M, int64_t N,
           int64_t K, EpiArgs ea) {
-  constexpr int NW = 8, WM = 128, WN = 64, MI = WM / 16, NI = WN / 16, ROUNDS = 256 / (NW * 8);
+  constexpr int WM = 128, WN = 512 / NW, MI = WM / 16, NI = WN / 16, ROUNDS = 256 / (NW * 8);
   constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = 2 * ROUNDS;
   extern __shared__ __align__(1024) uint8_t smem[];   // 2 stages x (X tile 32 KB | W tile 32 KB)
   const int tid = threadIdx.x, lane = tid & 63;
@@ -400,18 +405,47 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // A slice of 32 k: NMF MFMAs on F in a fixed order -- after each, one fragment read of
-  // the next slice into G (the first NRD of them) and, on the DMA slice, one DMA part --
-  // with scheduling fences between, so the DMA and the reads never bunch up.
-  auto slice = [&](const Frag& F, Frag& G, int rstage, int rkk, bool dma, int dt, int dstage) {
+  // A step is 2 NMF MFMAs (two slices of 32 k) in a fixed order, with scheduling fences
+  // between, so that reads, DMA and barriers never bunch up:
+  //   MFMAs 0 .. NRD-1     read this step's second-slice fragments (stage cur) into F1;
+  //   MFMA B1              barrier: every wave is done with stage cur, which is free;
+  //   MFMAs B1 .. B1+DS-1  the DMA of step t+2 into stage cur, one part every DS/NDMA MFMAs;
+  //   MFMA B2              barrier: step t+1's DMA, out since the step before, has landed;
+  //   MFMAs B2 .. B2+NRD-1 read step t+1's first-slice fragments (stage cur^1) into F0.
+  // The DMA then has from B1 of one step to B2 of the next to land (about 1.6 steps), and the
+  // barrier before the DMA waits on no memory.
+  constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DSPREAD = NMF;
+  // B2 lets this step's NDMA DMA parts stay outstanding, and no more: they must all be out
+  static_assert(B1 >= NRD && B1 + DSPREAD <= B2 && B2 + NRD <= 2 * NMF, "step schedule");
+  auto step = [&](Frag& F0, Frag& F1, int t) {
+    const int cur = t & 1, nx = min(t + 2, KT - 1);
 #pragma unroll
-    for (int x = 0; x < NMF; ++x) {
-      acc[x / NI][x % NI] =
-          __builtin_amdgcn_mfma_f32_16x16x32_bf16(F.v[x / NI], F.v[MI + x % NI], acc[x / NI][x % NI], 0, 0, 0);
-      if (x < NRD) rd1(G, rstage, rkk, x);
-      if (dma) {
+    for (int x = 0; x < 2 * NMF; ++x) {
+      if (x == B1) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));   // LDS reads done
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      if (x == B2) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt((NDMA & 15) | (0x7 << 4) | (0x0 << 8) | ((NDMA >> 4) << 14));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      const int y = x % NMF;
+      if (x < NMF)
+        acc[y / NI][y % NI] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(F0.v[y / NI], F0.v[MI + y % NI], acc[y / NI][y % NI], 0, 0, 0);
+      else
+        acc[y / NI][y % NI] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(F1.v[y / NI], F1.v[MI + y % NI], acc[y / NI][y % NI], 0, 0, 0);
+      if (x < NRD) rd1(F1, cur, 1, x);
+      if (x >= B2 && x < B2 + NRD) rd1(F0, cur ^ 1, 0, x - B2);
+      if (x >= B1 && x < B1 + DSPREAD) {
 #pragma unroll
-        for (int p = (x * NDMA) / NMF; p < ((x + 1) * NDMA) / NMF; ++p) dma_part(dt, dstage, p);
+        for (int p = ((x - B1) * NDMA) / DSPREAD; p < ((x - B1 + 1) * NDMA) / DSPREAD && p < NDMA; ++p)
+          dma_part(nx, cur, p);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -420,30 +454,23 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
 #pragma unroll
   for (int p = 0; p < NDMA; ++p) dma_part(0, 0, p);
   LDS_VMCNT0_BARRIER();
-  if (KT > 1) {
 #pragma unroll
-    for (int p = 0; p < NDMA; ++p) dma_part(1, 1, p);
-  }
+  for (int p = 0; p < NDMA; ++p) dma_part(min(1, KT - 1), 1, p);
 #pragma unroll
   for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
-  for (int t = 0; t < KT; ++t) {
-    const int cur = t & 1;
-    slice(F0, F1, cur, 1, false, 0, 0);
-    // every wave has its slice-1 fragments and its DMA of step t+1 has landed: stage cur is free
-    LDS_VMCNT0_BARRIER();
-    // the step after next into stage cur (past the end: the last step again, never read), the
-    // next step's first fragments from the other stage -- no branch, so the order holds
-    slice(F1, F0, cur ^ 1, 0, true, min(t + 2, KT - 1), cur);
-  }
+  // past the end the DMA re-reads the last step into the free stage, and nothing reads it:
+  // no branch, so the order holds
+  for (int t = 0; t < KT; ++t) step(F0, F1, t);
   LDS_VMCNT0_BARRIER();   // the last DMA has landed before the epilogue takes the LDS over
-  epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * 72), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
+  epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
 template <int EPI>
 static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* wb, int64_t M, int64_t N,
                             int64_t K, const EpiArgs& ea) {
   const size_t shm = 2 * 65536;
-  auto kern = k_gemm_bt<EPI>;
+  constexpr int NW = 8;
+  auto kern = k_gemm_bt<EPI, NW>;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
@@ -451,7 +478,7 @@ static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const
     attr = true;
   }
   dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256));
-  hipLaunchKernelGGL(kern, grid, dim3(512), shm, s, x, lda, wb, M, N, K, ea);
+  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, M, N, K, ea);
   return hipGetLastError();
 }
 
