@@ -212,27 +212,33 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 
     // S of tile t+1 from K stage ST^1, one MFMA a slot, with one pair of tile t's P values
     // (two exp2, an fp16 pack, and the row sum of the fp16 values the product uses) a slot
+    // Fragment reads run KD MFMAs ahead of their use (an LDS read takes several 32-cycle MFMA
+    // slots to return); the first KD V^T fragments of the O product go out in the last slots
+    // of the S product, since V^T of tile t is in LDS since the step's barrier.
+    constexpr int KD = 3;
     f32x16 sn[2];
     uint32_t pk[16];   // pair i: keys of S element (i / 8, 2 (i % 8)) and the next
-    f16x8 ka, kb;
+    f16x8 kq[KD], vq[KD];
     if constexpr (!LAST) {
       const float c0 = unit ? -mrun : 0.f;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) sn[b][r] = c0;
-      ka = kfrag(std::integral_constant<int, ST ^ 1>(), 0);
-      kb = kfrag(std::integral_constant<int, ST ^ 1>(), 1);
+#pragma unroll
+      for (int i = 0; i < KD; ++i) kq[i] = kfrag(std::integral_constant<int, ST ^ 1>(), i);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if constexpr (!LAST) {
         f16x8 kn = {};
-        if (i + 2 < 16) kn = kfrag(std::integral_constant<int, ST ^ 1>(), i + 2);
-        sn[i % 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[i / 2], sn[i % 2], 0, 0, 0);
-        ka = kb;
-        kb = kn;
+        if (i + KD < 16) kn = kfrag(std::integral_constant<int, ST ^ 1>(), i + KD);
+        sn[i % 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kq[0], qf[i / 2], sn[i % 2], 0, 0, 0);
+#pragma unroll
+        for (int d = 0; d + 1 < KD; ++d) kq[d] = kq[d + 1];
+        kq[KD - 1] = kn;
       }
+      if (i >= 16 - KD) vq[i - (16 - KD)] = vfrag(std::integral_constant<int, ST>(), i - (16 - KD));
       const int b = i / 8, r = 2 * (i % 8);
       pk[i] = pack_f16x2(__builtin_amdgcn_exp2f(sc[b][r]), __builtin_amdgcn_exp2f(sc[b][r + 1]));
       lrun = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk[i]), ones, lrun, false);
@@ -240,16 +246,16 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
     }
 
     // O^T += V^T P^T of tile t over 4 steps of 16 keys (step bu: block bu / 2, rows 8 (bu % 2) ..)
-    f16x8 va = vfrag(std::integral_constant<int, ST>(), 0), vb = vfrag(std::integral_constant<int, ST>(), 1);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       f16x8 vn = {};
-      if (j + 2 < 16) vn = vfrag(std::integral_constant<int, ST>(), j + 2);
+      if (j + KD < 16) vn = vfrag(std::integral_constant<int, ST>(), j + KD);
       const int bu = j / 4;
       const f16x8 pb = __builtin_bit_cast(f16x8, u32x4{pk[4 * bu], pk[4 * bu + 1], pk[4 * bu + 2], pk[4 * bu + 3]});
-      o[j % 4] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[j % 4], 0, 0, 0);
-      va = vb;
-      vb = vn;
+      o[j % 4] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vq[0], pb, o[j % 4], 0, 0, 0);
+#pragma unroll
+      for (int d = 0; d + 1 < KD; ++d) vq[d] = vq[d + 1];
+      vq[KD - 1] = vn;
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (!LAST) {
