@@ -419,8 +419,10 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   static_assert(B1 >= NRD && B1 + DSPREAD <= B2 && B2 + NRD <= 2 * NMF, "step schedule");
   auto step = [&](Frag& F0, Frag& F1, int t) {
     const int cur = t & 1, nx = min(t + 2, KT - 1);
-#pragma unroll
-    for (int x = 0; x < 2 * NMF; ++x) {
+    // MFMA position x of the step: a lambda unrolled over two loops of NMF, each small
+    // enough for the compiler to unroll whole (one loop of 2 NMF is past its limit once
+    // anything is added to the body)
+    auto pos = [&](const int x) {
       if (x == B1) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));   // LDS reads done
@@ -448,7 +450,11 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
           dma_part(nx, cur, p);
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+#pragma unroll
+    for (int x = 0; x < NMF; ++x) pos(x);
+#pragma unroll
+    for (int x = NMF; x < 2 * NMF; ++x) pos(x);
   };
   Frag F0, F1;
 #pragma unroll
