@@ -311,7 +311,7 @@ def main():
                    **({"tflops": round(prof[c][2] / (prof[c][0] * 1e-3) / 1e12, 1)} if prof[c][2] else {}),
                    **({"gbs": round(prof[c][3] / (prof[c][0] * 1e-3) / 1e9, 1)} if prof[c][3] and not prof[c][2]
                       else {})}
-               for c in X.Dit.PROFILE_CLASSES}
+               for c in X.Dit.PROFILE_CLASSES if prof[c][1]}
     out = {
         "metric": METRIC, "value": round(ms, 3), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak",

@@ -564,6 +564,32 @@ int exn_qkv_prep(exn_ctx* ctx, const uint16_t* qkv, int64_t n, const float* wq, 
   return EXN_OK;
 }
 
+int exn_mm_qkv(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, const float* wq, const float* wk,
+               const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap) {
+  TRY(use(ctx));
+  TRY(check_gemm(w, n));
+  if (!x_bf16 || !wq || !wk || !cs || !q || !k || !vt) FAIL(EXN_EINVAL, "null pointer");
+  if (w->rows != 3 * EXN_W || w->cols != EXN_W || w->pairs)
+    FAIL(EXN_EINVAL, "exn_mm_qkv: the fused q | k | v matrix (12288 x 4096) only");
+  if (w->kind == EXN_Q8_0 && !w->wx_ok) FAIL(EXN_EINVAL, "exn_mm_qkv: bf16 weights (exn_weight_resident) only");
+  EpiArgs ea{};
+  ea.n0 = (int)row0;
+  ea.wq = wq;
+  ea.wk = wk;
+  ea.cs = cs;
+  ea.qscale = QK_QSCALE;
+  ea.q = q;
+  ea.kc = k;
+  ea.vt = vt;
+  ea.lcap = lcap;
+  if (row0 < 0 || row0 > INT32_MAX) FAIL(EXN_EINVAL, "row0");
+  const hipError_t r = gemm_qkv(ctx->stream, x_bf16, EXN_W, w->kind == EXN_Q8_0 ? w->wx : w->wb, n, EXN_W, ea);
+  if (r == hipErrorNotSupported)
+    FAIL(EXN_EINVAL, "exn_mm_qkv: 16-byte aligned arrays, lcap a multiple of 64, row0 + n <= lcap");
+  HIPCHK(r);
+  return EXN_OK;
+}
+
 int exn_attend(exn_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out, int n, int q0,
                int p, int l, int64_t lcap, int b0, int b1, float scale) {
   TRY(use(ctx));
@@ -1246,14 +1272,33 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes);
       HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 0 * EXN_W, y, 1));
     }
-    {
+    // the QKV product with qk-norm, RoPE and the K/V^T stores in its epilogue (bf16 weights),
+    // else the product to fp16 rows and qkv_prep over them
+    bool fused = false;
+    if (L.qkv->kind != EXN_Q8_0 || L.qkv->wx_ok) {
       ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
       ea = EpiArgs{};
-      ea.y = qkv;
-      ea.ldy = 3 * EXN_W;
-      HIPCHK(gemm_any(s, L.qkv, y, EXN_W, n, EPI_F16, ea));
+      ea.n0 = n0;
+      ea.wq = L.norm_q;
+      ea.wk = L.norm_k;
+      ea.cs = d->cs;
+      ea.qscale = QK_QSCALE;
+      ea.q = q;
+      ea.kc = d->kc[(size_t)il];
+      ea.vt = d->vt[(size_t)il];
+      ea.lcap = d->lcap;
+      const hipError_t r = gemm_qkv(s, y, EXN_W, L.qkv->kind == EXN_Q8_0 ? L.qkv->wx : L.qkv->wb, n, EXN_W, ea);
+      if (r != hipErrorNotSupported) HIPCHK(r);
+      fused = r == hipSuccess;
     }
-    {
+    if (!fused) {
+      {
+        ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
+        ea = EpiArgs{};
+        ea.y = qkv;
+        ea.ldy = 3 * EXN_W;
+        HIPCHK(gemm_any(s, L.qkv, y, EXN_W, n, EPI_F16, ea));
+      }
       ProfScope ps(d, EXN_PROF_QKV_PREP, 0, qkv_bytes);
       HIPCHK(qkv_prep(s, qkv, n, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap));
     }

@@ -271,7 +271,7 @@ hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* 
                     uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap) {
   if (n == 0) return hipSuccess;
   // q is scaled by 1/sqrt(128) * log2(e): the attention's scores are then in log2 units
-  const float qscale = 0.08838834764831845f * 1.4426950408889634f;
+  const float qscale = QK_QSCALE;
   hipLaunchKernelGGL(k_qkv_prep, dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, n, wq, wk, cs, qscale, q, k, vt,
                      row0, lcap);
   return hipGetLastError();

@@ -146,14 +146,30 @@ namespace exn {
 // one MFMA step (16u + 8(j/4) + 4hi + j%4, j = 0..7) in 16 contiguous bytes.
 __host__ __device__ inline int64_t vt_pos(int64_t k) { return k ^ ((((k >> 2) ^ (k >> 3)) & 1) * 12); }
 
-enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_GATE_ADD = 2, EPI_SWIGLU = 3, EPI_GELU_BF16 = 4, EPI_F16 = 5 };
+// q's scale: 1/sqrt(128) x log2(e), so that the attention's scores come out in log2 units
+constexpr float QK_QSCALE = 0.08838834764831845f * 1.4426950408889634f;
+
+enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_GATE_ADD = 2, EPI_SWIGLU = 3, EPI_GELU_BF16 = 4, EPI_F16 = 5, EPI_QKV = 6 };
 
 struct EpiArgs {
   void* y;             // EPI_F32 / EPI_BF16 / EPI_GELU_BF16: output rows (ldy elements apart); EPI_SWIGLU: bf16 out (N/2 wide)
   int64_t ldy;         // output row stride in elements
   float* resid;        // EPI_GATE_ADD: the fp32 residual rows, ldy apart
   const float* gate;   // EPI_GATE_ADD: gate rows (row 0, row 1 = gate + mstride)
-  int n0, p, mstride;  // EPI_GATE_ADD: the sequence row of output row 0, the prefix length, the modulation row stride
+  int n0, p, mstride;  // EPI_GATE_ADD, EPI_QKV: the sequence row of output row 0; EPI_GATE_ADD: the prefix length,
+                       // the modulation row stride
+  // EPI_QKV: the fused QKV product (N = 3 x 4096: q | k | v, heads of 128 columns) straight into
+  // the attention's layouts -- q and k RMS-normed over each head (weights wq, wk, eps 1e-6) and
+  // rotated by cs ([sequence row][128]: cos, sin of each pair), q times qscale; Q [32][M][128],
+  // K [32][lcap][128] at key n0 + m, V^T [32][128][lcap] at column vt_pos(n0 + m), all fp16
+  const float* wq;
+  const float* wk;
+  const float* cs;
+  float qscale;
+  uint16_t* q;
+  uint16_t* kc;
+  uint16_t* vt;
+  int64_t lcap;
 };
 
 // Y = X W^T with X bf16 (M x K, lda), W Q8_0 SoA (qs N x K int8, d N x K/32 fp16) or bf16 (N x K)
@@ -161,6 +177,10 @@ hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* 
                    int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w,
                       int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
+// the QKV product with the q/k norm, RoPE and the K/V^T stores fused (EPI_QKV), bf16 weights;
+// hipErrorNotSupported when the shapes or alignments do not fit the fused path
+hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t K,
+                    const EpiArgs& ea);
 // the edge products: Y = X W^T all fp32 on the SIMD lanes (K % 32 == 0); optional GELU-tanh on Y
 hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
                     const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int gelu);

@@ -243,13 +243,10 @@ hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* 
 }
 
 // --- bf16 weights: the pipelined kernel ----------------------------------------------
-// 256 x 256 tiles, 8 waves of 128 x 64 (8 x 4 tiles of v_mfma_f32_16x16x32_bf16), BK = 64
-// in two slices of 32.  Both tiles go HBM/L2 -> LDS by the
-// LDS DMA path (buffer_load_dwordx4 ... lds: no VGPR staging, no ds_write), two stages.
-// Inside a step the wave's fragment registers are double-buffered: the ds_reads of
-// slice 1 are interleaved with the MFMAs of slice 0, and the step's one barrier sits
-// before slice 1, so the DMA of the step after next and the next step's first fragment
-// reads are spread over that slice's MFMAs.
+// 256 x 256 tiles, 8 waves of 128 x 64 (8 x 4 tiles of v_mfma_f32_16x16x32_bf16) or, for the
+// QKV product's fused epilogue, 64 x 128 (one head a wave); BK = 64 in two slices of 32.
+// Both tiles go HBM/L2 -> LDS by the LDS DMA path (buffer_load_dwordx4 ... lds: no VGPR
+// staging, no ds_write), two stages, with the step schedule described at the kernel.
 // LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by (row/2)%8: the
 // fragment reads of 32 rows x 16 bytes are bank-conflict free.
 typedef __attribute__((address_space(3))) void lds_void;
@@ -338,6 +335,101 @@ __device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* 
   }
 }
 
+// The QKV product's epilogue (EPI_QKV): a wave's 64 rows x 128 columns are one head of q, k
+// or v for 64 tokens (output row m is sequence row n0 + m).  q and k: the RMS of each row
+// over the head from the accumulators (the lane's 8 values, then the 16 lanes that share the
+// row), then rows through the wave's LDS block 16 at a time, each lane 4 consecutive
+// columns: the norm weight, the rotation of its two pairs (one 16-byte cos/sin load), q's
+// scale, and 8 bytes of fp16 into Q or the K cache.  v: 16 tokens of V^T at a time, 16 bytes
+// (8 keys) a lane when the 16 keys are one aligned group of the V^T order, else key by key.
+// The same arithmetic as qkv_prep (eltwise.hip) on the fp32 sums instead of their fp16
+// rounding; V^T's values are the same fp16 roundings.
+template <int MI, int NI>
+__device__ __forceinline__ void epilogue_qkv(f32x4 (&acc)[MI][NI], float* stage, int64_t wrow, int64_t wcol,
+                                             int lane, int64_t M, const EpiArgs& ea) {
+  static_assert(MI == 4 && NI == 8, "a wave holds 64 rows of one head (128 columns)");
+  constexpr int LS = 132;   // LDS row: 128 floats and 4 of padding
+  const int part = (int)(wcol / EXN_W), h = (int)((wcol % EXN_W) / EXN_HD);   // part 0 q, 1 k, 2 v
+  const int c16 = lane & 15, q4 = lane >> 4;
+  const int c4 = (lane & 31) * 4;
+  // the cos/sin of a 16-row block (2 rows a wave instruction, 8 loads a lane) go out one block
+  // ahead of their use -- the first before the RMS -- so their latency hides under the work
+  auto cs_load = [&](f32x4 (&dst)[8], int i) {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int64_t m = min(wrow + 16 * i + 2 * it + (lane >> 5), M - 1);   // rows past M: loaded, unused
+      dst[it] = *(const f32x4*)(ea.cs + (ea.n0 + m) * EXN_HD + c4);
+    }
+  };
+  f32x4 csa[8], csb[8];
+  if (part < 2) cs_load(csa, 0);
+  if (part < 2) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) ss += acc[i][j][r] * acc[i][j][r];
+        const float inv = rsqrtf(row16_sum(ss) * (1.f / 128.f) + 1e-6f);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j][r] *= inv;
+      }
+  }
+  f32x4 w = {1.f, 1.f, 1.f, 1.f};
+  if (part == 0) w = *(const f32x4*)(ea.wq + c4);
+  if (part == 1) w = *(const f32x4*)(ea.wk + c4);
+  const float sc = part == 0 ? ea.qscale : 1.f;
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    // accumulators of v_mfma_f32_16x16x32: lane l holds column l%16, rows 4*(l/16) + r
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) stage[(4 * q4 + r) * LS + 16 * j + c16] = acc[i][j][r];
+    const int64_t mb = wrow + 16 * i;   // the output row of the 16 staged rows' first
+    if (part < 2) {
+      f32x4(&csc)[8] = i % 2 == 0 ? csa : csb;
+      if (i + 1 < MI) cs_load(i % 2 == 0 ? csb : csa, i + 1);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int row = 2 * it + (lane >> 5);
+        const int64_t m = mb + row;
+        if (m >= M) continue;
+        const f32x4 v = *(const f32x4*)(stage + row * LS + c4);
+        const f32x4 cs = csc[it];   // cos, sin of the lane's 2 pairs
+        const float a0 = v[0] * w[0], a1 = v[1] * w[1], a2 = v[2] * w[2], a3 = v[3] * w[3];
+        const u32x2 o = {pack_f16x2((a0 * cs[0] - a1 * cs[1]) * sc, (a0 * cs[1] + a1 * cs[0]) * sc),
+                         pack_f16x2((a2 * cs[2] - a3 * cs[3]) * sc, (a2 * cs[3] + a3 * cs[2]) * sc)};
+        uint16_t* dst = part == 0 ? ea.q + ((int64_t)h * M + m) * EXN_HD + c4
+                                  : ea.kc + ((int64_t)h * ea.lcap + ea.n0 + m) * EXN_HD + c4;
+        *(u32x2*)dst = o;
+      }
+    } else {
+      const int64_t kb = ea.n0 + mb;   // the key of the first staged row
+      if (kb % 16 == 0 && mb + 16 <= M) {
+        // one aligned group of 16 keys: V^T column kb + c holds key kb + vt_pos(c); a lane
+        // packs 8 columns of one dim, 4 times (128 dims x 2 halves)
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          const int task = it * 64 + lane, d = task >> 1, hf = task & 1;
+          uint32_t pk[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            pk[e] = pack_f16x2(stage[vt_pos(8 * hf + 2 * e) * LS + d], stage[vt_pos(8 * hf + 2 * e + 1) * LS + d]);
+          *(u32x4*)(ea.vt + ((int64_t)h * EXN_HD + d) * ea.lcap + kb + 8 * hf) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        }
+      } else {
+        for (int it = 0; it < 32; ++it) {
+          const int task = it * 64 + lane, d = task & 127, k = task >> 7;
+          if (mb + k < M)
+            ea.vt[((int64_t)h * EXN_HD + d) * ea.lcap + vt_pos(kb + k)] = (uint16_t)(pack_f16x2(stage[k * LS + d], 0.f) & 0xFFFF);
+        }
+      }
+    }
+  }
+}
+
 // One 16-byte DMA lane of a tile: the buffer's extent makes rows past the matrix read as zeros.
 __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
   __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
@@ -351,7 +443,10 @@ template <int EPI, int NW>
 __global__ void __launch_bounds__(NW * 64)
 k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB, int64_t M, int64_t N,
           int64_t K, EpiArgs ea) {
-  constexpr int WM = 128, WN = 512 / NW, MI = WM / 16, NI = WN / 16, ROUNDS = 256 / (NW * 8);
+  constexpr bool HEADS = EPI == EPI_QKV;   // a wave's columns one head of 128
+  constexpr int WM = HEADS ? 64 : 128, WN = HEADS ? 128 : 512 / NW, MI = WM / 16, NI = WN / 16;
+  constexpr int ROUNDS = 256 / (NW * 8);
+  static_assert((256 / WM) * (256 / WN) == NW, "the waves tile 256 x 256");
   constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = 2 * ROUNDS;
   extern __shared__ __align__(1024) uint8_t smem[];   // 2 stages x (X tile 32 KB | W tile 32 KB)
   const int tid = threadIdx.x, lane = tid & 63;
@@ -468,7 +563,10 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // no branch, so the order holds
   for (int t = 0; t < KT; ++t) step(F0, F1, t);
   LDS_VMCNT0_BARRIER();   // the last DMA has landed before the epilogue takes the LDS over
-  epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
+  if constexpr (HEADS)
+    epilogue_qkv<MI, NI>(acc, (float*)smem + wave * (16 * 132), m0 + wm * WM, n0 + wn * WN, lane, M, ea);
+  else
+    epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
 template <int EPI>
@@ -486,6 +584,19 @@ static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const
   dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256));
   hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, M, N, K, ea);
   return hipGetLastError();
+}
+
+hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t K,
+                    const EpiArgs& ea) {
+  const int64_t N = 3 * EXN_W;
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  // the DMA path's conditions, and 16-byte rows of q, k, V^T, the weights and the cos/sin table
+  const bool ok = K % 64 == 0 && lda % 8 == 0 && a16(x) && a16(w) && M * lda < (int64_t)1 << 30 &&
+                  N * K < (int64_t)1 << 30 && a16(ea.q) && a16(ea.kc) && a16(ea.vt) && a16(ea.wq) && a16(ea.wk) &&
+                  a16(ea.cs) && ea.lcap % 64 == 0 && ea.n0 >= 0 && ea.n0 + M <= ea.lcap;
+  if (!ok) return hipErrorNotSupported;
+  if (M == 0) return hipSuccess;
+  return launch_bt<EPI_QKV>(s, x, lda, w, M, N, K, ea);
 }
 
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,

@@ -75,6 +75,7 @@ SIGNATURES = {
     "exn_gelu_tanh": (c_int, [vp, c_int64, vp]),
     "exn_silu": (c_int, [vp, c_int64, vp]),
     "exn_qkv_prep": (c_int, [vp, vp, c_int64, vp, vp, vp, vp, vp, vp, c_int64, c_int64]),
+    "exn_mm_qkv": (c_int, [vp, vp, vp, c_int64, vp, vp, vp, vp, vp, vp, c_int64, c_int64]),
     "exn_attend": (c_int, [vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int64, c_int, c_int, c_float]),
     "exn_euler": (c_int, [vp, c_int64, vp, vp, c_float]),
     "exn_dit_create": (c_int, [vp, c_int, POINTER(vp)]),

@@ -132,6 +132,12 @@ int exn_silu(exn_ctx* ctx, int64_t count, float* x);
  * inside every aligned 16 keys, the order exn_attend's P V product reads them in) */
 int exn_qkv_prep(exn_ctx* ctx, const uint16_t* qkv, int64_t n, const float* wq, const float* wk, const float* cs,
                  uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap);
+/* mm on the fused QKV matrix (src/cuda-dit.lisp:115-130) with x_qk_norm_rope (src/cuda/dit.cu:43-58)
+ * in the product's store: X_BF16 [n][4096] times W (12288 x 4096, bf16 or resident Q8_0), then
+ * exn_qkv_prep's outputs from the fp32 sums, without the fp16 QKV rows in between.  Arrays
+ * 16-byte aligned, LCAP % 64 == 0, ROW0 + n <= LCAP, CS with rows ROW0 .. ROW0 + n - 1. */
+int exn_mm_qkv(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, const float* wq, const float* wk,
+               const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap);
 /* x_attend_mma (src/cuda/dit.cu:208-336) with xa_lim's mask (:60-66): OUT [n][4096]
  * bf16 for queries = sequence rows Q0..Q0+n-1 over keys 0..l-1; Q, K, V^T fp16 in the
  * layouts exn_qkv_prep writes.  SCALE multiplies the scores, which are in log2

@@ -327,6 +327,63 @@ def test_qkv_prep(ctx):
     assert sorted(vt_pos(np.arange(lcap))) == list(range(lcap))  # a permutation inside each 16 keys
 
 
+@pytest.mark.parametrize("n,row0,lcap", [(300, 37, 384), (512, 256, 832), (257, 0, 320)])
+def test_mm_qkv_fused(ctx, n, row0, lcap):
+    """exn_mm_qkv: the QKV product with x_qk_norm_rope and the K/V^T stores in its epilogue,
+    against the unfused pair (exn_mm to fp16 rows, then exn_qkv_prep) on the same operands --
+    V^T bit-exact (the same fp32 sums, rounded once), q and k within fp16 rounding -- and
+    against float64 on three heads.  row0 37: V^T key by key; 256: 16 keys at once; n 257:
+    a last tile of one row.  K rows and V^T columns outside row0 .. row0+n-1 stay as they were."""
+    say("mm_qkv n", n, "row0", row0, "lcap", lcap)
+    rng = np.random.default_rng(n + row0)
+    w = X.Weight.synth(ctx, 9, 400, 3 * 4096, 4096).resident()
+    x = rng.normal(0, 1, (n, 4096)).astype(np.float32)
+    xb = bf16(x)
+    wq = (1 + 0.1 * rng.normal(0, 1, 128)).astype(np.float32)
+    wk = (1 + 0.1 * rng.normal(0, 1, 128)).astype(np.float32)
+    pos = rng.integers(-32, 300, (row0 + n, 3)).astype(np.float32)
+    cos, sin = xo.rope_tables(pos)
+    cs = np.stack([cos, sin], -1).reshape(row0 + n, 128).astype(np.float32)
+    dx, dwq, dwk, dcs = dev(ctx, xb), dev(ctx, wq), dev(ctx, wk), dev(ctx, cs)
+    SENT = 0x7BFF
+    outs = []
+    for fused in (True, False):
+        q = X.DevBuf.of(ctx, np.full((32, n, 128), SENT, np.uint16))
+        k = X.DevBuf.of(ctx, np.full((32, lcap, 128), SENT, np.uint16))
+        vt = X.DevBuf.of(ctx, np.full((32, 128, lcap), SENT, np.uint16))
+        if fused:
+            X.call("exn_mm_qkv", ctx.h, w.h, dx.h, n, dwq.h, dwk.h, dcs.h, q.h, k.h, vt.h, row0, lcap)
+        else:
+            qkv = X.DevBuf(ctx, (n, 3 * 4096), np.uint16)
+            X.call("exn_mm", ctx.h, w.h, dx.h, X.DT_BF16, qkv.h, 2, n)
+            X.call("exn_qkv_prep", ctx.h, qkv.h, n, dwq.h, dwk.h, dcs.h, q.h, k.h, vt.h, row0, lcap)
+        outs.append((q.get(), k.get(), vt.get()))
+    (fq, fk, fvt), (uq, uk, uvt) = outs
+    cols = vt_pos(np.arange(row0, row0 + n))
+    outside = np.setdiff1d(np.arange(lcap), cols)
+    assert (fk[:, :row0] == SENT).all() and (fk[:, row0 + n:] == SENT).all()
+    assert (fvt[:, :, outside] == SENT).all()
+    assert np.array_equal(fvt[:, :, cols], uvt[:, :, cols])
+    for a, b in ((fq, uq), (fk[:, row0:row0 + n], uk[:, row0:row0 + n])):
+        fa, fb = from_f16(a), from_f16(b)
+        assert np.abs(fa - fb).max() <= 2e-3 * np.abs(fb).max()
+    # float64 on heads 0, 17, 31 of q, k and v: bf16 operands, the oracle's norm and rotation
+    wf = xo.dequant_q8_0(*xo.q8_0_synth(9, 400, 3 * 4096, 4096))
+    wb = from_bf16(bf16(wf)).astype(np.float64)
+    xf = from_bf16(xb).astype(np.float64)
+    c, sn = cos[row0:], sin[row0:]
+    for hh in (0, 17, 31):
+        y = [xf @ wb[part * 4096 + hh * 128:part * 4096 + hh * 128 + 128].T for part in range(3)]
+        wantq = xo.rope(xo.rmsnorm(y[0][:, None], wq), c, sn)[:, 0] * (math.log2(math.e) / math.sqrt(128))
+        wantk = xo.rope(xo.rmsnorm(y[1][:, None], wk), c, sn)[:, 0]
+        gq = from_f16(fq[hh]).astype(np.float64)
+        gk = from_f16(fk[hh, row0:row0 + n]).astype(np.float64)
+        gv = from_f16(fvt[hh][:, cols]).T.astype(np.float64)
+        assert np.abs(gq - wantq).max() <= 2e-3 * np.abs(wantq).max()
+        assert np.abs(gk - wantk).max() <= 2e-3 * np.abs(wantk).max()
+        assert np.abs(gv - y[2]).max() <= 2 ** -10 * np.abs(y[2]).max() + 1e-3
+
+
 def vt_pos(k):
     """V^T's column of key k (exn_qkv_prep's layout): bits 2 and 3 swapped."""
     k = np.asarray(k)
