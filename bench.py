@@ -9,9 +9,9 @@ with every input already in HBM.  The first (uncached) step and the whole
 8-step loop are reported beside it.  Prints one JSON line.
 
 roofline: the dominant kernel (the gate_up product with SwiGLU fused) from
-HIP events recorded around each of its launches in the timed region, on the
-stream they run on; its algorithmic FLOPs per launch are 2 x 4096 x 24576 x
-4096.  traffic: HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE /
+HIP events recorded around every 4th of its launches in the timed region (blocks
+0, 4, .. 28 of each step), on the stream they run on; its algorithmic FLOPs per
+launch are 2 x 4096 x 24576 x 4096.  traffic: HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE /
 WRITE_SIZE (profiles/), or null.
 
 cpu_baseline: the oracle (oracle/exn_oracle.py, numpy fp32) timed on this
@@ -233,8 +233,10 @@ def main():
     for i in range(a.warmup):
         step(1 + i, key)
     ctx.sync()
-    # the timed steps carry HIP events around the roofline kernel's launches only
-    d.profile(True, classes=["gate_up"])
+    # the timed steps carry HIP events around every 4th launch of the roofline kernel (blocks
+    # 0, 4, .. 28 of each step): its mean launch time, measured live, at a quarter of the
+    # events' cost to the step
+    d.profile(True, classes=["gate_up"], every=4)
     ctx.sync()
     t0 = time.perf_counter()
     for i in range(a.steps):
@@ -246,7 +248,7 @@ def main():
     ms = t_steps * 1e3 / a.steps
     # the per-kernel breakdown from 3 more steps with events around every launch
     BREAKDOWN = 3
-    d.profile(True)
+    d.profile(True, every=1)
     for i in range(BREAKDOWN):
         step(1 + i, key)
     ctx.sync()
@@ -336,7 +338,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights (resident expansion of Q8_0)",
                      "achieved": round(achieved, 1) if achieved else None, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4) if achieved else None, "traffic": traffic,
-                     "avg_launch_ms": round(gu_avg, 4)},
+                     "avg_launch_ms": round(gu_avg, 4), "launches_timed": gu_n},
     }
     if not a.no_cpu:
         print("bench: timing the CPU baseline (oracle, one block)", file=sys.stderr, flush=True)

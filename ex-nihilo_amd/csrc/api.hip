@@ -694,6 +694,8 @@ struct exn_dit {
     double flops, bytes;
   };
   unsigned prof = 0;   // bit per kernel class recorded
+  int prof_every = 1;  // events around every prof_every-th launch of a recorded class
+  int64_t prof_seen[EXN_PROF_CLASSES] = {};
   std::vector<Rec> recs;
   std::vector<hipEvent_t> pool;
   size_t pool_used = 0;
@@ -715,7 +717,8 @@ struct ProfScope {
   double flops, bytes;
   hipEvent_t a = nullptr;
   ProfScope(exn_dit* d_, int c, double f, double b) : d(d_), cls(c), flops(f), bytes(b) {
-    if ((d->prof >> cls & 1u) && (a = prof_event(d))) (void)hipEventRecord(a, d->ctx->stream);
+    if ((d->prof >> cls & 1u) && d->prof_seen[cls]++ % d->prof_every == 0 && (a = prof_event(d)))
+      (void)hipEventRecord(a, d->ctx->stream);
   }
   ~ProfScope() {
     if (!a) return;
@@ -839,6 +842,13 @@ int exn_dit_profile(exn_dit* d, int on) {
     d->pool_used = 0;
   }
   d->prof = on < 0 ? (1u << EXN_PROF_CLASSES) - 1u : (unsigned)on & ((1u << EXN_PROF_CLASSES) - 1u);
+  return EXN_OK;
+}
+
+int exn_dit_profile_every(exn_dit* d, int every) {
+  if (!d || every < 1) FAIL(EXN_EINVAL, "profile sampling %d", every);
+  d->prof_every = every;
+  for (auto& c : d->prof_seen) c = 0;
   return EXN_OK;
 }
 

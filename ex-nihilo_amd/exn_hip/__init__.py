@@ -89,6 +89,7 @@ SIGNATURES = {
     "exn_dit_generate_dev": (c_int, [vp, vp, c_int, vp, c_int, c_int, vp, c_int, c_int, vp, c_int, c_int]),
     "exn_dit_trace": (c_int, [vp, vp, c_int64]),
     "exn_dit_profile": (c_int, [vp, c_int]),
+    "exn_dit_profile_every": (c_int, [vp, c_int]),
     "exn_dit_profile_read": (c_int, [vp, c_int, POINTER(c_double), POINTER(c_int64), POINTER(c_double),
                                      POINTER(c_double)]),
     "exn_dit_release": (c_int, [vp]),
@@ -303,11 +304,13 @@ class Dit:
 
     PROFILE_CLASSES = ("qkv", "attend", "out", "gate_up", "down", "ln_mod", "qkv_prep", "edge")
 
-    def profile(self, on, classes=None):
-        """Record HIP event pairs around the step's launches: all classes, or those named."""
+    def profile(self, on, classes=None, every=1):
+        """Record HIP event pairs around the step's launches: all classes, or those named;
+        around every EVERY-th launch of each only."""
         mask = 0
         if on:
             mask = -1 if classes is None else sum(1 << self.PROFILE_CLASSES.index(c) for c in classes)
+        call("exn_dit_profile_every", self.h, every)
         call("exn_dit_profile", self.h, mask)
 
     def profile_read(self):

@@ -194,16 +194,19 @@ int exn_dit_trace(exn_dit* d, float* buf, int64_t cap);
  * for all); (d, 0) stops.  exn_dit_profile_read gives a class's summed milliseconds,
  * launches, and algorithmic FLOPs and HBM bytes (one read of each input, one write of
  * each output) over the recorded launches. */
-#define EXN_PROF_QKV 0      /* LayerNormed rows x to_q|to_k|to_v, Q8_0 */
+#define EXN_PROF_QKV 0      /* LayerNormed rows x to_q|to_k|to_v (qk-norm, RoPE, K/V^T stores fused on bf16 weights) */
 #define EXN_PROF_ATTEND 1   /* attention */
 #define EXN_PROF_OUT 2      /* attention rows x to_out.0, gated residual fused */
 #define EXN_PROF_GATE_UP 3  /* LayerNormed rows x gate_up, SwiGLU fused */
 #define EXN_PROF_DOWN 4     /* SwiGLU rows x img_mlp.out, gated residual fused */
 #define EXN_PROF_LN_MOD 5   /* LayerNorm x (1 + scale) */
-#define EXN_PROF_QKV_PREP 6 /* QK RMSNorm + RoPE, V transposed */
+#define EXN_PROF_QKV_PREP 6 /* QK RMSNorm + RoPE, V transposed (Q8_0 weights only) */
 #define EXN_PROF_EDGE 7     /* timestep, txt_in, img_in, proj_out and the rest */
 #define EXN_PROF_CLASSES 8
 int exn_dit_profile(exn_dit* d, int on);
+/* events around every EVERY-th launch of each recorded class only (default 1): the sampled
+ * launches' mean duration at a fraction of the events' cost; restarts the count */
+int exn_dit_profile_every(exn_dit* d, int every);
 int exn_dit_profile_read(exn_dit* d, int cls, double* ms, int64_t* launches, double* flops, double* bytes);
 /* dit-release (src/cuda-dit.lisp:99-108): scratch and kept prompt K/V freed, weights kept */
 int exn_dit_release(exn_dit* d);
