@@ -1500,7 +1500,13 @@ struct exn_vae {
   std::vector<VExpect> expect;
   std::map<std::string, VT> t;
   std::map<std::string, Buf> bufs;
+  float* part = nullptr;   // split-K partial sums of the small convolutions (a decode's scratch)
+  int64_t part_cap = 0;
 };
+
+// split-K scratch: a split convolution has S x tiles <= 256 workgroups of 256 pixels x at most
+// 288 channels, so 256 x 256 x 288 floats hold any of its partials
+static const int64_t kVaePartCap = (int64_t)256 * 256 * 288;
 
 static int vae_buf(exn_vae* v, const char* key, size_t bytes, void** out) {
   Buf& b = v->bufs[key];
@@ -1574,6 +1580,8 @@ int exn_vae_release(exn_vae* v) {
   HIPCHK(hipStreamSynchronize(v->ctx->stream));
   for (auto& kv : v->bufs) dev_free(kv.second.p);
   v->bufs.clear();
+  v->part = nullptr;
+  v->part_cap = 0;
   return EXN_OK;
 }
 
@@ -1680,7 +1688,7 @@ static int vae_conv_named(exn_vae* v, const std::string& name, int up, int out, 
   const VT* wt = vae_t(v, name + ".weight");
   const VT* b = vae_t(v, name + ".bias");
   if (!wt || !b) FAIL(EXN_ESTATE, "decoder: missing %s", name.c_str());
-  const VaeEpi ep{res, keep, kcin, ft, y2};
+  const VaeEpi ep{res, keep, kcin, ft, y2, v->part, v->part_cap};
   HIPCHK(vae_conv(v->ctx->stream, wt->taps, up, out, x, (const uint16_t*)wt->p, (const float*)b->p, ep, y, h, w,
                   wt->ci, (int)wt->o, wt->kp));
   return EXN_OK;
@@ -1771,6 +1779,8 @@ static int vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba
   TRY(vae_buf(v, "t1", (size_t)most * 2, (void**)&t1));
   TRY(vae_buf(v, "u", (size_t)most * 2, (void**)&u));
   TRY(vae_buf(v, "xs", (size_t)most * 2, (void**)&xs));
+  TRY(vae_buf(v, "part", (size_t)kVaePartCap * 4, (void**)&v->part));
+  v->part_cap = kVaePartCap;
   int hh = h, ww = w;
   const int64_t n0 = (int64_t)h * w;
   // the latent's pixels, conv2 (1 x 1), decoder.conv1 (3 x 3 to the top width)
@@ -1845,11 +1855,11 @@ int exn_vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba) {
 
 // op-level entry points of the decoder's kernels (tests)
 int exn_vae_conv(exn_ctx* ctx, int taps, int up, int outdt, const uint16_t* x, const uint16_t* wt, const float* bias,
-                 const float* res, void* y, int h, int w, int c, int cout, int kp) {
+                 const float* res, void* y, int h, int w, int c, int cout, int kp, float* part, int64_t part_cap) {
   TRY(use(ctx));
-  if (!x || !wt || !bias || !y || (taps != 1 && taps != 9) || outdt < 0 || outdt > 2)
+  if (!x || !wt || !bias || !y || (taps != 1 && taps != 9) || outdt < 0 || outdt > 2 || part_cap < 0)
     FAIL(EXN_EINVAL, "vae conv arguments");
-  const VaeEpi ep{res, nullptr, 0, 0, nullptr};
+  const VaeEpi ep{res, nullptr, 0, 0, nullptr, part, part ? part_cap : 0};
   const hipError_t e = vae_conv(ctx->stream, taps, up, outdt, x, wt, bias, ep, y, h, w, c, cout, kp);
   if (e == hipErrorInvalidValue)
     FAIL(EXN_EINVAL, "vae conv: taps %d up %d out %d, %d x %d x %d -> %d, kp %d", taps, up, outdt, h, w, c, cout, kp);

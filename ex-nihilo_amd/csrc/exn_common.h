@@ -215,12 +215,17 @@ hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uin
 // the VAE decoder (vae.hip).  vae_conv's outputs: fp32 (+ bias, + res when given), bf16 (+ bias,
 // + res when given), fp32 (+ bias) clamped to -1 .. 1, fp32 (+ bias, + DupUp3D of keep: kcin
 // channels at half size, frame ft - 1 of ft); taps 9 or 1; up: the input is the half-size picture
-enum VaeOut { VAE_F32 = 0, VAE_BF16 = 1, VAE_CLAMP = 2, VAE_DUPUP = 3 };
+enum VaeOut { VAE_F32 = 0, VAE_BF16 = 1, VAE_CLAMP = 2, VAE_DUPUP = 3, VAE_PART = 4 };
 struct VaeEpi {
   const float* res;    // VAE_F32 / VAE_BF16: added when not null (the output's layout)
   const float* keep;   // VAE_DUPUP: the stage's input, pixel rows of kcin
   int kcin, ft;
   uint16_t* y2;        // VAE_F32 / VAE_DUPUP: when not null, a bf16 copy of the output too
+  // scratch for split-K partial sums (S x pixels x cout floats, part_cap floats): when given, a
+  // 3 x 3 convolution of too few tiles to fill the chip splits its K over S workgroups (VAE_PART
+  // partials, then a sum in fixed order with bias and res)
+  float* part;
+  int64_t part_cap;
 };
 hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
                     const float* bias, const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp);

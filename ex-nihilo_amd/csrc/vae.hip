@@ -54,7 +54,8 @@ struct ConvTile {
 };
 
 // OUT: VAE_F32 fp32 (+ bias, + res when given), VAE_BF16 bf16 (+ bias, + res when given),
-// VAE_CLAMP fp32 (+ bias) clamped to -1 .. 1, VAE_DUPUP fp32 (+ bias, + DupUp3D of keep)
+// VAE_CLAMP fp32 (+ bias) clamped to -1 .. 1, VAE_DUPUP fp32 (+ bias, + DupUp3D of keep),
+// VAE_PART the fp32 sums of k-steps kt0 .. kt1-1 only (workgroup z of a split K) into z's slice
 template <int BN, int TAPS, int UP, int OUT>
 __global__ void __launch_bounds__(512)
 k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
@@ -66,7 +67,9 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   const int wm = wave % T::NWM, wn = wave / T::NWM;
   const int P = H * W;
   const int m0 = blockIdx.x * VBM, n0 = blockIdx.y * BN;
-  const int KT = Kp / 64;
+  // split K (VAE_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1
+  const int KTT = Kp / 64, S = gridDim.z, z = blockIdx.z;
+  const int kt0 = (int)((int64_t)KTT * z / S), kt1 = (int)((int64_t)KTT * (z + 1) / S);
   const int Hs = UP ? H >> 1 : H, Ws = UP ? W >> 1 : W;
   const uint32_t xext = (uint32_t)((int64_t)Hs * Ws * C * 2);
   const uint16_t* wbase = Wt + (int64_t)n0 * Kp;
@@ -82,7 +85,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
     const int y = m / W;
     py[i] = m < P ? y : -0x40000000;   // a row past the picture: every neighbour off it
     px[i] = m - y * W;
-    const int k = 8 * ((lane & 7) ^ ((r >> 1) & 7));
+    const int k = 64 * kt0 + 8 * ((lane & 7) ^ ((r >> 1) & 7));
     tp[i] = k / C;
     cc[i] = k - tp[i] * C;
   }
@@ -154,29 +157,29 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   };
 
   if constexpr (T::NST == 3) {
-    dma(0, 0);
-    dma(min(1, KT - 1), 1);   // every step issues NDMA instructions a wave, so vmcnt(NDMA) below
+    dma(kt0, 0);
+    dma(min(kt0 + 1, kt1 - 1), 1);   // every step issues NDMA instructions a wave, so vmcnt(NDMA) below
     int s = 0;
-    for (int t = 0; t < KT; ++t) {
+    for (int t = kt0; t < kt1; ++t) {
       // step t has landed for every wave, and every wave is done with stage (t + 2) % 3
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt((T::NDMA & 0xF) | (0x7 << 4) | (0x0 << 8));   // vmcnt(NDMA) lgkmcnt(0)
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      dma(min(t + 2, KT - 1), s >= 1 ? s - 1 : 2);   // into (t + 2) % 3; past the end a reload, never read
+      dma(min(t + 2, kt1 - 1), s >= 1 ? s - 1 : 2);   // into (t + 2) % 3; past the end a reload, never read
       step(smem + s * T::STAGE);
       s = s == 2 ? 0 : s + 1;
     }
   } else {
-    dma(0, 0);
-    for (int t = 0; t < KT; ++t) {
+    dma(kt0, 0);
+    for (int t = kt0; t < kt1; ++t) {
       // step t has landed for every wave, and every wave is done with the other stage
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // vmcnt(0) lgkmcnt(0)
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      dma(min(t + 1, KT - 1), (t + 1) & 1);   // past the end a reload, never read
-      step(smem + (t & 1) * T::STAGE);
+      dma(min(t + 1, kt1 - 1), (t - kt0 + 1) & 1);   // past the end a reload, never read
+      step(smem + ((t - kt0) & 1) * T::STAGE);
     }
   }
   asm volatile("" ::: "memory");
@@ -214,7 +217,8 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
         ok[q] = m < P && n < cout;
         const int mc = min(m, P - 1), nc = min(n, cout - 4);   // in bounds for the loads either way
         at[q] = mc * cout + nc;
-        v[q] = *(const f32x4*)(stg + row * 148 + 4 * c4) + *(const f32x4*)(bias + nc);
+        v[q] = *(const f32x4*)(stg + row * 148 + 4 * c4);
+        if constexpr (OUT != VAE_PART) v[q] += *(const f32x4*)(bias + nc);
         add[q] = f32x4{0.f, 0.f, 0.f, 0.f};
         if constexpr (OUT == VAE_DUPUP) {
           // channel c of pixel (yy, xx) adds keep's channel j / rep of pixel (yy/2, xx/2),
@@ -237,6 +241,8 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
         const f32x4 o = v[q] + add[q];
         if constexpr (OUT == VAE_BF16) {
           *(u32x2*)((uint16_t*)Y + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        } else if constexpr (OUT == VAE_PART) {
+          *(f32x4*)((float*)Y + (int64_t)z * P * cout + at[q]) = o;
         } else if constexpr (OUT == VAE_CLAMP) {
           f32x4 c;
 #pragma unroll
@@ -253,9 +259,37 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   }
 }
 
+// y = the S partial sums of a split-K convolution in order, + bias, + res when given; fp32 or
+// bf16 out; 4 channels a thread
+template <int BF16OUT>
+__global__ void __launch_bounds__(256)
+k_part_sum(int S, int64_t n4, int cout, const float* __restrict__ part, const float* __restrict__ bias,
+           const float* __restrict__ res, void* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  f32x4 v = ((const f32x4*)part)[i];
+  for (int zz = 1; zz < S; ++zz) v += ((const f32x4*)part)[zz * n4 + i];
+  v += *(const f32x4*)(bias + (4 * i) % cout);
+  if (res) v += ((const f32x4*)res)[i];
+  if constexpr (BF16OUT)
+    ((u32x2*)y)[i] = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  else
+    ((f32x4*)y)[i] = v;
+}
+
+static hipError_t part_sum(hipStream_t s, int S, int64_t n, int cout, const float* part, const float* bias,
+                           const float* res, void* y, bool bf16out) {
+  const int64_t n4 = n / 4;
+  if (bf16out)
+    hipLaunchKernelGGL(k_part_sum<1>, dim3(grid_of(n4, 256)), dim3(256), 0, s, S, n4, cout, part, bias, res, y);
+  else
+    hipLaunchKernelGGL(k_part_sum<0>, dim3(grid_of(n4, 256)), dim3(256), 0, s, S, n4, cout, part, bias, res, y);
+  return hipGetLastError();
+}
+
 template <int BN, int TAPS, int UP, int OUT>
 static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const VaeEpi& ep,
-                              void* y, int h, int w, int c, int cout, int kp) {
+                              void* y, int h, int w, int c, int cout, int kp, int split = 1) {
   auto kern = k_conv<BN, TAPS, UP, OUT>;
   constexpr int lds = ConvTile<BN>::LDS;
   static bool attr = false;
@@ -264,7 +298,7 @@ static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* 
     if (e != hipSuccess) return e;
     attr = true;
   }
-  dim3 grid(grid_of((int64_t)h * w, VBM), grid_of(cout, BN));
+  dim3 grid(grid_of((int64_t)h * w, VBM), grid_of(cout, BN), split);
   hipLaunchKernelGGL(kern, grid, dim3(512), lds, s, x, wt, bias, ep, y, h, w, c, cout, kp);
   return hipGetLastError();
 }
@@ -272,6 +306,18 @@ static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* 
 template <int BN>
 static hipError_t conv_bn(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
                           const float* bias, const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp) {
+  // a 3 x 3 convolution of fewer tiles than the chip's CUs (the decoder's 64 x 64 stages: 64
+  // tiles) splits its K over up to 4 workgroups a tile, each at least 16 k-steps, into fp32
+  // partials; k_part_sum adds them in order with bias and res
+  const int64_t P = (int64_t)h * w, tiles = grid_of(P, VBM) * (int64_t)grid_of(cout, BN);
+  int64_t split = 256 / tiles < 4 ? 256 / tiles : 4;
+  if (kp / 64 / 16 < split) split = kp / 64 / 16;
+  if (taps == 9 && !up && (out == VAE_F32 || out == VAE_BF16) && !ep.y2 && ep.part && tiles < 192 && split >= 2 &&
+      split * P * cout <= ep.part_cap) {
+    hipError_t e = launch_conv<BN, 9, 0, VAE_PART>(s, x, wt, bias, ep, ep.part, h, w, c, cout, kp, (int)split);
+    if (e != hipSuccess) return e;
+    return part_sum(s, (int)split, P * cout, cout, ep.part, bias, ep.res, y, out == VAE_BF16);
+  }
   if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
   if (taps == 9 && !up && out == VAE_BF16) return launch_conv<BN, 9, 0, VAE_BF16>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
   if (taps == 9 && !up && out == VAE_CLAMP) return launch_conv<BN, 9, 0, VAE_CLAMP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
@@ -288,7 +334,7 @@ hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x,
   // epilogue moves 4 channels at once; every offset and extent fits 31 bits
   if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || cout % 4 || h <= 0 || w <= 0 ||
       (up && (h % 2 || w % 2)) || ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || ((uintptr_t)y & 15) ||
-      ((uintptr_t)bias & 15) || ((uintptr_t)ep.res & 15) || ((uintptr_t)ep.y2 & 7) ||
+      ((uintptr_t)bias & 15) || ((uintptr_t)ep.res & 15) || ((uintptr_t)ep.y2 & 7) || ((uintptr_t)ep.part & 15) ||
       (int64_t)h * w * c * 2 >= ((int64_t)1 << 31) || (int64_t)cout * kp * 2 >= ((int64_t)1 << 31) ||
       (int64_t)h * w * cout >= ((int64_t)1 << 31) ||
       (out == VAE_DUPUP && (!ep.keep || ep.ft < 1 || ep.kcin <= 0 || (int64_t)cout * ep.ft * 4 % ep.kcin || h % 2 ||

@@ -104,7 +104,8 @@ SIGNATURES = {
     "exn_vae_release": (c_int, [vp]),
     "exn_vae_destroy": (c_int, [vp]),
     "exn_vae_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
-    "exn_vae_conv": (c_int, [vp, c_int, c_int, c_int, vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int]),
+    "exn_vae_conv": (c_int, [vp, c_int, c_int, c_int, vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int, vp,
+                             c_int64]),
     "exn_vae_rms_silu": (c_int, [vp, c_int64, c_int, vp, vp, vp, c_int]),
     "exn_vae_dupup_add": (c_int, [vp, c_int, c_int, c_int, c_int, c_int, vp, vp]),
 }

@@ -242,9 +242,11 @@ int exn_vae_memory(exn_vae* v, int64_t* weights, int64_t* scratch);
  * x_up2 folded in (UP), bias and residual fused; v_rms with x_silu; x_dupup_add).  X: bf16 pixel
  * rows (H x W x C, or H/2 x W/2 x C with UP); WT: bf16 rows of (tap, channel), KP long (a
  * multiple of 64, zero past TAPS * C); OUTDT 0 fp32 (+ RES when not null), 1 bf16, 2 fp32
- * clamped to -1..1.  C a multiple of 8, at least 64. */
+ * clamped to -1..1.  C a multiple of 8, at least 64.  PART (PART_CAP floats, or null): scratch
+ * with which a 3 x 3 convolution of fewer 256 x 288 tiles than the chip has CUs splits its K
+ * over up to 4 workgroups a tile and sums their partials in order. */
 int exn_vae_conv(exn_ctx* ctx, int taps, int up, int outdt, const uint16_t* x, const uint16_t* wt, const float* bias,
-                 const float* res, void* y, int h, int w, int c, int cout, int kp);
+                 const float* res, void* y, int h, int w, int c, int cout, int kp, float* part, int64_t part_cap);
 int exn_vae_rms_silu(exn_ctx* ctx, int64_t n, int c, const float* x, const float* gamma, uint16_t* y, int silu);
 int exn_vae_dupup_add(exn_ctx* ctx, int cin, int cout, int ft, int h, int w, const float* x, float* y);
 

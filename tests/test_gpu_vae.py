@@ -66,12 +66,21 @@ CONV_CASES = [  # (h, w, c, cout, taps, up, out, with res)
 ]
 
 
-@pytest.mark.parametrize("case", CONV_CASES)
-def test_conv_against_float64(ctx, case):
+SPLIT_CASES = [  # split K: fewer tiles than CUs, 3 x 3, no upsampling, fp32 or bf16 out
+    (12, 13, 1152, 1152, 9, 0, 0, True),
+    (9, 7, 576, 288, 9, 0, 1, True),
+    (16, 20, 288, 144, 9, 0, 0, False),
+    (4, 4, 1152, 576, 9, 0, 0, True),
+]
+
+
+@pytest.mark.parametrize("case,split", [(c, False) for c in CONV_CASES] + [(c, True) for c in SPLIT_CASES])
+def test_conv_against_float64(ctx, case, split):
     """The implicit-GEMM convolution: partial pixel and channel tiles, K not a
-    multiple of 64 (144, 288 wide), the upsampling fold, the three outputs."""
+    multiple of 64 (144, 288 wide), the upsampling fold, the three outputs; with a
+    partials buffer, K split over up to 4 workgroups a tile (their sum in order)."""
     h, w, c, cout, taps, up, out, with_res = case
-    say("conv", case)
+    say("conv", case, "split" if split else "")
     rng = np.random.default_rng(h * 1000 + c + cout)
     hs, ws = (h // 2, w // 2) if up else (h, w)
     x = xo.bf16_round(rng.standard_normal((hs, ws, c)).astype(np.float32))
@@ -88,8 +97,10 @@ def test_conv_against_float64(ctx, case):
         want = np.clip(want, -1, 1)
     y = X.DevBuf(ctx, (h * w, cout), np.uint16 if out == 1 else np.float32)
     rbuf = dev(ctx, res) if with_res else None
+    part = X.DevBuf(ctx, (4 * h * w * cout,), np.float32) if split else None
     X.call("exn_vae_conv", ctx.h, taps, up, out, dev(ctx, xo.bf16_bits(x)).h, dev(ctx, pack_conv(wt, kp)).h,
-           dev(ctx, b).h, rbuf.h if rbuf else None, y.h, h, w, c, cout, kp)
+           dev(ctx, b).h, rbuf.h if rbuf else None, y.h, h, w, c, cout, kp, part.h if part else None,
+           4 * h * w * cout if part else 0)
     got = y.get()
     if out == 1:
         got = xo.bf16_to_f32(got)
@@ -101,7 +112,8 @@ def test_conv_against_float64(ctx, case):
 def test_conv_rejects_bad_shapes(ctx):
     with pytest.raises(X.ExnError) as e:
         X.call("exn_vae_conv", ctx.h, 9, 0, 0, dev(ctx, np.zeros(64, np.uint16)).h, dev(ctx, np.zeros(64, np.uint16)).h,
-               dev(ctx, np.zeros(4, np.float32)).h, None, dev(ctx, np.zeros(64, np.float32)).h, 1, 1, 40, 4, 384)
+               dev(ctx, np.zeros(4, np.float32)).h, None, dev(ctx, np.zeros(64, np.float32)).h, 1, 1, 40, 4, 384,
+               None, 0)
     assert e.value.code == X.EINVAL
 
 
