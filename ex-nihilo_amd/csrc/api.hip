@@ -1684,11 +1684,11 @@ int exn_vae_memory(exn_vae* v, int64_t* weights, int64_t* scratch) {
 // output), RES added when given
 static int vae_conv_named(exn_vae* v, const std::string& name, int up, int out, const uint16_t* x, const float* res,
                           void* y, int h, int w, const float* keep = nullptr, int kcin = 0, int ft = 0,
-                          uint16_t* y2 = nullptr) {
+                          uint16_t* y2 = nullptr, const float* gamma = nullptr, uint16_t* yr = nullptr) {
   const VT* wt = vae_t(v, name + ".weight");
   const VT* b = vae_t(v, name + ".bias");
   if (!wt || !b) FAIL(EXN_ESTATE, "decoder: missing %s", name.c_str());
-  const VaeEpi ep{res, keep, kcin, ft, y2, v->part, v->part_cap};
+  const VaeEpi ep{res, keep, kcin, ft, y2, v->part, v->part_cap, gamma, yr};
   HIPCHK(vae_conv(v->ctx->stream, wt->taps, up, out, x, (const uint16_t*)wt->p, (const float*)b->p, ep, y, h, w,
                   wt->ci, (int)wt->o, wt->kp));
   return EXN_OK;
@@ -1699,28 +1699,51 @@ static const float* vae_vec(const exn_vae* v, const std::string& name) {
   return t ? (const float*)t->p : nullptr;
 }
 
+// a width whose output channels one convolution tile holds: the norm can ride in its store
+static bool vae_one_tile(int c) { return c == 144 || c == 288; }
+
 // OUT = conv(silu(norm(conv(silu(norm(X)))))) + (X, or its 1 x 1 shortcut): src/cuda-vae.lisp's
 // resblock, inspect/ref_vae.py:59-65.  OUT fp32, or bf16 when OUT_BF16 (a product's input next);
-// XB: X in bf16 when the caller has it (the shortcut's input), else cast here.  T1/U bf16
-// scratch, T2 fp32 scratch.
-static int vae_resblock(exn_vae* v, const std::string& p, const float* x, const uint16_t* xb, void* out, bool out_bf16,
-                        int i, int o, int h, int w, uint16_t* t1, float* t2, uint16_t* u) {
+// XB: X in bf16 when the caller has it (the shortcut's input), else cast here; XRS: silu(norm(X))
+// in bf16 when the step that wrote X made it, else made here.  At a one-tile width the inner
+// norm rides in the first convolution's store, and with GNEXT the second leaves
+// silu(norm(OUT) x GNEXT) in YNEXT for the next block or the head (*MADE then true).  T1, T3, U
+// bf16 scratch, T2 fp32 scratch; YNEXT may be T1.
+static int vae_resblock(exn_vae* v, const std::string& p, const float* x, const uint16_t* xb, const uint16_t* xrs,
+                        void* out, bool out_bf16, int i, int o, int h, int w, uint16_t* t1, float* t2, uint16_t* u,
+                        uint16_t* t3, const float* gnext = nullptr, uint16_t* ynext = nullptr, bool* made = nullptr) {
   hipStream_t s = v->ctx->stream;
   const int64_t n = (int64_t)h * w;
   const float* g0 = vae_vec(v, p + ".residual.0.gamma");
   const float* g3 = vae_vec(v, p + ".residual.3.gamma");
   if (!g0 || !g3) FAIL(EXN_ESTATE, "decoder: missing %s gammas", p.c_str());
-  const int oo = out_bf16 ? VAE_BF16 : VAE_F32;
-  HIPCHK(vae_rms_silu(s, n, i, x, g0, t1, 1));
-  TRY(vae_conv_named(v, p + ".residual.2", 0, VAE_F32, t1, nullptr, t2, h, w));
-  HIPCHK(vae_rms_silu(s, n, o, t2, g3, t1, 1));
-  if (i == o) return vae_conv_named(v, p + ".residual.6", 0, oo, t1, x, out, h, w);
-  if (!xb) {
-    HIPCHK(f32_to_bf16(s, x, u, n * i));
-    xb = u;
+  if (made) *made = false;
+  if (!xrs) {
+    HIPCHK(vae_rms_silu(s, n, i, x, g0, t1, 1));
+    xrs = t1;
   }
-  TRY(vae_conv_named(v, p + ".shortcut", 0, VAE_F32, xb, nullptr, t2, h, w));
-  return vae_conv_named(v, p + ".residual.6", 0, oo, t1, t2, out, h, w);
+  const bool one = vae_one_tile(o);
+  if (one) {
+    TRY(vae_conv_named(v, p + ".residual.2", 0, VAE_RMS, xrs, nullptr, nullptr, h, w, nullptr, 0, 0, nullptr, g3, t3));
+  } else {
+    TRY(vae_conv_named(v, p + ".residual.2", 0, VAE_F32, xrs, nullptr, t2, h, w));
+    HIPCHK(vae_rms_silu(s, n, o, t2, g3, t3, 1));
+  }
+  const float* res = x;
+  if (i != o) {
+    if (!xb) {
+      HIPCHK(f32_to_bf16(s, x, u, n * i));
+      xb = u;
+    }
+    TRY(vae_conv_named(v, p + ".shortcut", 0, VAE_F32, xb, nullptr, t2, h, w));
+    res = t2;
+  }
+  if (one && gnext && ynext && !out_bf16) {
+    TRY(vae_conv_named(v, p + ".residual.6", 0, VAE_F32, t3, res, out, h, w, nullptr, 0, 0, nullptr, gnext, ynext));
+    if (made) *made = true;
+    return EXN_OK;
+  }
+  return vae_conv_named(v, p + ".residual.6", 0, out_bf16 ? VAE_BF16 : VAE_F32, t3, res, out, h, w);
 }
 
 // one head over the n pixels, c wide (inspect/ref_vae.py:68-76): OUT = proj(softmax(q k^T /
@@ -1779,6 +1802,8 @@ static int vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba
   TRY(vae_buf(v, "t1", (size_t)most * 2, (void**)&t1));
   TRY(vae_buf(v, "u", (size_t)most * 2, (void**)&u));
   TRY(vae_buf(v, "xs", (size_t)most * 2, (void**)&xs));
+  uint16_t* t3;
+  TRY(vae_buf(v, "t3", (size_t)most * 2, (void**)&t3));
   TRY(vae_buf(v, "part", (size_t)kVaePartCap * 4, (void**)&v->part));
   v->part_cap = kVaePartCap;
   int hh = h, ww = w;
@@ -1787,43 +1812,63 @@ static int vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba
   HIPCHK(vae_latent_pixels(s, n0, kVaeZ, latent, t1));
   TRY(vae_conv_named(v, "conv2", 0, VAE_BF16, t1, nullptr, u, hh, ww));
   TRY(vae_conv_named(v, "decoder.conv1", 0, VAE_F32, u, nullptr, A, hh, ww));
-  TRY(vae_resblock(v, "decoder.middle.0", A, nullptr, B, false, top, top, hh, ww, t1, t2, u));
+  TRY(vae_resblock(v, "decoder.middle.0", A, nullptr, nullptr, B, false, top, top, hh, ww, t1, t2, u, t3));
   TRY(vae_attention(v, "decoder.middle.1", B, C, hh, ww, top, t1));
-  TRY(vae_resblock(v, "decoder.middle.2", C, nullptr, A, false, top, top, hh, ww, t1, t2, u));
+  TRY(vae_resblock(v, "decoder.middle.2", C, nullptr, nullptr, A, false, top, top, hh, ww, t1, t2, u, t3));
+  const float* ghead = vae_vec(v, "decoder.head.0.gamma");
+  if (!ghead) FAIL(EXN_ESTATE, "decoder: missing decoder.head.0.gamma");
+  // the residual.0 gamma of block j of stage si (the norm its input takes)
+  auto g0_of = [&](int si, int j) {
+    char q[96];
+    snprintf(q, sizeof q, "decoder.upsamples.%d.upsamples.%d.residual.0.gamma", si, j);
+    return vae_vec(v, q);
+  };
   char p[96];
   const uint16_t* a_bf16 = nullptr;   // A in bf16, when the step that wrote A kept a copy
+  const uint16_t* a_rs = nullptr;     // silu(norm(A)) for the stage's first block, when made (in t1)
+  bool made = false;
   for (int si = 0; si < 5; ++si) {
     const VStage& st = kVaeStages[si];
     // A holds the stage's input, kept for DupUp3D; the last block of an upsampling stage
-    // writes bf16 straight for the resample convolution
+    // writes bf16 straight for the resample convolution.  At one-tile widths each block's
+    // second convolution leaves the next block's (or the head's) normed input in t1.
     snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.0", si);
-    TRY(vae_resblock(v, p, A, a_bf16, B, false, st.in, st.out, hh, ww, t1, t2, u));
+    TRY(vae_resblock(v, p, A, a_bf16, a_rs, B, false, st.in, st.out, hh, ww, t1, t2, u, t3, g0_of(si, 1), t1, &made));
+    const uint16_t* b_rs = made ? t1 : nullptr;
     snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.1", si);
-    TRY(vae_resblock(v, p, B, nullptr, C, false, st.out, st.out, hh, ww, t1, t2, u));
+    TRY(vae_resblock(v, p, B, nullptr, b_rs, C, false, st.out, st.out, hh, ww, t1, t2, u, t3, g0_of(si, 2), t1,
+                     &made));
+    const uint16_t* c_rs = made ? t1 : nullptr;
     snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.2", si);
     if (st.up) {
-      TRY(vae_resblock(v, p, C, nullptr, u, true, st.out, st.out, hh, ww, t1, t2, u));
+      TRY(vae_resblock(v, p, C, nullptr, c_rs, u, true, st.out, st.out, hh, ww, t1, t2, u, t3));
       // nearest x2 folded into the convolution's loads, DupUp3D of the stage's input into its
-      // store, and a bf16 copy when the next stage's first block takes a 1 x 1 shortcut of it
+      // store, a bf16 copy when the next stage's first block takes a 1 x 1 shortcut of it, and
+      // that block's normed input when the width is one tile
       const bool copy = si + 1 < 5 && kVaeStages[si + 1].in != kVaeStages[si + 1].out;
+      const bool norm = si + 1 < 5 && vae_one_tile(st.out);
       snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.3.resample.1", si);
       TRY(vae_conv_named(v, p, 1, VAE_DUPUP, u, nullptr, C, 2 * hh, 2 * ww, A, st.in, st.tup ? 2 : 1,
-                         copy ? xs : nullptr));
+                         copy ? xs : nullptr, norm ? g0_of(si + 1, 0) : nullptr, norm ? t1 : nullptr));
       a_bf16 = copy ? xs : nullptr;
+      a_rs = norm ? t1 : nullptr;
       hh *= 2;
       ww *= 2;
       std::swap(A, C);
     } else {
-      TRY(vae_resblock(v, p, C, nullptr, B, false, st.out, st.out, hh, ww, t1, t2, u));
+      TRY(vae_resblock(v, p, C, nullptr, c_rs, B, false, st.out, st.out, hh, ww, t1, t2, u, t3,
+                       si + 1 < 5 ? g0_of(si + 1, 0) : ghead, t1, &made));
       a_bf16 = nullptr;
+      a_rs = made ? t1 : nullptr;
       std::swap(A, B);
     }
   }
   // the head: norm, SiLU, 3 x 3 to RGBA, clamped
-  const float* g = vae_vec(v, "decoder.head.0.gamma");
-  if (!g) FAIL(EXN_ESTATE, "decoder: missing decoder.head.0.gamma");
-  HIPCHK(vae_rms_silu(s, (int64_t)hh * ww, kVaeStages[4].out, A, g, t1, 1));
-  return vae_conv_named(v, "decoder.head.2", 0, VAE_CLAMP, t1, nullptr, rgba, hh, ww);
+  if (!a_rs) {
+    HIPCHK(vae_rms_silu(s, (int64_t)hh * ww, kVaeStages[4].out, A, ghead, t1, 1));
+    a_rs = t1;
+  }
+  return vae_conv_named(v, "decoder.head.2", 0, VAE_CLAMP, a_rs, nullptr, rgba, hh, ww);
 }
 
 extern "C" {

@@ -215,7 +215,7 @@ hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uin
 // the VAE decoder (vae.hip).  vae_conv's outputs: fp32 (+ bias, + res when given), bf16 (+ bias,
 // + res when given), fp32 (+ bias) clamped to -1 .. 1, fp32 (+ bias, + DupUp3D of keep: kcin
 // channels at half size, frame ft - 1 of ft); taps 9 or 1; up: the input is the half-size picture
-enum VaeOut { VAE_F32 = 0, VAE_BF16 = 1, VAE_CLAMP = 2, VAE_DUPUP = 3, VAE_PART = 4 };
+enum VaeOut { VAE_F32 = 0, VAE_BF16 = 1, VAE_CLAMP = 2, VAE_DUPUP = 3, VAE_PART = 4, VAE_RMS = 5 };
 struct VaeEpi {
   const float* res;    // VAE_F32 / VAE_BF16: added when not null (the output's layout)
   const float* keep;   // VAE_DUPUP: the stage's input, pixel rows of kcin
@@ -226,6 +226,11 @@ struct VaeEpi {
   // partials, then a sum in fixed order with bias and res)
   float* part;
   int64_t part_cap;
+  // when gamma is given (a convolution whose one channel tile holds every output channel: cout
+  // 144 or 288): yr = silu(rms(output) x gamma) in bf16 too, the next block's or the head's
+  // normed input; VAE_RMS writes yr only
+  const float* gamma;
+  uint16_t* yr;
 };
 hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
                     const float* bias, const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp);

@@ -55,8 +55,10 @@ struct ConvTile {
 
 // OUT: VAE_F32 fp32 (+ bias, + res when given), VAE_BF16 bf16 (+ bias, + res when given),
 // VAE_CLAMP fp32 (+ bias) clamped to -1 .. 1, VAE_DUPUP fp32 (+ bias, + DupUp3D of keep),
-// VAE_PART the fp32 sums of k-steps kt0 .. kt1-1 only (workgroup z of a split K) into z's slice
-template <int BN, int TAPS, int UP, int OUT>
+// VAE_PART the fp32 sums of k-steps kt0 .. kt1-1 only (workgroup z of a split K) into z's slice,
+// VAE_RMS none (yr only).  GAM: the tile holds every output channel, and ep.yr gets
+// silu(rms(output) x ep.gamma) in bf16.
+template <int BN, int TAPS, int UP, int OUT, int GAM>
 __global__ void __launch_bounds__(512)
 k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
        VaeEpi ep, void* __restrict__ Y, int H, int W, int C, int cout, int Kp) {
@@ -204,7 +206,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
         for (int r = 0; r < 4; ++r) stg[(16 * i + 4 * q4 + r) * 148 + 16 * j + lo] = acc[2 * half + i][j][r];
     __syncthreads();
     // 18 chunks a lane, in batches of 6 (3 at BN 288, where half the accumulators are still live)
-    constexpr int CH = BN == 144 ? 6 : (OUT == VAE_DUPUP ? 2 : 3);
+    constexpr int CH = BN == 144 ? 6 : (OUT == VAE_DUPUP || GAM ? 2 : 3);
 #pragma unroll
     for (int bt = 0; bt < 18 / CH; ++bt) {
       f32x4 v[CH], add[CH];
@@ -237,9 +239,14 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
       }
 #pragma unroll
       for (int q = 0; q < CH; ++q) {
-        if (!ok[q]) continue;
         const f32x4 o = v[q] + add[q];
-        if constexpr (OUT == VAE_BF16) {
+        if constexpr (GAM) {   // the output back into its staging row, for the norm below
+          const int k = (bt * CH + q) * 64 + lane, row = k / 36, c4 = k - row * 36;
+          *(f32x4*)(stg + row * 148 + 4 * c4) = o;
+        }
+        if (!ok[q]) continue;
+        if constexpr (OUT == VAE_RMS) {
+        } else if constexpr (OUT == VAE_BF16) {
           *(u32x2*)((uint16_t*)Y + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         } else if constexpr (OUT == VAE_PART) {
           *(f32x4*)((float*)Y + (int64_t)z * P * cout + at[q]) = o;
@@ -254,6 +261,39 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
             if (ep.y2) *(u32x2*)(ep.y2 + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           }
         }
+      }
+    }
+    if constexpr (GAM) {
+      // each staged row's sum of squares: lanes 2r and 2r + 1 take its two halves of 72, then
+      // swap; at BN 288 the row's other 144 channels are the partner wave's (same pixels)
+      const int rr = lane >> 1, hh = lane & 1;
+      float ss = 0.f;
+#pragma unroll 3
+      for (int c = 0; c < 18; ++c) {
+        const f32x4 t = *(const f32x4*)(stg + rr * 148 + 72 * hh + 4 * c);
+        ss += (t[0] * t[0] + t[1] * t[1]) + (t[2] * t[2] + t[3] * t[3]);
+      }
+      ss += dpp_f<0xB1>(ss);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+      if constexpr (T::NWN == 2) {
+        if (hh == 0) stg[rr * 148 + 144] = ss;
+        __syncthreads();
+        const int partner = wn ? wave - T::NWM : wave + T::NWM;
+        ss += ((const float*)smem + partner * (32 * 148))[rr * 148 + 144];
+      }
+      const float inv = sqrtf((float)cout) / fmaxf(sqrtf(ss), 1e-12f);
+      if (hh == 0) stg[rr * 148 + 145] = inv;
+      asm volatile("" ::: "memory");
+#pragma unroll 2
+      for (int q = 0; q < 18; ++q) {
+        const int k = q * 64 + lane, row = k / 36, c4 = k - row * 36;
+        const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + 144 * wn + 4 * c4;
+        if (m >= P) continue;
+        const f32x4 o = *(const f32x4*)(stg + row * 148 + 4 * c4), g = *(const f32x4*)(ep.gamma + n);
+        const float iv = stg[row * 148 + 145];
+        float e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = silu_bf16out(o[j] * iv * g[j]);
+        *(u32x2*)(ep.yr + (int64_t)m * cout + n) = u32x2{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3])};
       }
     }
   }
@@ -287,10 +327,10 @@ static hipError_t part_sum(hipStream_t s, int S, int64_t n, int cout, const floa
   return hipGetLastError();
 }
 
-template <int BN, int TAPS, int UP, int OUT>
+template <int BN, int TAPS, int UP, int OUT, int GAM = 0>
 static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const VaeEpi& ep,
                               void* y, int h, int w, int c, int cout, int kp, int split = 1) {
-  auto kern = k_conv<BN, TAPS, UP, OUT>;
+  auto kern = k_conv<BN, TAPS, UP, OUT, GAM>;
   constexpr int lds = ConvTile<BN>::LDS;
   static bool attr = false;
   if (!attr) {
@@ -309,6 +349,13 @@ static hipError_t conv_bn(hipStream_t s, int taps, int up, int out, const uint16
   // a 3 x 3 convolution of fewer tiles than the chip's CUs (the decoder's 64 x 64 stages: 64
   // tiles) splits its K over up to 4 workgroups a tile, each at least 16 k-steps, into fp32
   // partials; k_part_sum adds them in order with bias and res
+  if (ep.gamma) {   // the output's norm too: one channel tile (cout == BN), never split
+    if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    if (taps == 9 && !up && out == VAE_RMS) return launch_conv<BN, 9, 0, VAE_RMS, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    if (taps == 9 && up && out == VAE_DUPUP)
+      return launch_conv<BN, 9, 1, VAE_DUPUP, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    return hipErrorInvalidValue;
+  }
   const int64_t P = (int64_t)h * w, tiles = grid_of(P, VBM) * (int64_t)grid_of(cout, BN);
   int64_t split = 256 / tiles < 4 ? 256 / tiles : 4;
   if (kp / 64 / 16 < split) split = kp / 64 / 16;
@@ -335,6 +382,8 @@ hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x,
   if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || cout % 4 || h <= 0 || w <= 0 ||
       (up && (h % 2 || w % 2)) || ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || ((uintptr_t)y & 15) ||
       ((uintptr_t)bias & 15) || ((uintptr_t)ep.res & 15) || ((uintptr_t)ep.y2 & 7) || ((uintptr_t)ep.part & 15) ||
+      (ep.gamma && (!ep.yr || ((uintptr_t)ep.yr & 7) || ((uintptr_t)ep.gamma & 15) || (cout != 144 && cout != 288))) ||
+      (!ep.gamma && out == VAE_RMS) ||
       (int64_t)h * w * c * 2 >= ((int64_t)1 << 31) || (int64_t)cout * kp * 2 >= ((int64_t)1 << 31) ||
       (int64_t)h * w * cout >= ((int64_t)1 << 31) ||
       (out == VAE_DUPUP && (!ep.keep || ep.ft < 1 || ep.kcin <= 0 || (int64_t)cout * ep.ft * 4 % ep.kcin || h % 2 ||
