@@ -1847,9 +1847,12 @@ static int vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba
       // that block's normed input when the width is one tile
       const bool copy = si + 1 < 5 && kVaeStages[si + 1].in != kVaeStages[si + 1].out;
       const bool norm = si + 1 < 5 && vae_one_tile(st.out);
+      // the fp32 output is dead when the next block has both bf16 inputs (its norm and its
+      // shortcut's), adds the shortcut (in != out), and its stage keeps nothing for a DupUp3D
+      const bool dead = copy && norm && !kVaeStages[si + 1].up;
       snprintf(p, sizeof p, "decoder.upsamples.%d.upsamples.3.resample.1", si);
-      TRY(vae_conv_named(v, p, 1, VAE_DUPUP, u, nullptr, C, 2 * hh, 2 * ww, A, st.in, st.tup ? 2 : 1,
-                         copy ? xs : nullptr, norm ? g0_of(si + 1, 0) : nullptr, norm ? t1 : nullptr));
+      TRY(vae_conv_named(v, p, 1, VAE_DUPUP, u, nullptr, dead ? nullptr : C, 2 * hh, 2 * ww, A, st.in,
+                         st.tup ? 2 : 1, copy ? xs : nullptr, norm ? g0_of(si + 1, 0) : nullptr, norm ? t1 : nullptr));
       a_bf16 = copy ? xs : nullptr;
       a_rs = norm ? t1 : nullptr;
       hh *= 2;

@@ -256,7 +256,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
           for (int e = 0; e < 4; ++e) c[e] = fminf(1.f, fmaxf(-1.f, o[e]));
           *(f32x4*)((float*)Y + at[q]) = c;
         } else {
-          *(f32x4*)((float*)Y + at[q]) = o;
+          if (OUT != VAE_DUPUP || Y) *(f32x4*)((float*)Y + at[q]) = o;   // DupUp: no fp32 out when Y is null
           if constexpr (OUT == VAE_F32 || OUT == VAE_DUPUP) {
             if (ep.y2) *(u32x2*)(ep.y2 + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           }
@@ -381,6 +381,7 @@ hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x,
   // epilogue moves 4 channels at once; every offset and extent fits 31 bits
   if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || cout % 4 || h <= 0 || w <= 0 ||
       (up && (h % 2 || w % 2)) || ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || ((uintptr_t)y & 15) ||
+      (!y && !(out == VAE_DUPUP && (ep.y2 || ep.yr)) && out != VAE_RMS) ||
       ((uintptr_t)bias & 15) || ((uintptr_t)ep.res & 15) || ((uintptr_t)ep.y2 & 7) || ((uintptr_t)ep.part & 15) ||
       (ep.gamma && (!ep.yr || ((uintptr_t)ep.yr & 7) || ((uintptr_t)ep.gamma & 15) || (cout != 144 && cout != 288))) ||
       (!ep.gamma && out == VAE_RMS) ||
