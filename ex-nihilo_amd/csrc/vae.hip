@@ -39,14 +39,17 @@ __device__ __forceinline__ void conv_dma(const void* base, uint32_t extent, lds_
 #define VOFF_NONE 0x80000000u   // past any extent: the load reads zeros
 #define VEPI_LDS (8 * 32 * 148 * 4)   // the epilogue's staging: 8 waves x 32 pixels x 148 floats
 
-// Tiles of 256 pixels x BN output channels, BN = 144 (3 LDS stages) or 288 (2 stages; the
-// widths that 288 divides): 8 waves of WM pixels x 144 channels, each a (WM/16) x 9 grid of
+// Tiles of 256 pixels x BN output channels, BN = 144 (3 LDS stages), 288 (2 stages; the
+// widths that 288 divides) or 16 (3 stages; the head's 4 channels): 8 waves of WM pixels x WNC
+// channels (WNC = 144, or 16 at BN 16), each a (WM/16) x (WNC/16) grid of
 // v_mfma_f32_16x16x32_bf16 -- 0.61 fragment reads an MFMA at BN 144, 0.36 at BN 288.
 template <int BN>
 struct ConvTile {
-  static constexpr int NWN = BN / 144, NWM = 8 / NWN, WM = VBM / NWM, MI = WM / 16;
+  static constexpr int WNC = BN >= 144 ? 144 : BN, NJ = WNC / 16;   // a wave's channels, its 16-column blocks
+  static constexpr int NWN = BN / WNC, NWM = 8 / NWN, WM = VBM / NWM, MI = WM / 16;
+  static constexpr int LS = WNC + 4, RC = WNC / 4, NCH = 32 * RC / 64;   // staging: row floats, chunks a row, a lane
   static constexpr int STAGE = VBM * 128 + BN * 128;   // A rows | B rows, 64 bf16 of K each
-  static constexpr int NST = BN == 144 ? 3 : 2;
+  static constexpr int NST = BN <= 144 ? 3 : 2;
   static constexpr int BFULL = BN * 8 / 512;           // full B DMA rounds a step
   static constexpr int BREM = (BN * 8 - 512 * BFULL) / 8;   // lanes a wave in the partial round
   static constexpr int NDMA = 4 + BFULL + 1;           // DMA instructions a wave a step
@@ -136,12 +139,12 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
 
   // fragments: lane holds row lo of a 16-row block, K 8 q4 .. of a slice of 32
   const int lo = lane & 15, q4 = lane >> 4, fs = (lo >> 1) & 7;
-  const int a_rd = (T::WM * wm + lo) * 128, b_rd = 32768 + (144 * wn + lo) * 128;
-  f32x4 acc[T::MI][9];
+  const int a_rd = (T::WM * wm + lo) * 128, b_rd = 32768 + (T::WNC * wn + lo) * 128;
+  f32x4 acc[T::MI][T::NJ];
 #pragma unroll
   for (int i = 0; i < T::MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 9; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < T::NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto step = [&](const uint8_t* st) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
@@ -150,7 +153,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
 #pragma unroll
       for (int i = 0; i < T::MI; ++i) a[i] = *(const bf16x8*)(st + a_rd + i * 2048 + co);
 #pragma unroll
-      for (int j = 0; j < 9; ++j) {
+      for (int j = 0; j < T::NJ; ++j) {
         const bf16x8 b = *(const bf16x8*)(st + b_rd + j * 2048 + co);
 #pragma unroll
         for (int i = 0; i < T::MI; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][j], 0, 0, 0);
@@ -192,34 +195,36 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   // 32 x 144 block (row stride 148 floats), then moves it as 16-byte chunks, 4 channels of one
   // pixel a lane: bias, and the residual or the DupUp3D gather, loaded for a batch of chunks
   // before any of their stores.
-  float* stg = (float*)smem + wave * (32 * 148);
+  float* stg = (float*)smem + wave * (32 * T::LS);
   const float winv = 1.f / (float)W;
   const int rsh = OUT == VAE_DUPUP ? __builtin_ctz((unsigned)(cout * ep.ft * 4 / ep.kcin)) : 0;
 #pragma unroll
   for (int half = 0; half < T::MI / 2; ++half) {
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 9; ++j)
+    for (int j = 0; j < T::NJ; ++j)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) stg[(16 * i + 4 * q4 + r) * 148 + 16 * j + lo] = acc[2 * half + i][j][r];
+        for (int r = 0; r < 4; ++r) stg[(16 * i + 4 * q4 + r) * T::LS + 16 * j + lo] = acc[2 * half + i][j][r];
     __syncthreads();
-    // 18 chunks a lane, in batches of 6 (3 at BN 288, where half the accumulators are still live)
-    constexpr int CH = BN == 144 ? 6 : (OUT == VAE_DUPUP || GAM ? 2 : 3);
+    // NCH chunks a lane (18 at WNC 144), in batches of 6 (3 at BN 288, where half the
+    // accumulators are still live)
+    constexpr int CH = BN == 288 ? (OUT == VAE_DUPUP || GAM ? 2 : 3) : (T::NCH < 6 ? T::NCH : 6);
+    static_assert(T::NCH % CH == 0, "whole batches");
 #pragma unroll
-    for (int bt = 0; bt < 18 / CH; ++bt) {
+    for (int bt = 0; bt < T::NCH / CH; ++bt) {
       f32x4 v[CH], add[CH];
       int at[CH];
       bool ok[CH];
 #pragma unroll
       for (int q = 0; q < CH; ++q) {
-        const int k = (bt * CH + q) * 64 + lane, row = k / 36, c4 = k - row * 36;
-        const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + 144 * wn + 4 * c4;
+        const int k = (bt * CH + q) * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
+        const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + T::WNC * wn + 4 * c4;
         ok[q] = m < P && n < cout;
         const int mc = min(m, P - 1), nc = min(n, cout - 4);   // in bounds for the loads either way
         at[q] = mc * cout + nc;
-        v[q] = *(const f32x4*)(stg + row * 148 + 4 * c4);
+        v[q] = *(const f32x4*)(stg + row * T::LS + 4 * c4);
         if constexpr (OUT != VAE_PART) v[q] += *(const f32x4*)(bias + nc);
         add[q] = f32x4{0.f, 0.f, 0.f, 0.f};
         if constexpr (OUT == VAE_DUPUP) {
@@ -241,8 +246,8 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
       for (int q = 0; q < CH; ++q) {
         const f32x4 o = v[q] + add[q];
         if constexpr (GAM) {   // the output back into its staging row, for the norm below
-          const int k = (bt * CH + q) * 64 + lane, row = k / 36, c4 = k - row * 36;
-          *(f32x4*)(stg + row * 148 + 4 * c4) = o;
+          const int k = (bt * CH + q) * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
+          *(f32x4*)(stg + row * T::LS + 4 * c4) = o;
         }
         if (!ok[q]) continue;
         if constexpr (OUT == VAE_RMS) {
@@ -264,6 +269,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
       }
     }
     if constexpr (GAM) {
+      static_assert(T::WNC == 144, "the norm's layout: rows of 144 a wave");
       // each staged row's sum of squares: lanes 2r and 2r + 1 take its two halves of 72, then
       // swap; at BN 288 the row's other 144 channels are the partner wave's (same pixels)
       const int rr = lane >> 1, hh = lane & 1;
@@ -390,8 +396,13 @@ hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x,
       (out == VAE_DUPUP && (!ep.keep || ep.ft < 1 || ep.kcin <= 0 || (int64_t)cout * ep.ft * 4 % ep.kcin || h % 2 ||
                             w % 2 || ((cout * ep.ft * 4 / ep.kcin) & (cout * ep.ft * 4 / ep.kcin - 1)))))
     return hipErrorInvalidValue;
-  // the wide tile where 288 divides the width (1152, 576, 288 and the 3456 of q|k|v)
+  // the wide tile where 288 divides the width (1152, 576, 288 and the 3456 of q|k|v); a narrow
+  // one for a few channels (the head's 4): 16 columns of MFMA work instead of 144
   if (cout % 288 == 0) return conv_bn<288>(s, taps, up, out, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (cout <= 16 && !ep.gamma) {
+    if (taps == 9 && !up && out == VAE_CLAMP) return launch_conv<16, 9, 0, VAE_CLAMP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    if (taps == 9 && !up && out == VAE_F32) return launch_conv<16, 9, 0, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  }
   return conv_bn<144>(s, taps, up, out, x, wt, bias, ep, y, h, w, c, cout, kp);
 }
 

@@ -63,6 +63,7 @@ CONV_CASES = [  # (h, w, c, cout, taps, up, out, with res)
     (7, 9, 1152, 3456, 1, 0, 0, False),
     (11, 5, 288, 144, 1, 0, 0, True),
     (4, 4, 64, 64, 1, 0, 1, False),
+    (10, 7, 64, 12, 9, 0, 0, True),      # the narrow tile (16 columns) with a residual
 ]
 
 
