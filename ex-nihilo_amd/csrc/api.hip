@@ -456,6 +456,32 @@ static hipError_t gemm_any(hipStream_t s, const exn_w* w, const uint16_t* x, int
   return gemm_wbf16(s, x, lda, w->kind == EXN_Q8_0 ? w->wx : w->wb, n, w->rows, w->cols, epi, ea);
 }
 
+// split-K scratch of a block product's prompt rows: S x rows x N floats with S x tiles <= 256
+// workgroups of 256 x 256, so 256^3 floats hold any of them
+static const int64_t kSplitCap = (int64_t)256 * 256 * 256;
+
+// a block product over a pass's n rows: its first nh rows (the prompt's, in a pass that has
+// them: about one row of tiles) with K split over the chip, the rest as whole tiles, so that
+// the 4096 image rows of a 1024^2 picture fill whole waves.  A full-K tile's rows are the same
+// bits however the rows are tiled, so a cached pass's image rows match the uncached pass's.
+static hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, int64_t nh,
+                           Epi epi, const EpiArgs& ea, float* part) {
+  if (nh > 0 && nh < n && nh <= 1024 && part && (w->kind != EXN_Q8_0 || w->wx_ok)) {
+    const uint16_t* wb = w->kind == EXN_Q8_0 ? w->wx : w->wb;
+    const hipError_t r = gemm_split_rows(s, x, lda, wb, nh, w->rows, w->cols, epi, ea, part, kSplitCap);
+    if (r == hipSuccess) {
+      EpiArgs eb = ea;   // the remaining rows: every row pointer nh rows on
+      eb.n0 = ea.n0 + (int)nh;
+      if (epi == EPI_GATE_ADD) eb.resid = ea.resid + nh * ea.ldy;
+      else if (epi == EPI_F32) eb.y = (float*)ea.y + nh * ea.ldy;
+      else eb.y = (uint16_t*)ea.y + nh * ea.ldy;
+      return gemm_any(s, w, x + nh * lda, lda, n - nh, epi, eb);
+    }
+    if (r != hipErrorNotSupported) return r;
+  }
+  return gemm_any(s, w, x, lda, n, epi, ea);
+}
+
 int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n) {
   TRY(use(ctx));
   TRY(check_gemm(w, n));
@@ -1216,6 +1242,9 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   TRY(dit_buf(d, "x", (size_t)(l * EXN_W) * 4, (void**)&x));
   TRY(dit_buf(d, "y", (size_t)(l * EXN_W) * 2, (void**)&y));
   TRY(dit_buf(d, "qkv", (size_t)(l * 3 * EXN_W) * 2, (void**)&qkv));
+  float* part = nullptr;   // split-K partials of the prompt rows of an uncached pass
+  const int64_t nh = std::max<int64_t>(0, std::min<int64_t>(p - n0, n));
+  if (nh > 0 && nh < n) TRY(dit_buf(d, "split", (size_t)kSplitCap * 4, (void**)&part));
   TRY(dit_buf(d, "q", (size_t)(l * EXN_W) * 2, (void**)&q));
   TRY(dit_buf(d, "att", (size_t)(l * EXN_W) * 2, (void**)&att));
   TRY(dit_buf(d, "ff", (size_t)(l * EXN_F) * 2, (void**)&ff));
@@ -1325,7 +1354,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ea.n0 = n0;
       ea.p = p;
       ea.mstride = ms;
-      HIPCHK(gemm_any(s, L.out, att, EXN_W, n, EPI_GATE_ADD, ea));
+      HIPCHK(block_mm(s, L.out, att, EXN_W, n, nh, EPI_GATE_ADD, ea, part));
     }
     {
       ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes);
@@ -1336,7 +1365,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ea = EpiArgs{};
       ea.y = ff;
       ea.ldy = EXN_F;
-      HIPCHK(gemm_any(s, L.gate_up, y, EXN_W, n, EPI_SWIGLU, ea));
+      HIPCHK(block_mm(s, L.gate_up, y, EXN_W, n, nh, EPI_SWIGLU, ea, part));
     }
     {
       ProfScope ps(d, EXN_PROF_DOWN, 2 * nd * Fd * Wd, nd * Fd * 2 + Fd * Wd * 1.0625 + nd * Wd * 4 * 2);
@@ -1347,7 +1376,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ea.n0 = n0;
       ea.p = p;
       ea.mstride = ms;
-      HIPCHK(gemm_any(s, L.down, ff, EXN_F, n, EPI_GATE_ADD, ea));
+      HIPCHK(block_mm(s, L.down, ff, EXN_F, n, nh, EPI_GATE_ADD, ea, part));
     }
     if (d->trace && (int64_t)(il + 2) * n * EXN_W <= d->trace_cap)
       HIPCHK(hipMemcpyAsync(d->trace + (int64_t)(il + 1) * n * EXN_W, x, (size_t)(n * EXN_W) * 4,

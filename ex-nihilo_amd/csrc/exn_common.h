@@ -149,7 +149,8 @@ __host__ __device__ inline int64_t vt_pos(int64_t k) { return k ^ ((((k >> 2) ^ 
 // q's scale: 1/sqrt(128) x log2(e), so that the attention's scores come out in log2 units
 constexpr float QK_QSCALE = 0.08838834764831845f * 1.4426950408889634f;
 
-enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_GATE_ADD = 2, EPI_SWIGLU = 3, EPI_GELU_BF16 = 4, EPI_F16 = 5, EPI_QKV = 6 };
+enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_GATE_ADD = 2, EPI_SWIGLU = 3, EPI_GELU_BF16 = 4, EPI_F16 = 5, EPI_QKV = 6,
+           EPI_PART = 7 };   // EPI_PART: split K, fp32 sums of workgroup z's k-steps into y + z M ldy
 
 struct EpiArgs {
   void* y;             // EPI_F32 / EPI_BF16 / EPI_GELU_BF16: output rows (ldy elements apart); EPI_SWIGLU: bf16 out (N/2 wide)
@@ -177,6 +178,11 @@ hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* 
                    int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w,
                       int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
+// rows 0 .. M-1 of a product too short to fill the chip (a pass's prompt rows) with its K split
+// over S workgroups a tile into PART (S x M x N floats, at most PART_CAP), then the sums in
+// order through the epilogue: EPI_GATE_ADD, EPI_SWIGLU, EPI_F32, EPI_BF16 or EPI_F16; bf16 weights
+hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
+                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap);
 // the QKV product with the q/k norm, RoPE and the K/V^T stores fused (EPI_QKV), bf16 weights;
 // hipErrorNotSupported when the shapes or alignments do not fit the fused path
 hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t K,

@@ -315,6 +315,8 @@ __device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* 
         const f32x4 v = *(const f32x4*)(stage + row * LS + c4);
         if constexpr (EPI == EPI_F32) {
           *(f32x4*)((float*)ea.y + m * ea.ldy + n) = v;
+        } else if constexpr (EPI == EPI_PART) {
+          *(f32x4*)((float*)ea.y + ((int64_t)blockIdx.z * M + m) * ea.ldy + n) = v;
         } else if constexpr (EPI == EPI_BF16) {
           *(u32x2*)((uint16_t*)ea.y + m * ea.ldy + n) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         } else if constexpr (EPI == EPI_F16) {
@@ -464,7 +466,9 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     bn = in / sz;
   }
   const int64_t m0 = (int64_t)bm * 256, n0 = (int64_t)bn * 256;
-  const int KT = (int)(K / 64);
+  // split K (EPI_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1
+  const int KTT = (int)(K / 64), SK = gridDim.z, zk = blockIdx.z;
+  const int kt0 = (int)((int64_t)KTT * zk / SK), kt1 = (int)((int64_t)KTT * (zk + 1) / SK);
   // DMA: round i of wave w moves rows (i*8 + w)*8 .. +7 of a tile, lane l row +l/8, LDS chunk l%8
   // (global chunk (l%8) ^ swizzle); the k-step is the scalar offset
   const uint16_t* xbase = X + m0 * lda;
@@ -513,7 +517,7 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // B2 lets this step's NDMA DMA parts stay outstanding, and no more: they must all be out
   static_assert(B1 >= NRD && B1 + DSPREAD <= B2 && B2 + NRD <= 2 * NMF, "step schedule");
   auto step = [&](Frag& F0, Frag& F1, int t) {
-    const int cur = t & 1, nx = min(t + 2, KT - 1);
+    const int cur = (t - kt0) & 1, nx = min(t + 2, kt1 - 1);
     // MFMA position x of the step: a lambda unrolled over two loops of NMF, each small
     // enough for the compiler to unroll whole (one loop of 2 NMF is past its limit once
     // anything is added to the body)
@@ -553,15 +557,15 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   };
   Frag F0, F1;
 #pragma unroll
-  for (int p = 0; p < NDMA; ++p) dma_part(0, 0, p);
+  for (int p = 0; p < NDMA; ++p) dma_part(kt0, 0, p);
   LDS_VMCNT0_BARRIER();
 #pragma unroll
-  for (int p = 0; p < NDMA; ++p) dma_part(min(1, KT - 1), 1, p);
+  for (int p = 0; p < NDMA; ++p) dma_part(min(kt0 + 1, kt1 - 1), 1, p);
 #pragma unroll
   for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
   // past the end the DMA re-reads the last step into the free stage, and nothing reads it:
   // no branch, so the order holds
-  for (int t = 0; t < KT; ++t) step(F0, F1, t);
+  for (int t = kt0; t < kt1; ++t) step(F0, F1, t);
   LDS_VMCNT0_BARRIER();   // the last DMA has landed before the epilogue takes the LDS over
   if constexpr (HEADS)
     epilogue_qkv<MI, NI>(acc, (float*)smem + wave * (16 * 132), m0 + wm * WM, n0 + wn * WN, lane, M, ea);
@@ -571,7 +575,7 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
 
 template <int EPI>
 static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* wb, int64_t M, int64_t N,
-                            int64_t K, const EpiArgs& ea) {
+                            int64_t K, const EpiArgs& ea, int split = 1) {
   const size_t shm = 2 * 65536;
   constexpr int NW = 8;
   auto kern = k_gemm_bt<EPI, NW>;
@@ -581,8 +585,78 @@ static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const
     if (e != hipSuccess) return e;
     attr = true;
   }
-  dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256));
+  dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256), (unsigned)split);
   hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, M, N, K, ea);
+  return hipGetLastError();
+}
+
+// the S partial sums of a split product in order, through the epilogue: 4 output columns a
+// thread (SwiGLU: 4 output columns from their gate and up columns, interleaved by 32)
+template <int EPI>
+__global__ void __launch_bounds__(256)
+k_split_sum(int S, int64_t M, int64_t N, const float* __restrict__ part, EpiArgs ea) {
+  constexpr int OC = EPI == EPI_SWIGLU ? 2 : 1;   // input columns an output column takes
+  const int64_t NO = N / OC, i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * NO / 4) return;
+  const int64_t m = i / (NO / 4), c = (i % (NO / 4)) * 4;   // output row, first output column
+  auto sum = [&](int64_t col) {
+    f32x4 v = *(const f32x4*)(part + m * N + col);
+    for (int z = 1; z < S; ++z) v += *(const f32x4*)(part + ((int64_t)z * M + m) * N + col);
+    return v;
+  };
+  if constexpr (EPI == EPI_SWIGLU) {
+    const int64_t gc = 64 * (c >> 5) + (c & 31);   // the gate column of output column c; up is 32 on
+    const f32x4 v = sum(gc), u = sum(gc + 32);
+    *(u32x2*)((uint16_t*)ea.y + m * ea.ldy + c) =
+        u32x2{pack_bf16x2(silu_bf16out(v[0]) * u[0], silu_bf16out(v[1]) * u[1]),
+              pack_bf16x2(silu_bf16out(v[2]) * u[2], silu_bf16out(v[3]) * u[3])};
+  } else {
+    const f32x4 v = sum(c);
+    if constexpr (EPI == EPI_GATE_ADD) {
+      const float* gr = ea.gate + (ea.n0 + m < ea.p ? ea.mstride : 0) + c;
+      f32x4* x = (f32x4*)(ea.resid + m * ea.ldy + c);
+      f32x4 xv = *x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[e] = xv[e] + tanh_f(gr[e]) * v[e];
+      *x = xv;
+    } else if constexpr (EPI == EPI_F32) {
+      *(f32x4*)((float*)ea.y + m * ea.ldy + c) = v;
+    } else if constexpr (EPI == EPI_BF16) {
+      *(u32x2*)((uint16_t*)ea.y + m * ea.ldy + c) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    } else if constexpr (EPI == EPI_F16) {
+      *(u32x2*)((uint16_t*)ea.y + m * ea.ldy + c) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+    }
+  }
+}
+
+hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
+                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap) {
+  if (M == 0) return hipSuccess;
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  // S workgroups a tile, about one wave in all, at least 4 k-steps each
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  int64_t S = 256 / tiles;
+  if (S > K / 64 / 4) S = K / 64 / 4;
+  if (S > 16) S = 16;
+  if (S < 1) S = 1;
+  const bool ok = K % 64 == 0 && lda % 8 == 0 && N % 256 == 0 && a16(x) && a16(w) && a16(part) &&
+                  M * lda < (int64_t)1 << 30 && N * K < (int64_t)1 << 30 && S * M * N <= part_cap &&
+                  (epi == EPI_GATE_ADD || epi == EPI_SWIGLU || epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_F16);
+  if (!ok) return hipErrorNotSupported;
+  EpiArgs pa{};
+  pa.y = part;
+  pa.ldy = N;
+  hipError_t e = launch_bt<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
+  if (e != hipSuccess) return e;
+  const int64_t threads = M * (epi == EPI_SWIGLU ? N / 2 : N) / 4;
+  const dim3 g((unsigned)((threads + 255) / 256));
+  switch (epi) {
+    case EPI_GATE_ADD: hipLaunchKernelGGL(k_split_sum<EPI_GATE_ADD>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL(k_split_sum<EPI_SWIGLU>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    case EPI_F32: hipLaunchKernelGGL(k_split_sum<EPI_F32>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    case EPI_BF16: hipLaunchKernelGGL(k_split_sum<EPI_BF16>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    default: hipLaunchKernelGGL(k_split_sum<EPI_F16>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+  }
   return hipGetLastError();
 }
 
