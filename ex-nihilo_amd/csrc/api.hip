@@ -586,7 +586,7 @@ int exn_qkv_prep(exn_ctx* ctx, const uint16_t* qkv, int64_t n, const float* wq, 
   TRY(use(ctx));
   if (n < 0 || row0 < 0 || row0 + n > lcap || !qkv || !wq || !wk || !cs || !q || !k || !vt)
     FAIL(EXN_EINVAL, "qkv_prep arguments");
-  HIPCHK(qkv_prep(ctx->stream, qkv, n, wq, wk, cs, q, k, vt, row0, lcap));
+  HIPCHK(qkv_prep(ctx->stream, qkv, n, wq, wk, cs, q, k, vt, row0, lcap, n));
   return EXN_OK;
 }
 
@@ -1312,7 +1312,8 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 0 * EXN_W, y, 1));
     }
     // the QKV product with qk-norm, RoPE and the K/V^T stores in its epilogue (bf16 weights),
-    // else the product to fp16 rows and qkv_prep over them
+    // else the product to fp16 rows and qkv_prep over them.  (Splitting an uncached pass's
+    // prompt rows off, as the other products do, measured no faster here: 768 + 48 tiles.)
     bool fused = false;
     if (L.qkv->kind != EXN_Q8_0 || L.qkv->wx_ok) {
       ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
@@ -1323,6 +1324,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ea.cs = d->cs;
       ea.qscale = QK_QSCALE;
       ea.q = q;
+      ea.qld = n;
       ea.kc = d->kc[(size_t)il];
       ea.vt = d->vt[(size_t)il];
       ea.lcap = d->lcap;
@@ -1339,7 +1341,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
         HIPCHK(gemm_any(s, L.qkv, y, EXN_W, n, EPI_F16, ea));
       }
       ProfScope ps(d, EXN_PROF_QKV_PREP, 0, qkv_bytes);
-      HIPCHK(qkv_prep(s, qkv, n, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap));
+      HIPCHK(qkv_prep(s, qkv, n, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap, n));
     }
     {
       ProfScope ps(d, EXN_PROF_ATTEND, 4.0 * EXN_HD * EXN_H * pairs, nd * Wd * 2 * 2 + 2.0 * l * Wd * 2);

@@ -185,7 +185,7 @@ hipError_t silu(hipStream_t s, int64_t count, float* x) {
 __global__ void __launch_bounds__(256)
 k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict__ wq, const float* __restrict__ wk,
            const float* __restrict__ cs, float qscale, uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
-           uint16_t* __restrict__ vt, int64_t row0, int64_t lcap) {
+           uint16_t* __restrict__ vt, int64_t row0, int64_t lcap, int64_t qld) {
   __shared__ uint16_t tile[64][128 + 2];
   const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * 64;
@@ -243,7 +243,7 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
       ok[e] = pack_f16x2(ak * cx - bk * cy, ak * cy + bk * cx);
     }
     if (t < n) {
-      *(u32x4*)(q + ((int64_t)h * n + t) * 128 + d8) = oq;
+      *(u32x4*)(q + ((int64_t)h * qld + t) * 128 + d8) = oq;
       *(u32x4*)(kc + ((int64_t)h * lcap + row0 + t) * 128 + d8) = ok;
     }
   }
@@ -268,12 +268,13 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
 }
 
 hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk, const float* cs,
-                    uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap) {
+                    uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap,
+                    int64_t qld) {
   if (n == 0) return hipSuccess;
   // q is scaled by 1/sqrt(128) * log2(e): the attention's scores are then in log2 units
   const float qscale = QK_QSCALE;
   hipLaunchKernelGGL(k_qkv_prep, dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, n, wq, wk, cs, qscale, q, k, vt,
-                     row0, lcap);
+                     row0, lcap, qld);
   return hipGetLastError();
 }
 

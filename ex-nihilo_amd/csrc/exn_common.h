@@ -171,6 +171,7 @@ struct EpiArgs {
   uint16_t* kc;
   uint16_t* vt;
   int64_t lcap;
+  int64_t qld;   // EPI_QKV: Q's rows a head (the pass's; 0: M)
 };
 
 // Y = X W^T with X bf16 (M x K, lda), W Q8_0 SoA (qs N x K int8, d N x K/32 fp16) or bf16 (N x K)
@@ -211,7 +212,8 @@ hipError_t swiglu(hipStream_t s, int64_t n, int f, const uint16_t* gu, uint16_t*
 hipError_t gelu_tanh(hipStream_t s, int64_t count, float* x);
 hipError_t silu(hipStream_t s, int64_t count, float* x);
 hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk,
-                    const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap);
+                    const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap,
+                    int64_t qld);
 hipError_t latent_rows(hipStream_t s, const float* latent, int64_t nimg, float* rows);
 hipError_t rows_to_latent(hipStream_t s, const float* rows, int64_t nimg, float* latent);
 hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float ds);

@@ -403,7 +403,7 @@ __device__ __forceinline__ void epilogue_qkv(f32x4 (&acc)[MI][NI], float* stage,
         const float a0 = v[0] * w[0], a1 = v[1] * w[1], a2 = v[2] * w[2], a3 = v[3] * w[3];
         const u32x2 o = {pack_f16x2((a0 * cs[0] - a1 * cs[1]) * sc, (a0 * cs[1] + a1 * cs[0]) * sc),
                          pack_f16x2((a2 * cs[2] - a3 * cs[3]) * sc, (a2 * cs[3] + a3 * cs[2]) * sc)};
-        uint16_t* dst = part == 0 ? ea.q + ((int64_t)h * M + m) * EXN_HD + c4
+        uint16_t* dst = part == 0 ? ea.q + ((int64_t)h * (ea.qld ? ea.qld : M) + m) * EXN_HD + c4
                                   : ea.kc + ((int64_t)h * ea.lcap + ea.n0 + m) * EXN_HD + c4;
         *(u32x2*)dst = o;
       }
