@@ -432,6 +432,38 @@ __device__ __forceinline__ void epilogue_qkv(f32x4 (&acc)[MI][NI], float* stage,
   }
 }
 
+// SwiGLU's epilogue, in registers first: a wave's 64 columns are 32 gate columns then their 32
+// up columns (gate_up interleaved by 32), so the lane holding gate column block j holds its up
+// block j + 2, and silu(gate) x up is computed on the accumulators.  Only the bf16 outputs
+// (128 rows x 32 columns a wave, rows 40 halves apart) go through LDS, to come back as 8
+// consecutive columns a lane for 16-byte stores.
+template <int MI, int NI>
+__device__ __forceinline__ void epilogue_swiglu(const f32x4 (&acc)[MI][NI], uint16_t* stage, int64_t wrow, int64_t wcol,
+                                                int lane, int64_t M, int64_t N, const EpiArgs& ea) {
+  static_assert(NI == 4, "a wave's 64 columns: one gate/up pair of 32");
+  constexpr int LS = 40;
+  const int c16 = lane & 15, q4 = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float o = silu_bf16out(acc[i][j][r]) * acc[i][j + 2][r];
+        stage[(16 * i + 4 * q4 + r) * LS + 16 * j + c16] = (uint16_t)(pack_bf16x2(o, 0.f) & 0xFFFF);
+      }
+  // rows of 32 outputs: 4 chunks of 8; 16 rows a wave instruction, 16 MI / 16 = MI instructions
+  const int64_t col = wcol / 2 + 8 * (lane & 3);
+  if (2 * (wcol / 2) >= N) return;
+#pragma unroll
+  for (int it = 0; it < MI; ++it) {
+    const int row = 16 * it + (lane >> 2);
+    const int64_t m = wrow + row;
+    const u32x4 v = *(const u32x4*)(stage + row * LS + 8 * (lane & 3));
+    if (m < M) *(u32x4*)((uint16_t*)ea.y + m * ea.ldy + col) = v;
+  }
+}
+
 // One 16-byte DMA lane of a tile: the buffer's extent makes rows past the matrix read as zeros.
 __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
   __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
@@ -569,6 +601,8 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   LDS_VMCNT0_BARRIER();   // the last DMA has landed before the epilogue takes the LDS over
   if constexpr (HEADS)
     epilogue_qkv<MI, NI>(acc, (float*)smem + wave * (16 * 132), m0 + wm * WM, n0 + wn * WN, lane, M, ea);
+  else if constexpr (EPI == EPI_SWIGLU)
+    epilogue_swiglu<MI, NI>(acc, (uint16_t*)smem + wave * (WM * 40), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
   else
     epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
