@@ -1250,11 +1250,15 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   TRY(dit_buf(d, "ff", (size_t)(l * EXN_F) * 2, (void**)&ff));
   TRY(dit_buf(d, "tok", (size_t)((nimg > nref ? nimg : nref) * EXN_LAT) * 4, (void**)&tok));
   TRY(dit_buf(d, "vrows", (size_t)(nimg * EXN_LAT) * 4, (void**)&vrows));
+  // split-K partials of the edge products with few tiles (proj_out's 64 columns): 8 slices
+  float* epart = nullptr;
+  const int64_t epart_cap = 8 * std::max<int64_t>(nimg, 256) * EXN_LAT;
+  TRY(dit_buf(d, "epart", (size_t)epart_cap * 4, (void**)&epart));
 
   // an edge product in fp32: Y (m rows, ldy apart) = X (m rows of the matrix's inputs) W^T
   auto edge_mm = [&](int e, const float* xin, int64_t m, float* yout, int gelu) {
     const exn_w* W = d->edge[e];
-    return gemm_f32(s, xin, W->cols, W->qs, W->d, W->wb, m, W->rows, W->cols, yout, W->rows, gelu);
+    return gemm_f32(s, xin, W->cols, W->qs, W->d, W->wb, m, W->rows, W->cols, yout, W->rows, gelu, epart, epart_cap);
   };
   {
   ProfScope prologue(d, EXN_PROF_EDGE, 0, 0);

@@ -742,8 +742,12 @@ k_gemm_f32(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ 
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
   const int lr = tid >> 2, lk = (tid & 3) * 8;   // loader: row lr of the tile, k lk .. lk+7
+  // split K: workgroup z of gridDim.z takes blocks of 32 kb0 .. kb1-1 and writes its raw sums
+  // to Y + z M ldy (gelu then applies after the sum)
+  const int64_t KB = K / 32, kb0 = KB * blockIdx.z / gridDim.z, kb1 = KB * (blockIdx.z + 1) / gridDim.z;
+  if (gridDim.z > 1) Y += (int64_t)blockIdx.z * M * ldy;
   float acc[4][4] = {};
-  for (int64_t k0 = 0; k0 < K; k0 += 32) {
+  for (int64_t k0 = 32 * kb0; k0 < 32 * kb1; k0 += 32) {
     {
       const int64_t m = min(m0 + lr, M - 1);
       const f32x4* src = (const f32x4*)(X + m * ldx + k0 + lk);
@@ -790,15 +794,41 @@ k_gemm_f32(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t n = n0 + tx + 16 * j;
-      if (n < N) Y[m * ldy + n] = gelu ? gelu_tanh_f(acc[i][j]) : acc[i][j];
+      if (n < N) Y[m * ldy + n] = gelu && gridDim.z == 1 ? gelu_tanh_f(acc[i][j]) : acc[i][j];
     }
   }
 }
 
+// Y = the S partial sums of a split edge product in order (M x N, ldy apart), GELU-tanh when asked
+__global__ void __launch_bounds__(256)
+k_f32_part_sum(int S, int64_t M, int64_t N, const float* __restrict__ part, float* __restrict__ Y, int64_t ldy,
+               int gelu) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float v = part[i];
+  for (int z = 1; z < S; ++z) v += part[(int64_t)z * M * N + i];
+  Y[m * ldy + n] = gelu ? gelu_tanh_f(v) : v;
+}
+
 hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
-                    const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int gelu) {
+                    const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int gelu,
+                    float* part, int64_t part_cap) {
   if (K % 32 || M <= 0) return M == 0 ? hipSuccess : hipErrorInvalidValue;
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+  // few tiles over a long K (proj_out: 64 tiles of 64 x 64 over 4096): K split over up to 8
+  // workgroups a tile, at least 8 blocks of 32 each, their sums added in order after
+  const int64_t tiles = (int64_t)grid.x * grid.y;
+  int64_t S = tiles < 128 ? 256 / tiles : 1;
+  if (S > 8) S = 8;
+  if (S > K / 256) S = K / 256;
+  if (S >= 2 && part && S * M * N <= part_cap) {
+    grid.z = (unsigned)S;
+    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, M, N, K, part, N, gelu);
+    hipLaunchKernelGGL(k_f32_part_sum, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, s, (int)S, M, N, part, y,
+                       ldy, gelu);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, M, N, K, y, ldy, gelu);
   return hipGetLastError();
 }
