@@ -272,30 +272,59 @@ __device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* 
   // this lane's 4 columns (SwiGLU: 4 output columns, 8 NI / 4 lanes a row; others 16 NI / 4)
   constexpr int LPR = EPI == EPI_SWIGLU ? 2 * NI : 4 * NI;
   const int c4 = (lane % LPR) * 4;
+  // the gated residual's rows are loaded two 32-row chunks at a time, before either is stored:
+  // a wave waits out two round trips to HBM instead of one a row group (with loads and stores
+  // both in flight the wait counter only tells when all have ended, so every load issued after
+  // a store would be waited for alone).  The first pair goes out with the gate's loads.
+  constexpr int IT = 32 * LPR / 64;
+  f32x4 rb[2][IT];
+  auto load_pair = [&](int i2) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int64_t m = wrow + 32 * (i2 + c) + it * (64 / LPR) + lane / LPR, n = wcol + c4;
+        rb[c][it] = (i2 + c < MI / 2 && m < M && n < N) ? *(const f32x4*)(ea.resid + m * ea.ldy + n)
+                                                         : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  };
+  // the gates' tanh is taken after the first pair's wait (below), so no wait of its own
   f32x4 g0 = {0.f, 0.f, 0.f, 0.f}, g1 = g0;
   if constexpr (EPI == EPI_GATE_ADD) {
     const int64_t n = wcol + c4;
     if (n < N) {
-      const f32x4 a = *(const f32x4*)(ea.gate + n), b = *(const f32x4*)(ea.gate + ea.mstride + n);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        g0[e] = tanh_f(a[e]);
-        g1[e] = tanh_f(b[e]);
-      }
+      g0 = *(const f32x4*)(ea.gate + n);
+      g1 = *(const f32x4*)(ea.gate + ea.mstride + n);
     }
+    load_pair(0);
   }
   // accumulators of v_mfma_f32_16x16x32: lane l holds column l%16, rows 4*(l/16) + r
   const int c16 = lane & 15, q4 = lane >> 4;
 #pragma unroll
   for (int i2 = 0; i2 < MI / 2; ++i2) {
+    if constexpr (EPI == EPI_GATE_ADD) {
+      if (i2 % 2 == 0 && i2 > 0) load_pair(i2);
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int j = 0; j < NI; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) stage[(16 * h + 4 * q4 + r) * LS + 16 * j + c16] = acc[2 * i2 + h][j][r];
+    if constexpr (EPI == EPI_GATE_ADD) {
+      // the pair's residual loads have landed: one wait here, outside the per-row branches
+      // (a wait inside one would be repeated at every row after it)
+      if (i2 % 2 == 0) __builtin_amdgcn_s_waitcnt((0x0) | (0x7 << 4) | (0xF << 8) | (0x0 << 14));   // vmcnt(0)
+      if (i2 == 0) {
 #pragma unroll
-    for (int it = 0; it < 32 * LPR / 64; ++it) {
+        for (int e = 0; e < 4; ++e) {
+          g0[e] = tanh_f(g0[e]);
+          g1[e] = tanh_f(g1[e]);
+        }
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
       const int row = it * (64 / LPR) + lane / LPR;
       const int64_t m = wrow + 32 * i2 + row;
       if (m >= M) continue;
@@ -326,11 +355,10 @@ __device__ __forceinline__ void epilogue_lds(const f32x4 (&acc)[MI][NI], float* 
               u32x2{pack_bf16x2(gelu_tanh_f(v[0]), gelu_tanh_f(v[1])), pack_bf16x2(gelu_tanh_f(v[2]), gelu_tanh_f(v[3]))};
         } else if constexpr (EPI == EPI_GATE_ADD) {
           const f32x4 g = (ea.n0 + m < ea.p) ? g1 : g0;
-          f32x4* x = (f32x4*)(ea.resid + m * ea.ldy + n);
-          f32x4 xv = *x;
+          f32x4 xv = rb[i2 % 2][it];
 #pragma unroll
           for (int e = 0; e < 4; ++e) xv[e] = xv[e] + g[e] * v[e];
-          *x = xv;
+          *(f32x4*)(ea.resid + m * ea.ldy + n) = xv;
         }
       }
     }
