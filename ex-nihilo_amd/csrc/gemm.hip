@@ -382,8 +382,11 @@ __device__ __forceinline__ void epilogue_qkv(f32x4 (&acc)[MI][NI], float* stage,
   const int part = (int)(wcol / EXN_W), h = (int)((wcol % EXN_W) / EXN_HD);   // part 0 q, 1 k, 2 v
   const int c16 = lane & 15, q4 = lane >> 4;
   const int c4 = (lane & 31) * 4;
-  // the cos/sin of a 16-row block (2 rows a wave instruction, 8 loads a lane) go out one block
-  // ahead of their use -- the first before the RMS -- so their latency hides under the work
+  // the cos/sin of a 16-row block: 2 rows a wave instruction, 8 loads a lane.  Blocks 0 and 1
+  // go out before the RMS; a buffer is refilled with block i + 2 once block i is stored, and
+  // one wait before blocks 0 and 2 (outside the per-row branches) covers a pair: with loads
+  // and stores both in flight the wait counter only tells when all have ended, so waits
+  // inside the row loop would hold each store for the one before it
   auto cs_load = [&](f32x4 (&dst)[8], int i) {
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
@@ -391,9 +394,21 @@ __device__ __forceinline__ void epilogue_qkv(f32x4 (&acc)[MI][NI], float* stage,
       dst[it] = *(const f32x4*)(ea.cs + (ea.n0 + m) * EXN_HD + c4);
     }
   };
-  f32x4 csa[8], csb[8];
-  if (part < 2) cs_load(csa, 0);
+  // a wave's 64 x 128 accumulators through LDS 16 rows at a time
+  auto stage_block = [&](int i) {
+    // accumulators of v_mfma_f32_16x16x32: lane l holds column l%16, rows 4*(l/16) + r
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) stage[(4 * q4 + r) * LS + 16 * j + c16] = acc[i][j][r];
+  };
+  // q and k, and v, each in a loop of its own: the two paths meet only at the end, so the
+  // wait counter's state is exact inside each
   if (part < 2) {
+    f32x4 csa[8], csb[8];
+    cs_load(csa, 0);
+    if (MI > 1) cs_load(csb, 1);
+    const f32x4 w = *(const f32x4*)((part == 0 ? ea.wq : ea.wk) + c4);
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -405,22 +420,13 @@ __device__ __forceinline__ void epilogue_qkv(f32x4 (&acc)[MI][NI], float* stage,
 #pragma unroll
         for (int j = 0; j < NI; ++j) acc[i][j][r] *= inv;
       }
-  }
-  f32x4 w = {1.f, 1.f, 1.f, 1.f};
-  if (part == 0) w = *(const f32x4*)(ea.wq + c4);
-  if (part == 1) w = *(const f32x4*)(ea.wk + c4);
-  const float sc = part == 0 ? ea.qscale : 1.f;
+    const float sc = part == 0 ? ea.qscale : 1.f;
 #pragma unroll
-  for (int i = 0; i < MI; ++i) {
-    // accumulators of v_mfma_f32_16x16x32: lane l holds column l%16, rows 4*(l/16) + r
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) stage[(4 * q4 + r) * LS + 16 * j + c16] = acc[i][j][r];
-    const int64_t mb = wrow + 16 * i;   // the output row of the 16 staged rows' first
-    if (part < 2) {
+    for (int i = 0; i < MI; ++i) {
+      stage_block(i);
+      const int64_t mb = wrow + 16 * i;   // the output row of the 16 staged rows' first
+      if (i % 2 == 0) __builtin_amdgcn_s_waitcnt((0x0) | (0x7 << 4) | (0xF << 8) | (0x0 << 14));   // vmcnt(0)
       f32x4(&csc)[8] = i % 2 == 0 ? csa : csb;
-      if (i + 1 < MI) cs_load(i % 2 == 0 ? csb : csa, i + 1);
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int row = 2 * it + (lane >> 5);
@@ -435,7 +441,13 @@ __device__ __forceinline__ void epilogue_qkv(f32x4 (&acc)[MI][NI], float* stage,
                                   : ea.kc + ((int64_t)h * ea.lcap + ea.n0 + m) * EXN_HD + c4;
         *(u32x2*)dst = o;
       }
-    } else {
+      if (i + 2 < MI) cs_load(csc, i + 2);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      stage_block(i);
+      const int64_t mb = wrow + 16 * i;
       const int64_t kb = ea.n0 + mb;   // the key of the first staged row
       if (kb % 16 == 0 && mb + 16 <= M) {
         // one aligned group of 16 keys: V^T column kb + c holds key kb + vt_pos(c); a lane
