@@ -208,63 +208,81 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
 #pragma unroll
         for (int r = 0; r < 4; ++r) stg[(16 * i + 4 * q4 + r) * T::LS + 16 * j + lo] = acc[2 * half + i][j][r];
     __syncthreads();
-    // NCH chunks a lane (18 at WNC 144), in batches of 6 (3 at BN 288, where half the
-    // accumulators are still live)
+    // NCH chunks a lane (18 at WNC 144), 4 channels of one pixel each, in two passes.  Pass 1
+    // adds bias and the residual or the DupUp3D gather in place in the staging rows, in batches
+    // of 6 chunks (3 at BN 288, where half the accumulators are still live); with no stores
+    // among them the loads of one batch can be in flight while the last is summed.  Pass 2
+    // stores the rows: no load is left to wait for.  (Stores among the loads would make
+    // every batch wait for the stores before it, a round trip to HBM each.)
     constexpr int CH = BN == 288 ? (OUT == VAE_DUPUP || GAM ? 2 : 3) : (T::NCH < 6 ? T::NCH : 6);
     static_assert(T::NCH % CH == 0, "whole batches");
+    if constexpr (OUT != VAE_PART) {
+#pragma unroll BN == 288 ? 2 : T::NCH / CH
+      for (int bt = 0; bt < T::NCH / CH; ++bt) {
+        f32x4 v[CH], add[CH];
 #pragma unroll
-    for (int bt = 0; bt < T::NCH / CH; ++bt) {
-      f32x4 v[CH], add[CH];
-      int at[CH];
-      bool ok[CH];
+        for (int q = 0; q < CH; ++q) {
+          const int k = (bt * CH + q) * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
+          const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + T::WNC * wn + 4 * c4;
+          const int mc = min(m, P - 1), nc = min(n, cout - 4);   // in bounds for the loads either way
+          v[q] = *(const f32x4*)(stg + row * T::LS + 4 * c4);
+          v[q] += *(const f32x4*)(bias + nc);
+          add[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (OUT == VAE_DUPUP) {
+            // channel c of pixel (yy, xx) adds keep's channel j / rep of pixel (yy/2, xx/2),
+            // j = ((c ft + ft - 1) 2 + yy%2) 2 + xx%2, rep = cout ft 4 / kcin (a power of two)
+            int yy = (int)(((float)mc + 0.5f) * winv);   // mc / W, corrected to exact below
+            yy -= yy * W > mc;
+            yy += (yy + 1) * W <= mc;
+            const int xx = mc - yy * W;
+            const float* kr = ep.keep + (((yy >> 1) * (W >> 1) + (xx >> 1)) * ep.kcin);
+            const int j0 = ((nc * ep.ft + ep.ft - 1) * 2 + (yy & 1)) * 2 + (xx & 1);
+            // keep channel of channel nc + e: (j0 >> rsh) + e * kstep, kstep = kcin / cout (rep
+            // divides 4 ft then).  At kstep 1 that is channels nc .. nc + 3, at kstep 2 channels
+            // 2 nc + d + 0, 2, 4, 6 (d = 0 or 1): one or two aligned 16-byte loads.
+            const int kstep = (4 * ep.ft) >> rsh, k0 = j0 >> rsh;
+            if (kstep == 1 && (4 * ep.ft) % (1 << rsh) == 0) {
+              add[q] = *(const f32x4*)(kr + k0);
+            } else if (kstep == 2 && (4 * ep.ft) % (1 << rsh) == 0) {
+              const f32x4 t0 = *(const f32x4*)(kr + 2 * nc), t1 = *(const f32x4*)(kr + 2 * nc + 4);
+              const int d = k0 - 2 * nc;
+              add[q] = d ? f32x4{t0[1], t0[3], t1[1], t1[3]} : f32x4{t0[0], t0[2], t1[0], t1[2]};
+            } else {
 #pragma unroll
-      for (int q = 0; q < CH; ++q) {
-        const int k = (bt * CH + q) * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
-        const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + T::WNC * wn + 4 * c4;
-        ok[q] = m < P && n < cout;
-        const int mc = min(m, P - 1), nc = min(n, cout - 4);   // in bounds for the loads either way
-        at[q] = mc * cout + nc;
-        v[q] = *(const f32x4*)(stg + row * T::LS + 4 * c4);
-        if constexpr (OUT != VAE_PART) v[q] += *(const f32x4*)(bias + nc);
-        add[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (OUT == VAE_DUPUP) {
-          // channel c of pixel (yy, xx) adds keep's channel j / rep of pixel (yy/2, xx/2),
-          // j = ((c ft + ft - 1) 2 + yy%2) 2 + xx%2, rep = cout ft 4 / kcin (a power of two)
-          int yy = (int)(((float)mc + 0.5f) * winv);   // mc / W, corrected to exact below
-          yy -= yy * W > mc;
-          yy += (yy + 1) * W <= mc;
-          const int xx = mc - yy * W;
-          const float* kr = ep.keep + (((yy >> 1) * (W >> 1) + (xx >> 1)) * ep.kcin);
-          const int j0 = ((nc * ep.ft + ep.ft - 1) * 2 + (yy & 1)) * 2 + (xx & 1);
+              for (int e = 0; e < 4; ++e) add[q][e] = kr[(j0 + 4 * ep.ft * e) >> rsh];
+            }
+          } else if constexpr (OUT == VAE_F32 || OUT == VAE_BF16) {
+            if (ep.res) add[q] = *(const f32x4*)(ep.res + (int64_t)mc * cout + nc);
+          }
+        }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) add[q][e] = kr[(j0 + 4 * ep.ft * e) >> rsh];
-        } else if constexpr (OUT == VAE_F32 || OUT == VAE_BF16) {
-          if (ep.res) add[q] = *(const f32x4*)(ep.res + at[q]);
+        for (int q = 0; q < CH; ++q) {
+          const int k = (bt * CH + q) * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
+          *(f32x4*)(stg + row * T::LS + 4 * c4) = v[q] + add[q];
         }
       }
+    }
+#pragma unroll BN == 288 ? 3 : 6
+    for (int q = 0; q < T::NCH; ++q) {
+      const int k = q * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
+      const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + T::WNC * wn + 4 * c4;
+      if (m >= P || n >= cout) continue;
+      const int at = m * cout + n;
+      const f32x4 o = *(const f32x4*)(stg + row * T::LS + 4 * c4);
+      if constexpr (OUT == VAE_RMS) {
+      } else if constexpr (OUT == VAE_BF16) {
+        *(u32x2*)((uint16_t*)Y + at) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+      } else if constexpr (OUT == VAE_PART) {
+        *(f32x4*)((float*)Y + (int64_t)z * P * cout + at) = o;
+      } else if constexpr (OUT == VAE_CLAMP) {
+        f32x4 c;
 #pragma unroll
-      for (int q = 0; q < CH; ++q) {
-        const f32x4 o = v[q] + add[q];
-        if constexpr (GAM) {   // the output back into its staging row, for the norm below
-          const int k = (bt * CH + q) * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
-          *(f32x4*)(stg + row * T::LS + 4 * c4) = o;
-        }
-        if (!ok[q]) continue;
-        if constexpr (OUT == VAE_RMS) {
-        } else if constexpr (OUT == VAE_BF16) {
-          *(u32x2*)((uint16_t*)Y + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-        } else if constexpr (OUT == VAE_PART) {
-          *(f32x4*)((float*)Y + (int64_t)z * P * cout + at[q]) = o;
-        } else if constexpr (OUT == VAE_CLAMP) {
-          f32x4 c;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) c[e] = fminf(1.f, fmaxf(-1.f, o[e]));
-          *(f32x4*)((float*)Y + at[q]) = c;
-        } else {
-          if (OUT != VAE_DUPUP || Y) *(f32x4*)((float*)Y + at[q]) = o;   // DupUp: no fp32 out when Y is null
-          if constexpr (OUT == VAE_F32 || OUT == VAE_DUPUP) {
-            if (ep.y2) *(u32x2*)(ep.y2 + at[q]) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-          }
+        for (int e = 0; e < 4; ++e) c[e] = fminf(1.f, fmaxf(-1.f, o[e]));
+        *(f32x4*)((float*)Y + at) = c;
+      } else {
+        if (OUT != VAE_DUPUP || Y) *(f32x4*)((float*)Y + at) = o;   // DupUp: no fp32 out when Y is null
+        if constexpr (OUT == VAE_F32 || OUT == VAE_DUPUP) {
+          if (ep.y2) *(u32x2*)(ep.y2 + at) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         }
       }
     }
