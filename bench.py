@@ -188,8 +188,8 @@ def main():
         traffic_from(*a.traffic_from)
         return
     if a.gpus != 1:
-        print("bench.py: this build measures one GPU; --gpus %d is not supported (the step shards over image "
-              "rows across GPUs only by design, see DESIGN.md)" % a.gpus, file=sys.stderr)
+        print("bench.py: the step runs on one GPU; --gpus %d is not supported (a split of the image rows "
+              "across GPUs is designed, not built)" % a.gpus, file=sys.stderr)
         sys.exit(2)
     if a.vae_only:
         vae_only(a.steps, a.warmup)
