@@ -10,10 +10,11 @@
 // x_gate_add (src/cuda/dit.cu:34-41), x_swiglu2 (:186-192) and x_gelu_tanh
 // (:194-199) into the product's store.
 //
-// Tiles: BM x BN per workgroup, BK = 64 (two Q8_0 blocks) per step, waves
-// of WM x WN, each a grid of 32x32 accumulators (v_mfma_f32_32x32x16_bf16).
-// LDS is double-buffered; the next step's global loads are in registers
-// while the current step's MFMAs run.
+// The Q8_0 kernel (k_gemm): BM x BN per workgroup, BK = 64 (two Q8_0 blocks)
+// per step, waves of WM x WN, each a grid of 32x32 accumulators
+// (v_mfma_f32_32x32x16_bf16); LDS is double-buffered, the next step's global
+// loads are in registers while the current step's MFMAs run.  The kernel on
+// resident bf16 weights (k_gemm_bt, below) is the one the step uses.
 #include "exn_common.h"
 
 namespace exn {

@@ -193,8 +193,8 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
 
   // The epilogue through LDS (free now), 32 of the wave's pixels at a time: the wave stages its
   // 32 x 144 block (row stride 148 floats), then moves it as 16-byte chunks, 4 channels of one
-  // pixel a lane: bias, and the residual or the DupUp3D gather, loaded for a batch of chunks
-  // before any of their stores.
+  // pixel a lane: bias, and the residual or the DupUp3D gather, summed into the staged rows
+  // first, then the stores.
   float* stg = (float*)smem + wave * (32 * T::LS);
   const float winv = 1.f / (float)W;
   const int rsh = OUT == VAE_DUPUP ? __builtin_ctz((unsigned)(cout * ep.ft * 4 / ep.kcin)) : 0;
