@@ -115,7 +115,7 @@ def traffic_from(fetch_db, write_db):
 
     f, w = per_kernel(fetch_db, "FETCH_SIZE"), per_kernel(write_db, "WRITE_SIZE")
     copy = [k for k in f if "copyBuffer" in k]
-    gemm = [k for k in f if "k_gemm_bt<3>" in k]
+    gemm = [k for k in f if "k_gemm_bt<3>" in k or "k_gemm_bt<3," in k]   # EPI_SWIGLU, any wave count
     if not copy or not gemm:
         sys.exit("bench.py: the databases hold no copy probe or no gate_up product")
     big = lambda v: max(v)                                   # the probe is the largest copy
@@ -125,7 +125,7 @@ def traffic_from(fetch_db, write_db):
     fetch = float(np.median(f[gemm[0]])) / rf
     write = float(np.median(w[gemm[0]])) / wf
     algo = 2 * (4096 * 4096 + 24576 * 4096 + 4096 * 12288)
-    rec = {"kernel": "k_gemm_bt<3>: gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights",
+    rec = {"kernel": "%s: gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights" % gemm[0].split("(")[0].replace("void ", ""),
            "bytes_per_launch": round(fetch + write), "fetch_bytes": round(fetch), "write_bytes": round(write),
            "algorithmic_bytes": algo, "copy_probe_bytes": PROBE_BYTES,
            "fetch_factor": round(rf, 4), "write_factor": round(wf, 4),
