@@ -63,12 +63,23 @@ struct exn_w {
   int64_t rows = 0, cols = 0;
   int8_t* qs = nullptr;
   uint16_t* d = nullptr;
-  uint16_t* wb = nullptr;  // bf16 rows (EXN_F32 / EXN_BF16 matrices)
+  uint16_t* wb = nullptr;  // bf16 rows (EXN_BF16 matrices; a dense layer matrix)
+  float* wf = nullptr;     // fp32 rows (EXN_F32 matrices)
   uint16_t* wx = nullptr;  // a Q8_0 matrix's resident bf16 expansion, bf16(fp32(d) * q) exactly
   bool wx_ok = false;      // wx matches qs/d
+  bool dense = false;      // a layer matrix that has a BF16 or F32 slot: its products read wb, every slot's rows
   bool pairs = false;      // gate/up rows interleaved by 32
   bool view = false;       // rows inside another allocation (not freed here)
 };
+
+// the bf16 rows the MFMA products stream, if the matrix has them: a BF16 matrix's, a dense layer
+// matrix's, or a Q8_0 matrix's resident expansion; null for Q8_0 without it (dequantised in the
+// product) and for F32 (multiplied in fp32)
+static const uint16_t* wbf(const exn_w* w) {
+  if (w->kind == EXN_BF16 || w->dense) return w->wb;
+  if (w->kind == EXN_Q8_0 && w->wx_ok) return w->wx;
+  return nullptr;
+}
 
 static int dev_alloc(void** p, size_t bytes) {
   *p = nullptr;
@@ -225,6 +236,8 @@ static int w_new(exn_ctx* ctx, int kind, int64_t rows, int64_t cols, exn_w** out
   if (kind == EXN_Q8_0) {
     r = dev_alloc((void**)&w->qs, (size_t)(rows * cols));
     if (r == EXN_OK) r = dev_alloc((void**)&w->d, (size_t)(rows * cols / 32) * 2);
+  } else if (kind == EXN_F32) {
+    r = dev_alloc((void**)&w->wf, (size_t)(rows * cols) * 4);
   } else {
     r = dev_alloc((void**)&w->wb, (size_t)(rows * cols) * 2);
   }
@@ -232,6 +245,7 @@ static int w_new(exn_ctx* ctx, int kind, int64_t rows, int64_t cols, exn_w** out
     dev_free(w->qs);
     dev_free(w->d);
     dev_free(w->wb);
+    dev_free(w->wf);
     delete w;
     return r;
   }
@@ -249,6 +263,7 @@ int exn_weight_free(exn_w* w) {
     dev_free(w->qs);
     dev_free(w->d);
     dev_free(w->wb);
+    dev_free(w->wf);
     dev_free(w->wx);
   }
   delete w;
@@ -297,12 +312,14 @@ int exn_weight_f32(exn_ctx* ctx, const float* data, int64_t rows, int64_t cols, 
   TRY(use(ctx));
   if (!data) FAIL(EXN_EINVAL, "null data");
   TRY(w_new(ctx, EXN_F32, rows, cols, out));
-  int r = upload_bf16_from(ctx, data, true, rows * cols, (*out)->wb);
-  if (r != EXN_OK) {
+  hipError_t e = hipMemcpyAsync((*out)->wf, data, (size_t)(rows * cols) * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
     exn_weight_free(*out);
     *out = nullptr;
+    FAIL(EXN_EHIP, "exn_weight_f32 upload: %s", hipGetErrorString(e));
   }
-  return r;
+  return EXN_OK;
 }
 
 int exn_weight_bf16(exn_ctx* ctx, const uint16_t* data, int64_t rows, int64_t cols, exn_w** out) {
@@ -356,8 +373,9 @@ int exn_dequant(exn_ctx* ctx, const exn_w* w, float* f32, uint16_t* bf16) {
 }
 
 // keep (bf16 = 1) or drop (0) a Q8_0 matrix's bf16 expansion; products use it while it is kept
+// (a dense layer matrix has its bf16 rows already)
 static int w_resident(exn_w* w, bool bf16) {
-  if (w->kind != EXN_Q8_0) return EXN_OK;
+  if (w->kind != EXN_Q8_0 || w->dense) return EXN_OK;
   if (!bf16) {
     if (w->wx) {
       HIPCHK(hipStreamSynchronize(w->ctx->stream));
@@ -449,11 +467,13 @@ static int check_gemm(const exn_w* w, int64_t n) {
   return EXN_OK;
 }
 
+// a bf16-operand product on any matrix but an F32 one (which multiplies in fp32: exn_mm)
 static hipError_t gemm_any(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, Epi epi,
                            const EpiArgs& ea) {
   if (n == 0) return hipSuccess;
-  if (w->kind == EXN_Q8_0 && !w->wx_ok) return gemm_q8(s, x, lda, w->qs, w->d, n, w->rows, w->cols, epi, ea);
-  return gemm_wbf16(s, x, lda, w->kind == EXN_Q8_0 ? w->wx : w->wb, n, w->rows, w->cols, epi, ea);
+  if (const uint16_t* b = wbf(w)) return gemm_wbf16(s, x, lda, b, n, w->rows, w->cols, epi, ea);
+  if (w->kind == EXN_Q8_0) return gemm_q8(s, x, lda, w->qs, w->d, n, w->rows, w->cols, epi, ea);
+  return hipErrorInvalidValue;
 }
 
 // split-K scratch of a block product's prompt rows: S x rows x N floats with S x tiles <= 256
@@ -466,8 +486,8 @@ static const int64_t kSplitCap = (int64_t)256 * 256 * 256;
 // bits however the rows are tiled, so a cached pass's image rows match the uncached pass's.
 static hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, int64_t nh,
                            Epi epi, const EpiArgs& ea, float* part) {
-  if (nh > 0 && nh < n && nh <= 1024 && part && (w->kind != EXN_Q8_0 || w->wx_ok)) {
-    const uint16_t* wb = w->kind == EXN_Q8_0 ? w->wx : w->wb;
+  if (nh > 0 && nh < n && nh <= 1024 && part && wbf(w)) {
+    const uint16_t* wb = wbf(w);
     const hipError_t r = gemm_split_rows(s, x, lda, wb, nh, w->rows, w->cols, epi, ea, part, kSplitCap);
     if (r == hipSuccess) {
       EpiArgs eb = ea;   // the remaining rows: every row pointer nh rows on
@@ -482,24 +502,47 @@ static hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int
   return gemm_any(s, w, x, lda, n, epi, ea);
 }
 
-int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n) {
-  TRY(use(ctx));
+// exn_mm's checks and its products that need no scratch: an F32 matrix in fp32 (d41_mm_f32), n <= 4
+// fp32 rows through the GEMV, bf16 rows through the MFMA product.  *DONE is false when what is left is
+// an fp32-rows MFMA product, whose bf16 copy of X the caller stages.
+static int mm_direct(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n, bool* done) {
+  *done = true;
   TRY(check_gemm(w, n));
   if (!x || !y) FAIL(EXN_EINVAL, "null pointer");
   if (w->pairs) FAIL(EXN_EINVAL, "exn_mm on a paired gate_up matrix: use exn_mm_swiglu");
   if ((xdt != EXN_DT_F32 && xdt != EXN_DT_BF16) || (ydt != EXN_DT_F32 && ydt != EXN_DT_BF16 && ydt != EXN_DT_F16))
     FAIL(EXN_EINVAL, "dtype");
-  if (xdt == EXN_DT_F32 && n <= 4 && ydt == EXN_DT_F32) {
-    HIPCHK(gemv_q8(ctx->stream, (const float*)x, w->cols, w->qs, w->d, w->wb, n, w->rows, w->cols, (float*)y, w->rows, 0));
+  if (w->kind == EXN_F32) {  // fp32 weights are multiplied in fp32, as the reference's d41_mm_f32
+    if (xdt != EXN_DT_F32 || ydt != EXN_DT_F32)
+      FAIL(EXN_EINVAL, "an F32 matrix multiplies fp32 rows into fp32 rows (d41_mm_f32)");
+    if (n <= 4)
+      HIPCHK(gemv_q8(ctx->stream, (const float*)x, w->cols, nullptr, nullptr, nullptr, w->wf, n, w->rows, w->cols,
+                     (float*)y, w->rows, 0));
+    else
+      HIPCHK(gemm_f32(ctx->stream, (const float*)x, w->cols, nullptr, nullptr, nullptr, w->wf, n, w->rows, w->cols,
+                      (float*)y, w->rows, 0));
     return EXN_OK;
   }
-  const uint16_t* xb = (const uint16_t*)x;
-  if (xdt == EXN_DT_F32) {
-    void* t = nullptr;
-    TRY(ctx_tmp(ctx, (size_t)(n * w->cols) * 2, &t));
-    HIPCHK(f32_to_bf16(ctx->stream, (const float*)x, (uint16_t*)t, n * w->cols));
-    xb = (const uint16_t*)t;
+  if (xdt == EXN_DT_F32 && n <= 4 && ydt == EXN_DT_F32) {
+    HIPCHK(gemv_q8(ctx->stream, (const float*)x, w->cols, w->qs, w->d, w->kind == EXN_BF16 ? w->wb : nullptr, nullptr,
+                   n, w->rows, w->cols, (float*)y, w->rows, 0));
+    return EXN_OK;
   }
+  if (xdt == EXN_DT_F32) {
+    *done = false;
+    return EXN_OK;
+  }
+  EpiArgs ea{};
+  ea.y = y;
+  ea.ldy = w->rows;
+  HIPCHK(gemm_any(ctx->stream, w, (const uint16_t*)x, w->cols, n,
+                  ydt == EXN_DT_F32 ? EPI_F32 : (ydt == EXN_DT_F16 ? EPI_F16 : EPI_BF16), ea));
+  return EXN_OK;
+}
+
+// the MFMA product of fp32 rows X through their bf16 copy XB (n x cols, staged by the caller)
+static int mm_staged(exn_ctx* ctx, const exn_w* w, const float* x, uint16_t* xb, void* y, int ydt, int64_t n) {
+  HIPCHK(f32_to_bf16(ctx->stream, x, xb, n * w->cols));
   EpiArgs ea{};
   ea.y = y;
   ea.ldy = w->rows;
@@ -508,12 +551,23 @@ int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int yd
   return EXN_OK;
 }
 
+int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n) {
+  TRY(use(ctx));
+  bool done = false;
+  TRY(mm_direct(ctx, w, x, xdt, y, ydt, n, &done));
+  if (done) return EXN_OK;
+  void* t = nullptr;
+  TRY(ctx_tmp(ctx, (size_t)(n * w->cols) * 2, &t));
+  return mm_staged(ctx, w, (const float*)x, (uint16_t*)t, y, ydt, n);
+}
+
 int exn_mm_gate_add(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, float* resid, int n0, int p,
                     int mstride, const float* gate) {
   TRY(use(ctx));
   TRY(check_gemm(w, n));
   if (!x_bf16 || !resid || !gate) FAIL(EXN_EINVAL, "null pointer");
   if (w->pairs) FAIL(EXN_EINVAL, "a paired gate_up matrix");
+  if (w->kind == EXN_F32) FAIL(EXN_EINVAL, "exn_mm_gate_add: a Q8_0 or BF16 matrix (bf16 products)");
   EpiArgs ea{};
   ea.resid = resid;
   ea.ldy = w->rows;
@@ -530,6 +584,7 @@ int exn_mm_swiglu(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, uint16_t
   TRY(check_gemm(w, n));
   if (!x_bf16 || !ff) FAIL(EXN_EINVAL, "null pointer");
   if (!w->pairs) FAIL(EXN_EINVAL, "exn_mm_swiglu wants a matrix interleaved by exn_weight_pairs");
+  if (w->kind == EXN_F32) FAIL(EXN_EINVAL, "exn_mm_swiglu: a Q8_0 or BF16 matrix (bf16 products)");
   EpiArgs ea{};
   ea.y = ff;
   ea.ldy = w->rows / 2;
@@ -597,7 +652,7 @@ int exn_mm_qkv(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, 
   if (!x_bf16 || !wq || !wk || !cs || !q || !k || !vt) FAIL(EXN_EINVAL, "null pointer");
   if (w->rows != 3 * EXN_W || w->cols != EXN_W || w->pairs)
     FAIL(EXN_EINVAL, "exn_mm_qkv: the fused q | k | v matrix (12288 x 4096) only");
-  if (w->kind == EXN_Q8_0 && !w->wx_ok) FAIL(EXN_EINVAL, "exn_mm_qkv: bf16 weights (exn_weight_resident) only");
+  if (!wbf(w)) FAIL(EXN_EINVAL, "exn_mm_qkv: bf16 weights (BF16, or Q8_0 with exn_weight_resident) only");
   EpiArgs ea{};
   ea.n0 = (int)row0;
   ea.wq = wq;
@@ -609,7 +664,7 @@ int exn_mm_qkv(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, 
   ea.vt = vt;
   ea.lcap = lcap;
   if (row0 < 0 || row0 > INT32_MAX) FAIL(EXN_EINVAL, "row0");
-  const hipError_t r = gemm_qkv(ctx->stream, x_bf16, EXN_W, w->kind == EXN_Q8_0 ? w->wx : w->wb, n, EXN_W, ea);
+  const hipError_t r = gemm_qkv(ctx->stream, x_bf16, EXN_W, wbf(w), n, EXN_W, ea);
   if (r == hipErrorNotSupported)
     FAIL(EXN_EINVAL, "exn_mm_qkv: 16-byte aligned arrays, lcap a multiple of 64, row0 + n <= lcap");
   HIPCHK(r);
@@ -725,7 +780,37 @@ struct exn_dit {
   std::vector<Rec> recs;
   std::vector<hipEvent_t> pool;
   size_t pool_used = 0;
+  // the totals of records already folded (the record list is bounded: see prof_fold)
+  double fold_ms[EXN_PROF_CLASSES] = {}, fold_flops[EXN_PROF_CLASSES] = {}, fold_bytes[EXN_PROF_CLASSES] = {};
+  int64_t fold_n[EXN_PROF_CLASSES] = {};
 };
+
+// at most this many recorded launches hold events at once; past it the records so far are
+// waited for, summed into the per-class totals and their events reused
+static const size_t kProfRecs = 4096;
+
+static void prof_clear(exn_dit* d) {
+  d->recs.clear();
+  d->pool_used = 0;
+  for (int c = 0; c < EXN_PROF_CLASSES; ++c) {
+    d->fold_ms[c] = d->fold_flops[c] = d->fold_bytes[c] = 0;
+    d->fold_n[c] = 0;
+  }
+}
+
+static void prof_fold(exn_dit* d) {
+  if (hipStreamSynchronize(d->ctx->stream) != hipSuccess) return;
+  for (const auto& r : d->recs) {
+    float e = 0.f;
+    if (hipEventElapsedTime(&e, r.a, r.b) != hipSuccess) continue;
+    d->fold_ms[r.cls] += e;
+    d->fold_flops[r.cls] += r.flops;
+    d->fold_bytes[r.cls] += r.bytes;
+    ++d->fold_n[r.cls];
+  }
+  d->recs.clear();
+  d->pool_used = 0;
+}
 
 static hipEvent_t prof_event(exn_dit* d) {
   if (d->pool_used == d->pool.size()) {
@@ -743,8 +828,9 @@ struct ProfScope {
   double flops, bytes;
   hipEvent_t a = nullptr;
   ProfScope(exn_dit* d_, int c, double f, double b) : d(d_), cls(c), flops(f), bytes(b) {
-    if ((d->prof >> cls & 1u) && d->prof_seen[cls]++ % d->prof_every == 0 && (a = prof_event(d)))
-      (void)hipEventRecord(a, d->ctx->stream);
+    if (!(d->prof >> cls & 1u) || d->prof_seen[cls]++ % d->prof_every != 0) return;
+    if (d->recs.size() >= kProfRecs) prof_fold(d);
+    if ((a = prof_event(d))) (void)hipEventRecord(a, d->ctx->stream);
   }
   ~ProfScope() {
     if (!a) return;
@@ -864,8 +950,7 @@ int exn_dit_profile(exn_dit* d, int on) {
   TRY(use(d->ctx));
   if (on) {
     HIPCHK(hipStreamSynchronize(d->ctx->stream));
-    d->recs.clear();
-    d->pool_used = 0;
+    prof_clear(d);
   }
   d->prof = on < 0 ? (1u << EXN_PROF_CLASSES) - 1u : (unsigned)on & ((1u << EXN_PROF_CLASSES) - 1u);
   return EXN_OK;
@@ -882,8 +967,8 @@ int exn_dit_profile_read(exn_dit* d, int cls, double* ms, int64_t* launches, dou
   if (!d || cls < 0 || cls >= EXN_PROF_CLASSES) FAIL(EXN_EINVAL, "profile class %d", cls);
   TRY(use(d->ctx));
   HIPCHK(hipStreamSynchronize(d->ctx->stream));
-  double t = 0, f = 0, b = 0;
-  int64_t c = 0;
+  double t = d->fold_ms[cls], f = d->fold_flops[cls], b = d->fold_bytes[cls];
+  int64_t c = d->fold_n[cls];
   for (const auto& r : d->recs) {
     if (r.cls != cls) continue;
     float e = 0.f;
@@ -920,8 +1005,8 @@ int exn_dit_memory(exn_dit* d, int64_t* weights, int64_t* scratch) {
   int64_t w = 0, s = 0;
   auto wb = [](const exn_w* x) -> int64_t {
     if (!x) return 0;
-    return (x->kind == EXN_Q8_0 ? x->rows * x->cols + x->rows * x->cols / 16 : 2 * x->rows * x->cols) +
-           (x->wx ? 2 * x->rows * x->cols : 0);
+    const int64_t e = x->rows * x->cols;
+    return (x->qs ? e + e / 16 : 0) + (x->wb ? 2 * e : 0) + (x->wf ? 4 * e : 0) + (x->wx ? 2 * e : 0);
   };
   for (auto x : d->edge) w += wb(x);
   for (auto& l : d->L) w += wb(l.qkv) + wb(l.out) + wb(l.gate_up) + wb(l.down) + 2 * 4 * EXN_HD;
@@ -975,9 +1060,49 @@ static int set_vector(exn_dit* d, float** dst, int kind, const void* data, int64
   return EXN_OK;
 }
 
+// a layer matrix given a BF16 or F32 slot: from then on its products read wb, which holds every
+// slot's rows in bf16 -- the Q8_0 slots' dequantised exactly and rounded, bf16(fp32(d) * q), as the
+// resident expansion holds them
+static int make_dense(exn_w* w) {
+  if (w->dense) return EXN_OK;
+  TRY(dev_alloc((void**)&w->wb, (size_t)(w->rows * w->cols) * 2));
+  HIPCHK(dequant_q8(w->ctx->stream, w->qs, w->d, w->rows * w->cols, nullptr, w->wb));
+  HIPCHK(hipStreamSynchronize(w->ctx->stream));
+  dev_free(w->wx);
+  w->wx = nullptr;
+  w->wx_ok = false;
+  w->dense = true;
+  return EXN_OK;
+}
+
+// ROWS rows of fp32 (KIND EXN_F32, rounded to bf16, RNE) or bf16 host data into a dense layer
+// matrix's wb from row ROW0, or (PAIRED: the gate_up matrix) to the rows of the 32-row interleave
+static int set_dense_rows(exn_ctx* ctx, exn_w* w, int64_t row0, bool paired, int kind, const void* data,
+                          int64_t rows) {
+  const int64_t cols = w->cols, count = rows * cols;
+  if (!paired) return upload_bf16_from(ctx, data, kind == EXN_F32, count, w->wb + row0 * cols);
+  void* t = nullptr;
+  TRY(ctx_tmp(ctx, (size_t)count * (kind == EXN_F32 ? 6 : 2), &t));
+  uint16_t* tb = (uint16_t*)t;
+  if (kind == EXN_F32) {
+    float* tf = (float*)(tb + count);
+    HIPCHK(hipMemcpyAsync(tf, data, (size_t)count * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(f32_to_bf16(ctx->stream, tf, tb, count));
+  } else {
+    HIPCHK(hipMemcpyAsync(tb, data, (size_t)count * 2, hipMemcpyHostToDevice, ctx->stream));
+  }
+  const std::vector<int32_t> map = pair_rows(rows);
+  for (int64_t rr = 0; rr < rows; rr += 32)
+    HIPCHK(hipMemcpyAsync(w->wb + (row0 + map[(size_t)rr]) * cols, tb + rr * cols, (size_t)(32 * cols) * 2,
+                          hipMemcpyDeviceToDevice, ctx->stream));
+  HIPCHK(hipStreamSynchronize(ctx->stream));
+  return EXN_OK;
+}
+
 int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_t d0, int64_t d1) {
   if (!d || !name || !data) FAIL(EXN_EINVAL, "null argument");
   TRY(use(d->ctx));
+  d->kept = false;   // K/V kept from other weights are not this model's
   int edge, layer, slot;
   if (!lookup(d, name, &edge, &layer, &slot)) FAIL(EXN_EINVAL, "%s: not a tensor of the DiT", name);
   const Expect ex = edge >= 0 ? edge_expect(edge) : slot_expect(layer, slot);
@@ -1008,13 +1133,24 @@ int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_
     d->have_edge[edge] = true;
     return EXN_OK;
   }
-  if (kind != EXN_Q8_0) FAIL(EXN_EINVAL, "%s: block matrices must be Q8_0 (the real DiT's are)", name);
   exn_w* w = nullptr;
   int64_t row0 = 0;
   const int32_t* map = nullptr;
   TRY(layer_target(d, layer, slot, &w, &row0, &map));
-  TRY(upload_q8_blocks(ctx, data, rows, cols, map, w->qs + row0 * cols, w->d + row0 * (cols / 32)));
-  w->wx_ok = false;
+  if (kind == EXN_Q8_0) {
+    TRY(upload_q8_blocks(ctx, data, rows, cols, map, w->qs + row0 * cols, w->d + row0 * (cols / 32)));
+    w->wx_ok = false;
+    if (w->dense) {  // the slot's rows into the dense rows too (gate_up's slot is the whole matrix)
+      HIPCHK(dequant_q8(ctx->stream, w->qs + row0 * cols, w->d + row0 * (cols / 32), rows * cols, nullptr,
+                        w->wb + row0 * cols));
+      HIPCHK(hipStreamSynchronize(ctx->stream));
+    }
+  } else {
+    // upload-dit takes BF16 and F32 matrices too (src/cuda-dit.lisp:77-80); the block products take
+    // bf16 operands, so F32 rows are rounded to bf16 here
+    TRY(make_dense(w));
+    TRY(set_dense_rows(ctx, w, row0, map != nullptr, kind, data, rows));
+  }
   d->L[(size_t)layer].have |= (uint8_t)(1u << slot);
   return EXN_OK;
 }
@@ -1022,6 +1158,7 @@ int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_
 int exn_dit_synth(exn_dit* d, uint64_t seed) {
   if (!d) FAIL(EXN_EINVAL, "null model");
   TRY(use(d->ctx));
+  d->kept = false;
   hipStream_t s = d->ctx->stream;
   for (int i = 0; i < 9; ++i) {
     const Expect ex = edge_expect(i);
@@ -1055,6 +1192,12 @@ int exn_dit_synth(exn_dit* d, uint64_t seed) {
         TRY(layer_target(d, layer, sl, &w, &row0, &map));
         HIPCHK(synth_q8(s, key, ex.d1, ex.d0, ex.d0 / 32, map, w->qs + row0 * ex.d0, w->d + row0 * (ex.d0 / 32)));
         w->wx_ok = false;
+        if (w->dense) {  // every slot of the matrix is made Q8_0 again here
+          HIPCHK(hipStreamSynchronize(s));
+          dev_free(w->wb);
+          w->wb = nullptr;
+          w->dense = false;
+        }
       }
       L.have |= (uint8_t)(1u << sl);
     }
@@ -1066,6 +1209,7 @@ int exn_dit_synth(exn_dit* d, uint64_t seed) {
 int exn_dit_resident(exn_dit* d, int bf16) {
   if (!d) FAIL(EXN_EINVAL, "null model");
   TRY(use(d->ctx));
+  if (d->bf16 != (bf16 != 0)) d->kept = false;   // the other product path: K/V recomputed
   d->bf16 = bf16 != 0;
   for (auto& l : d->L)
     for (exn_w* w : {l.qkv, l.out, l.gate_up, l.down})
@@ -1258,7 +1402,8 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   // an edge product in fp32: Y (m rows, ldy apart) = X (m rows of the matrix's inputs) W^T
   auto edge_mm = [&](int e, const float* xin, int64_t m, float* yout, int gelu) {
     const exn_w* W = d->edge[e];
-    return gemm_f32(s, xin, W->cols, W->qs, W->d, W->wb, m, W->rows, W->cols, yout, W->rows, gelu, epart, epart_cap);
+    return gemm_f32(s, xin, W->cols, W->qs, W->d, W->wb, W->wf, m, W->rows, W->cols, yout, W->rows, gelu, epart,
+                    epart_cap);
   };
   {
   ProfScope prologue(d, EXN_PROF_EDGE, 0, 0);
@@ -1267,7 +1412,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   HIPCHK(hipGetLastError());
   auto gv = [&](int e, const float* xin, int64_t m, float* yout, int act) {
     const exn_w* W = d->edge[e];
-    return gemv_q8(s, xin, W->cols, W->qs, W->d, W->wb, m, W->rows, W->cols, yout, W->rows, act);
+    return gemv_q8(s, xin, W->cols, W->qs, W->d, W->wb, W->wf, m, W->rows, W->cols, yout, W->rows, act);
   };
   HIPCHK(gv(4, emb, 2, e1, 1));
   HIPCHK(gv(5, e1, 2, e2, 1));
@@ -1319,7 +1464,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
     // else the product to fp16 rows and qkv_prep over them.  (Splitting an uncached pass's
     // prompt rows off, as the other products do, measured no faster here: 768 + 48 tiles.)
     bool fused = false;
-    if (L.qkv->kind != EXN_Q8_0 || L.qkv->wx_ok) {
+    if (wbf(L.qkv)) {
       ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
       ea = EpiArgs{};
       ea.n0 = n0;
@@ -1332,7 +1477,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ea.kc = d->kc[(size_t)il];
       ea.vt = d->vt[(size_t)il];
       ea.lcap = d->lcap;
-      const hipError_t r = gemm_qkv(s, y, EXN_W, L.qkv->kind == EXN_Q8_0 ? L.qkv->wx : L.qkv->wb, n, EXN_W, ea);
+      const hipError_t r = gemm_qkv(s, y, EXN_W, wbf(L.qkv), n, EXN_W, ea);
       if (r != hipErrorNotSupported) HIPCHK(r);
       fused = r == hipSuccess;
     }
@@ -1451,6 +1596,25 @@ int exn_dit_generate_dev(exn_dit* d, const float* context, int p, float* z, int 
   for (int i = 0; i + 1 < nsig; ++i) {
     TRY(velocity(d, context, p, z, h, w, sigmas[i], key, ref_a, ref_latent, rh, rw, v));
     HIPCHK(euler(d->ctx->stream, count, z, v, (float)(sigmas[i + 1] - sigmas[i])));
+  }
+  return EXN_OK;
+}
+
+int exn_dit_rope_table(int p, int h, int w, int edit, int ref_a, int rh, int rw, int64_t rows_cap, int32_t* pos,
+                       float* cs) {
+  if (p < 0 || h <= 0 || w <= 0 || (edit && (rh <= 0 || rw <= 0 || ref_a < 0 || ref_a > p)))
+    FAIL(EXN_EINVAL, "rope table: p %d, %d x %d, edit %d (a %d, %d x %d)", p, h, w, edit, ref_a, rh, rw);
+  const int nref = edit ? rh * rw : 0;
+  const int64_t rows = (int64_t)p + nref + (int64_t)h * w;
+  if (rows > rows_cap) FAIL(EXN_EINVAL, "rope table: %lld rows, room for %lld", (long long)rows, (long long)rows_cap);
+  std::vector<int> pv;
+  positions(p + nref, h, w, edit ? ref_a : 0, rh, rw, edit != 0, pv);
+  if (pos)
+    for (size_t i = 0; i < pv.size(); ++i) pos[i] = pv[i];
+  if (cs) {
+    std::vector<float> c;
+    rope_table(pv, c);
+    memcpy(cs, c.data(), c.size() * 4);
   }
   return EXN_OK;
 }

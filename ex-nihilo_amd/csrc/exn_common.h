@@ -188,15 +188,17 @@ hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const 
 // hipErrorNotSupported when the shapes or alignments do not fit the fused path
 hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t K,
                     const EpiArgs& ea);
-// the edge products: Y = X W^T all fp32 on the SIMD lanes (K % 32 == 0); optional GELU-tanh on Y
+// the edge products: Y = X W^T all fp32 on the SIMD lanes (K % 32 == 0); optional GELU-tanh on Y.
+// W is read from wf32 (fp32 rows) when given, else wbf16 (bf16 rows), else qs/d (Q8_0).
 // ... with K split when the product has few tiles over a long K and PART (S x M x N floats, at
 // most PART_CAP) is given
 hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
-                    const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int gelu,
-                    float* part = nullptr, int64_t part_cap = 0);
-// small M (<= 4): Y = X W^T, X fp32, fp32 sums; optional SiLU on the output
+                    const uint16_t* wbf16, const float* wf32, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy,
+                    int gelu, float* part = nullptr, int64_t part_cap = 0);
+// small M (<= 4): Y = X W^T, X fp32, fp32 sums; optional SiLU on the output; W as gemm_f32 reads it
 hipError_t gemv_q8(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
-                   const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int silu);
+                   const uint16_t* wbf16, const float* wf32, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy,
+                   int silu);
 
 hipError_t synth_q8(hipStream_t s, uint64_t key, int64_t rows, int64_t cols, int64_t row_stride_blocks,
                     const int32_t* row_map, int8_t* qs, uint16_t* d);

@@ -773,13 +773,14 @@ hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint1
 
 // --- the edge products in fp32 -------------------------------------------------------
 // img_in, txt_in and proj_out feed the residual stream and the velocity straight,
-// and are 0.01% of a step's FLOPs: they run in fp32 on the SIMD lanes, the Q8_0
-// weights dequantised exactly.  64 x 64 tiles, K 32 (a Q8_0 block) a step, each
-// thread 4 x 4 outputs at a 16-row and 16-column stride.
+// and are 0.01% of a step's FLOPs: they run in fp32 on the SIMD lanes, the weights
+// as they are stored -- fp32 rows (the reference's d41_mm_f32, src/cuda-dit.lisp:
+// 127-130), bf16 rows, or Q8_0 dequantised exactly.  64 x 64 tiles, K 32 (a Q8_0
+// block) a step, each thread 4 x 4 outputs at a 16-row and 16-column stride.
 __global__ void __launch_bounds__(256)
 k_gemm_f32(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ QS, const uint16_t* __restrict__ D,
-           const uint16_t* __restrict__ WB, int64_t M, int64_t N, int64_t K, float* __restrict__ Y, int64_t ldy,
-           int gelu) {
+           const uint16_t* __restrict__ WB, const float* __restrict__ WF, int64_t M, int64_t N, int64_t K,
+           float* __restrict__ Y, int64_t ldy, int gelu) {
   __shared__ float xs[32][64 + 1];
   __shared__ float ws[32][64 + 1];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -801,7 +802,15 @@ k_gemm_f32(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ 
         xs[lk + 4 + e][lr] = b[e];
       }
       const int64_t n = min(n0 + lr, N - 1);
-      if (WB) {
+      if (WF) {
+        const f32x4* w = (const f32x4*)(WF + n * K + k0 + lk);
+        const f32x4 w0 = w[0], w1 = w[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ws[lk + e][lr] = w0[e];
+          ws[lk + 4 + e][lr] = w1[e];
+        }
+      } else if (WB) {
         const u32x4 w = *(const u32x4*)(WB + n * K + k0 + lk);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -855,8 +864,8 @@ k_f32_part_sum(int S, int64_t M, int64_t N, const float* __restrict__ part, floa
 }
 
 hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
-                    const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int gelu,
-                    float* part, int64_t part_cap) {
+                    const uint16_t* wbf16, const float* wf32, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy,
+                    int gelu, float* part, int64_t part_cap) {
   if (K % 32 || M <= 0) return M == 0 ? hipSuccess : hipErrorInvalidValue;
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
   // few tiles over a long K (proj_out: 64 tiles of 64 x 64 over 4096): K split over up to 8
@@ -867,12 +876,12 @@ hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs
   if (S > K / 256) S = K / 256;
   if (S >= 2 && part && S * M * N <= part_cap) {
     grid.z = (unsigned)S;
-    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, M, N, K, part, N, gelu);
+    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, wf32, M, N, K, part, N, gelu);
     hipLaunchKernelGGL(k_f32_part_sum, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, s, (int)S, M, N, part, y,
                        ldy, gelu);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, M, N, K, y, ldy, gelu);
+  hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, wf32, M, N, K, y, ldy, gelu);
   return hipGetLastError();
 }
 
@@ -880,7 +889,8 @@ hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs
 
 __global__ void __launch_bounds__(256)
 k_gemv(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ QS, const uint16_t* __restrict__ D,
-       const uint16_t* __restrict__ WB, int M, int64_t N, int64_t K, float* __restrict__ Y, int64_t ldy, int silu) {
+       const uint16_t* __restrict__ WB, const float* __restrict__ WF, int M, int64_t N, int64_t K,
+       float* __restrict__ Y, int64_t ldy, int silu) {
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -888,7 +898,15 @@ k_gemv(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ QS, 
   for (int64_t c = lane; c < K / 16; c += 64) {
     const int64_t k = 16 * c;
     float w[16];
-    if (WB) {
+    if (WF) {
+      const f32x4* src = (const f32x4*)(WF + n * K + k);
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const f32x4 v = src[e4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * e4 + e] = v[e];
+      }
+    } else if (WB) {
       const u32x4* src = (const u32x4*)(WB + n * K + k);
       const u32x4 a = src[0], b = src[1];
 #pragma unroll
@@ -927,10 +945,11 @@ k_gemv(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ QS, 
 }
 
 hipError_t gemv_q8(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs, const uint16_t* d,
-                   const uint16_t* wbf16, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy, int silu) {
+                   const uint16_t* wbf16, const float* wf32, int64_t M, int64_t N, int64_t K, float* y, int64_t ldy,
+                   int silu) {
   if (M > 4 || K % 16) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gemv, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s, x, ldx, qs, d, wbf16, (int)M, N, K, y, ldy,
-                     silu);
+  hipLaunchKernelGGL(k_gemv, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, s, x, ldx, qs, d, wbf16, wf32, (int)M, N, K,
+                     y, ldy, silu);
   return hipGetLastError();
 }
 

@@ -92,6 +92,7 @@ SIGNATURES = {
     "exn_dit_profile_every": (c_int, [vp, c_int]),
     "exn_dit_profile_read": (c_int, [vp, c_int, POINTER(c_double), POINTER(c_int64), POINTER(c_double),
                                      POINTER(c_double)]),
+    "exn_dit_rope_table": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64, vp, vp]),
     "exn_dit_release": (c_int, [vp]),
     "exn_dit_destroy": (c_int, [vp]),
     "exn_dit_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
@@ -232,6 +233,14 @@ class Weight:
         return cls(ctx, h, m.shape[0], m.shape[1])
 
     @classmethod
+    def bf16(cls, ctx, bits: np.ndarray):
+        """A BF16 matrix from its bit patterns (uint16, rows x cols)."""
+        b = np.ascontiguousarray(bits, dtype=np.uint16)
+        h = vp()
+        call("exn_weight_bf16", ctx.h, ptr(b), b.shape[0], b.shape[1], ctypes.byref(h))
+        return cls(ctx, h, b.shape[0], b.shape[1])
+
+    @classmethod
     def synth(cls, ctx, seed: int, tensor: int, rows: int, cols: int):
         h = vp()
         call("exn_weight_q8_0_synth", ctx.h, seed, tensor, rows, cols, ctypes.byref(h))
@@ -368,15 +377,46 @@ def dit_velocity(d: Dit, context: np.ndarray, p: int, latent: np.ndarray, h: int
     return v
 
 
+def rope_table(p: int, h: int, w: int, ref=None):
+    """The library's host-side dit-positions and rope-table (src/host.lisp:19-50), the
+    tables a step uploads: P text rows, an H x W image, REF = (a, rh, rw) for an edit's
+    reference picture.  Returns (positions: rows x 3 int32, cs: rows x 128 float32,
+    the cos and sin of each of the 64 pairs interleaved)."""
+    edit = ref is not None
+    a, rh, rw = ref if edit else (0, 0, 0)
+    rows = p + (rh * rw if edit else 0) + h * w
+    pos = np.empty((rows, 3), np.int32)
+    cs = np.empty((rows, 128), np.float32)
+    call("exn_dit_rope_table", p, h, w, 1 if edit else 0, a, rh, rw, rows, ptr(pos), ptr(cs))
+    return pos, cs
+
+
 def dit_release(d: Dit):
     """dit-release (src/cuda-dit.lisp:99-108)."""
     d.release()
 
 
+def prompt_key(context: np.ndarray, p: int, ref=None):
+    """A prefix key that names the prompt by its content, as generate's key is the prompt
+    itself (src/generate.lisp:134): the context rows and, for an edit, the reference
+    picture and where it sits.  Two prompts share kept K/V only if these are equal."""
+    import hashlib
+    hsh = hashlib.sha256(np.ascontiguousarray(context, dtype=np.float32).tobytes())
+    if ref is not None:
+        a, rl, rh, rw = ref
+        hsh.update(np.array([a, rh, rw], np.int64).tobytes())
+        hsh.update(np.ascontiguousarray(rl, dtype=np.float32).tobytes())
+    return ("prompt", p, hsh.hexdigest())
+
+
 def generate_latent(d: Dit, context: np.ndarray, p: int, z: np.ndarray, h: int, w: int,
-                    sigmas=TURBO_SIGMAS, prefix_key="prompt", ref=None) -> np.ndarray:
+                    sigmas=TURBO_SIGMAS, prefix_key=None, ref=None) -> np.ndarray:
     """generate's Euler loop (src/generate.lisp:133-135) on host arrays:
-    z <- z + (s' - s) v, (s' - s) rounded to a single float."""
+    z <- z + (s' - s) v, (s' - s) rounded to a single float.  The prompt's K/V are
+    kept from the first step under PREFIX_KEY, by default a key made from the
+    context (and reference picture) itself (prompt_key)."""
+    if prefix_key is None:
+        prefix_key = prompt_key(context, p, ref)
     z = np.array(z, dtype=np.float32, copy=True)
     for s, s2 in zip(sigmas[:-1], sigmas[1:]):
         v = dit_velocity(d, context, p, z, h, w, s, prefix_key=prefix_key, ref=ref)

@@ -79,7 +79,8 @@ int exn_copy(exn_ctx* ctx, void* dst, const void* src, size_t bytes);
  * fp16 d, 32 int8 q), e.g. the mmapped file itself; repacked on the device as
  * repack_q8 does (src/cuda-dit.lisp:71-76).  COLS % 32 == 0. */
 int exn_weight_q8_0(exn_ctx* ctx, const void* blocks, int64_t rows, int64_t cols, exn_w** out);
-/* a non-Q8_0 matrix (src/cuda-dit.lisp:77-80): fp32 or bf16 rows, kept as bf16 */
+/* a non-Q8_0 matrix (src/cuda-dit.lisp:77-80), kept as given: fp32 rows, multiplied in fp32
+ * (d41_mm_f32, :127-130), or bf16 rows, multiplied on the bf16 MFMA (g53_mm_bf16) */
 int exn_weight_f32(exn_ctx* ctx, const float* data, int64_t rows, int64_t cols, exn_w** out);
 int exn_weight_bf16(exn_ctx* ctx, const uint16_t* data, int64_t rows, int64_t cols, exn_w** out);
 /* test hook, no reference counterpart: a synthetic Q8_0 matrix made on the device by the
@@ -98,7 +99,9 @@ int exn_weight_resident(exn_ctx* ctx, exn_w* w, int bf16);
 /* --- ops: the kernels of src/cuda/dit.cu and illatio's products, on device pointers ------------------ */
 
 /* mm (src/cuda-dit.lisp:115-130): Y (n rows) = X (n rows) W^T.  X is fp32 or bf16
- * (XDT), Y fp32, bf16 or fp16 (YDT); n <= 4 with fp32 X and Y goes through a GEMV in fp32. */
+ * (XDT), Y fp32, bf16 or fp16 (YDT); n <= 4 with fp32 X and Y goes through a GEMV in fp32.
+ * An F32 matrix takes fp32 X and Y and multiplies in fp32 (d41_mm_f32); Q8_0 and BF16
+ * matrices take bf16 operands (fp32 X rounded to bf16 in a buffer the context grows). */
 int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n);
 /* mm, then x_gate_add fused into the product's store (src/cuda/dit.cu:34-41):
  * RESID[t] += tanh(GATE[row]) * (X W^T)[t]; sequence row N0 + t < P takes GATE + MSTRIDE */
@@ -156,7 +159,11 @@ int exn_dit_create(exn_ctx* ctx, int layers, exn_dit** out);
 /* one tensor of upload-dit (src/cuda-dit.lisp:59-81), by its name without the
  * "model.diffusion_model." prefix and its ggml dims D0 (contiguous) x D1 (1 for a vector);
  * KIND EXN_Q8_0 (block_q8_0 records), EXN_F32 or EXN_BF16.  Dims and names are held
- * against dit-expected (src/weights.lisp:22-45); txt_in.text_norm.weight is used as 1 + w. */
+ * against dit-expected (src/weights.lisp:22-45); txt_in.text_norm.weight is used as 1 + w.
+ * Edge matrices are kept as given (F32 multiplied in fp32).  A block matrix given as F32 or
+ * BF16 is kept as bf16 rows (F32 rounded to nearest even), the operands its products take;
+ * its layer matrix (q | k | v, or gate_up) then runs from bf16 rows, its Q8_0 slots
+ * dequantised into them exactly.  Setting or synthesising a tensor drops the kept prompt K/V. */
 int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_t d0, int64_t d1);
 /* test hook: every tensor of the model made on the device by the synthetic generator */
 int exn_dit_synth(exn_dit* d, uint64_t seed);
@@ -166,7 +173,7 @@ int exn_dit_check(exn_dit* d);
 /* no reference counterpart: BF16 = 1 (the default) runs the block matrices from resident
  * bf16 expansions (exn_weight_resident; 14 GB for the 7B model), made here for the matrices
  * present and at the next step for any set later; 0 drops them and runs from Q8_0 with the
- * dequantisation inside the product */
+ * dequantisation inside the product.  A change drops the kept prompt K/V. */
 int exn_dit_resident(exn_dit* d, int bf16);
 /* dit-velocity (src/cuda-dit.lisp:137-243): CONTEXT (P x 4096 fp32, the encoder's states),
  * LATENT (64 x H x W fp32, channel-major) -> V (64 x H x W), host memory, synchronous.
@@ -208,6 +215,13 @@ int exn_dit_profile(exn_dit* d, int on);
  * launches' mean duration at a fraction of the events' cost; restarts the count */
 int exn_dit_profile_every(exn_dit* d, int every);
 int exn_dit_profile_read(exn_dit* d, int cls, double* ms, int64_t* launches, double* flops, double* bytes);
+/* test hook: dit-positions and rope-table (src/host.lisp:19-50) as the step computes them, on
+ * the host (no GPU needed): for P text rows, an H x W image and, when EDIT, a RH x RW reference
+ * picture after the first REF_A text rows, each sequence row's (frame, row, col) into POS
+ * (3 ints a row) and the cos, sin of its 64 angles into CS (128 floats a row, pairs
+ * interleaved); either may be NULL.  Rows = P + (EDIT ? RH RW : 0) + H W, at most ROWS_CAP. */
+int exn_dit_rope_table(int p, int h, int w, int edit, int ref_a, int rh, int rw, int64_t rows_cap, int32_t* pos,
+                       float* cs);
 /* dit-release (src/cuda-dit.lisp:99-108): scratch and kept prompt K/V freed, weights kept */
 int exn_dit_release(exn_dit* d);
 int exn_dit_destroy(exn_dit* d);

@@ -6,6 +6,8 @@ itself pinned against the reference's ref_dit.py vectors), cached:
     python tests/golden/make_dit_vectors.py small      # dit_depth32_small.npz
     python tests/golden/make_dit_vectors.py cfg2       # dit_cfg2_8step.npz (about 1.5 hours)
     python tests/golden/make_dit_vectors.py full2      # dit_full_shapes_2blocks.npz (a few minutes)
+    python tests/golden/make_dit_vectors.py cfg3       # dit_cfg3_8step.npz (hours)
+    python tests/golden/make_dit_vectors.py cfg4       # dit_cfg4_edit_8step.npz (hours)
 
 small: 32 blocks of the real shape, synthetic Q8_0 weights (seed 1), 32 text
 rows, an 8 x 8 latent: the velocity of each of the 8 Turbo steps (the first
@@ -13,6 +15,11 @@ uncached, the rest on the kept prompt K/V) and the final latent.
 cfg2: the 1024^2 workload -- 4096 image rows, 256 text rows, 32 blocks (seed
 2) -- through the 8 Euler steps: the first step's velocity and the final
 latent, stored as float16 (far below the 2e-2 tolerance).
+cfg3: the 1536 x 1024 workload -- 6144 image rows (96 x 64), 256 text rows,
+32 blocks (seed 6) -- the same 8 steps and fields as cfg2.
+cfg4: the edit workload -- a 64 x 64 image after 512 text rows with a 64 x 64
+reference picture after the first 8 of them (8704 keys), 32 blocks (seed 7) --
+the same 8 steps (the prefix, text and reference picture, kept after the first).
 """
 import os
 import sys
@@ -25,10 +32,16 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 from oracle import exn_oracle as xo  # noqa: E402
 
 
-def run(seed, p, h, w, out, half=False):
+def run(seed, p, h, w, out, half=False, ref=None):
     sh = xo.Shape()
     wt = xo.SynthWeights(seed, sh, cache_bytes=0, keep_q8=True)
-    ctx, lat = xo.synth_inputs(seed, p, h, w, sh)
+    if ref is None:
+        ctx, lat = xo.synth_inputs(seed, p, h, w, sh)
+        oref = None
+    else:
+        a, rh, rw = ref
+        ctx, lat, rl = xo.synth_inputs(seed, p, h, w, sh, ref_hw=(rh, rw))
+        oref = (a, rl)
     vs = []
     t0 = time.time()
 
@@ -36,9 +49,11 @@ def run(seed, p, h, w, out, half=False):
         vs.append(v)
         print("step sigma %.6f: |v| %.4f, %.0fs" % (s, float(np.sqrt((v * v).mean())), time.time() - t0), flush=True)
 
-    z = xo.euler(wt, ctx, lat, sh, on_step=on_step)
+    z = xo.euler(wt, ctx, lat, sh, ref=oref, on_step=on_step)
     dt = np.float16 if half else np.float32
     arrays = {"meta": np.array([seed, p, h, w], np.int64), "z_final": z.astype(dt)}
+    if ref is not None:
+        arrays["ref"] = np.array(ref, np.int64)
     if half:
         arrays["v_step0"] = vs[0].astype(dt)
     else:
@@ -81,3 +96,7 @@ if __name__ == "__main__":
         run(2, 256, 64, 64, "dit_cfg2_8step.npz", half=True)
     elif which == "full2":
         full_shapes("dit_full_shapes_2blocks.npz")
+    elif which == "cfg3":
+        run(6, 256, 96, 64, "dit_cfg3_8step.npz", half=True)
+    elif which == "cfg4":
+        run(7, 512, 64, 64, "dit_cfg4_edit_8step.npz", half=True, ref=(8, 64, 64))

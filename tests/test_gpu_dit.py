@@ -113,6 +113,120 @@ def test_prefix_cache(ctx):
     d.destroy()
 
 
+def test_prefix_cache_follows_the_weights_and_the_prompt(ctx):
+    """Kept K/V belong to the weights and the prompt they were made from: re-synthesised
+    weights under the same key and length recompute them, and generate_latent's default
+    key is the prompt's content, so two prompts of one length each get their own."""
+    say("prefix cache vs new weights and new prompts, 2 blocks")
+    d = model(ctx, 2, 3)
+    ctxa, lat = xo.synth_inputs(3, 20, 4, 6)
+    X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9, prefix_key="a")                # keeps seed 3's K/V
+    d.synth(31)
+    v1 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9, prefix_key="a")
+    v0 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9)
+    assert xo.rel_l2(v1, v0) < 1e-6
+    # the same through exn_dit_set: one layer's to_out scaled
+    name = "transformer_blocks.1.attn.to_out.0.weight"
+    qs, dd = xo.q8_0_synth(31, xo.tensor_id(name), 4096, 4096)
+    X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9, prefix_key="b")
+    d.set(name, X.Q8_0, xo.q8_0_to_blocks(qs, (dd.astype(np.float32) * 2).astype(np.float16)), (4096, 4096))
+    v2 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9, prefix_key="b")
+    v3 = X.dit_velocity(d, ctxa, 20, lat, 4, 6, 0.9)
+    assert xo.rel_l2(v2, v3) < 1e-6 and xo.rel_l2(v3, v0) > 1e-4
+    # two prompts of one length through generate_latent: each as its own uncached run
+    ctxb = xo.synth_inputs(35, 20, 4, 6)[0]
+    sig = (1.0, 0.95418, 0.5)
+    za = X.generate_latent(d, ctxa, 20, lat, 4, 6, sigmas=sig)
+    zb = X.generate_latent(d, ctxb, 20, lat, 4, 6, sigmas=sig)
+    for c, z in ((ctxa, za), (ctxb, zb)):
+        want = lat.copy()
+        for s0, s1 in zip(sig[:-1], sig[1:]):
+            want = want + np.float32(s1 - s0) * X.dit_velocity(d, c, 20, want, 4, 6, s0)
+        assert xo.rel_l2(z, want) < 1e-5
+    assert xo.rel_l2(za, zb) > 1e-4
+    d.destroy()
+
+
+class _Weights:
+    """The oracle's synthetic weights with some matrices replaced."""
+
+    def __init__(self, base, over):
+        self.base, self.over = base, over
+
+    def __call__(self, name):
+        return self.over[name] if name in self.over else self.base(name)
+
+
+# matrices the real GGUF stores as F32 or BF16 (src/metal-dit.lisp:4-7), and the other edge ones
+EDGE_MATS = ["img_in.weight", "txt_in.in_layer.weight", "txt_in.out_layer.weight", "norm_out.linear.weight",
+             "proj_out.weight", "time_text_embed.timestep_embedder.linear_1.weight",
+             "time_text_embed.timestep_embedder.linear_2.weight", "modulation.1.weight"]
+
+
+def test_matrices_of_every_kind(ctx):
+    """upload-dit takes F32 and BF16 matrices besides Q8_0 (src/cuda-dit.lisp:77-80,127-130).
+    Edge matrices stay as given: F32 multiplied in fp32 (d41_mm_f32) -- the dequantised values
+    as F32 give the Q8_0 run's velocity bit for bit, and values off the bf16 grid reach the
+    block input at fp32 precision; BF16 on their bf16 values.  Block matrices given as F32 or
+    BF16 (or mixed with Q8_0 slots in one fused matrix) run from bf16 rows: the dequantised
+    values give the resident run's velocity bit for bit."""
+    seed, p, h, w = 13, 16, 8, 8
+    say("F32 / BF16 / Q8_0 matrices through exn_dit_set, 2 blocks")
+    d = model(ctx, 2, seed)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    wt = xo.SynthWeights(seed)
+    dims = dict(xo.dit_expected(xo.Shape(layers=2)))
+    v_q8 = X.dit_velocity(d, ctxa, p, lat, h, w, 0.6)
+    # (a) the edge matrices as F32, exactly the dequantised values
+    for name in EDGE_MATS:
+        d.set(name, X.F32, wt(name), dims[name])
+    v_f32 = X.dit_velocity(d, ctxa, p, lat, h, w, 0.6)
+    assert np.array_equal(v_f32, v_q8)
+    # (b) F32 and BF16 edge matrices off the bf16 grid, against the oracle on those weights
+    rng = np.random.default_rng(5)
+    over = {n: (wt(n) * (1 + 1e-2 * rng.normal(size=wt(n).shape))).astype(np.float32) for n in EDGE_MATS}
+    for kind in (X.F32, X.BF16):
+        o = dict(over) if kind == X.F32 else {n: xo.bf16_round(m) for n, m in over.items()}
+        for name in EDGE_MATS:
+            d.set(name, kind, o[name] if kind == X.F32 else xo.bf16_bits(o[name]), dims[name])
+        tr = _trace(ctx, d, p + h * w)
+        v = X.dit_velocity(d, ctxa, p, lat, h, w, 0.6)
+        X.call("exn_dit_trace", d.h, None, 0)
+        dump = {}
+        want = xo.forward(_Weights(wt, o), ctxa, lat, 0.6, dump=dump, layers=2)
+        x_in = np.concatenate([dump["txt"], xo.linear(xo.tokens(lat), o["img_in.weight"])])
+        e_in, e_v = xo.rel_l2(tr.get()[0], x_in), xo.rel_l2(v, want)
+        say("edge %s: block input rel-L2 %.2e, velocity %.2e" % ("F32" if kind == X.F32 else "BF16", e_in, e_v))
+        assert e_in < 1e-5 and e_v < 1e-2
+    # (c) back to Q8_0 edges; block matrices as F32, BF16 and Q8_0 slots of one fused matrix
+    d.synth(seed)
+    v_res = X.dit_velocity(d, ctxa, p, lat, h, w, 0.6)
+    assert np.array_equal(v_res, v_q8)
+    X.dit_velocity(d, ctxa, p, lat, h, w, 0.6, prefix_key="k")
+    blk = "transformer_blocks.%d."
+    d.set(blk % 0 + "attn.to_q.weight", X.F32, wt(blk % 0 + "attn.to_q.weight"), (4096, 4096))
+    d.set(blk % 0 + "attn.to_v.weight", X.BF16, xo.bf16_bits(wt(blk % 0 + "attn.to_v.weight")), (4096, 4096))
+    n = blk % 0 + "attn.to_k.weight"
+    d.set(n, X.Q8_0, xo.q8_0_to_blocks(*xo.q8_0_synth(seed, xo.tensor_id(n), 4096, 4096)), (4096, 4096))
+    d.set(blk % 1 + "img_mlp.gate_up.weight", X.BF16, xo.bf16_bits(wt(blk % 1 + "img_mlp.gate_up.weight")),
+          (4096, 2 * 12288))
+    d.set(blk % 1 + "img_mlp.out.weight", X.F32, wt(blk % 1 + "img_mlp.out.weight"), (12288, 4096))
+    d.set(blk % 1 + "attn.to_out.0.weight", X.BF16, xo.bf16_bits(wt(blk % 1 + "attn.to_out.0.weight")), (4096, 4096))
+    v_mix = X.dit_velocity(d, ctxa, p, lat, h, w, 0.6, prefix_key="k")    # the sets dropped the kept K/V
+    assert np.array_equal(v_mix, v_q8)
+    # the dense rows take a later Q8_0 slot's values: to_q scaled by 2 as Q8_0
+    n = blk % 0 + "attn.to_q.weight"
+    qs, dd = xo.q8_0_synth(seed, xo.tensor_id(n), 4096, 4096)
+    d2 = (dd.astype(np.float32) * 2).astype(np.float16)
+    d.set(n, X.Q8_0, xo.q8_0_to_blocks(qs, d2), (4096, 4096))
+    v_q2 = X.dit_velocity(d, ctxa, p, lat, h, w, 0.6)
+    want = xo.forward(_Weights(wt, {n: xo.dequant_q8_0(qs, d2)}), ctxa, lat, 0.6, layers=2)
+    e = xo.rel_l2(v_q2, want)
+    say("mixed fused matrix after a Q8_0 slot: velocity rel-L2 %.2e" % e)
+    assert e < 1e-2 and xo.rel_l2(v_q2, v_q8) > 1e-5
+    d.destroy()
+
+
 def test_edit_mode(ctx):
     """A reference picture in the prefix (src/cuda-dit.lisp:179-192; host.lisp:37-50):
     3 text rows, a 4 x 5 picture, 9 text rows more, a 4 x 6 image."""

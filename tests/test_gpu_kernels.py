@@ -157,20 +157,90 @@ def test_gemm_bf16_out_and_f32_in(ctx, resident):
 
 
 def test_gemm_weight_f32_branch(ctx):
-    """A non-Q8_0 matrix (src/cuda-dit.lisp:77-80): kept as bf16."""
-    say("gemm f32 weight")
+    """A non-Q8_0 matrix (src/cuda-dit.lisp:77-80): F32 kept as fp32 rows and multiplied in fp32,
+    as d41_mm_f32 (:127-130) -- against the float64 product of the unrounded operands, and
+    visibly apart from a product of bf16-rounded weights; BF16 rows on the bf16 MFMA."""
+    say("gemm f32 weight (fp32 product), bf16 weight")
     rng = np.random.default_rng(2)
+    for M, N, K in ((100, 192, 256), (300, 4096, 4096)):
+        wf = rng.normal(0, 0.05, (N, K)).astype(np.float32)      # not on the bf16 grid
+        x = rng.normal(0, 1, (M, K)).astype(np.float32)
+        w = X.Weight.f32(ctx, wf)
+        y = X.DevBuf(ctx, (M, N), np.float32)
+        X.call("exn_mm", ctx.h, w.h, dev(ctx, x).h, X.DT_F32, y.h, X.DT_F32, M)
+        want = x.astype(np.float64) @ wf.T.astype(np.float64)
+        e = xo.rel_l2(y.get(), want)
+        e_b = xo.rel_l2(y.get(), x.astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64))
+        say("f32 weight %dx%dx%d: rel-L2 %.2e to the fp32 product, %.2e to the bf16-weight product" % (M, N, K, e, e_b))
+        # fp32 sums over K terms: rounding grows about as sqrt(K) x 2^-24 (4096: 4e-6)
+        assert e < 4e-6 and e_b > 1e-4
+        yg = X.DevBuf(ctx, (2, N), np.float32)
+        X.call("exn_mm", ctx.h, w.h, dev(ctx, x[:2]).h, X.DT_F32, yg.h, X.DT_F32, 2)
+        assert xo.rel_l2(yg.get(), want[:2]) < 4e-6
+        # an fp32 matrix multiplies fp32 rows into fp32 rows only
+        with pytest.raises(X.ExnError) as err:
+            X.call("exn_mm", ctx.h, w.h, dev(ctx, bf16(x)).h, X.DT_BF16, y.h, X.DT_F32, M)
+        assert err.value.code == X.EINVAL
+        w.free()
+    # a BF16 matrix: bf16 operands on the MFMA product
     M, N, K = 100, 192, 256
-    wf = rng.normal(0, 0.05, (N, K)).astype(np.float32)
+    wb = bf16(rng.normal(0, 0.05, (N, K)).astype(np.float32))
     x = rng.normal(0, 1, (M, K)).astype(np.float32)
-    w = X.Weight.f32(ctx, wf)
+    wbh = X.Weight.bf16(ctx, wb)
     y = X.DevBuf(ctx, (M, N), np.float32)
-    X.call("exn_mm", ctx.h, w.h, dev(ctx, bf16(x)).h, X.DT_BF16, y.h, X.DT_F32, M)
-    want = from_bf16(bf16(x)).astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)
+    X.call("exn_mm", ctx.h, wbh.h, dev(ctx, bf16(x)).h, X.DT_BF16, y.h, X.DT_F32, M)
+    want = from_bf16(bf16(x)).astype(np.float64) @ from_bf16(wb).T.astype(np.float64)
     assert xo.rel_l2(y.get(), want) < 2e-6
-    yg = X.DevBuf(ctx, (2, N), np.float32)
-    X.call("exn_mm", ctx.h, w.h, dev(ctx, x[:2]).h, X.DT_F32, yg.h, X.DT_F32, 2)
-    assert xo.rel_l2(yg.get(), x[:2].astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)) < 1e-6
+
+
+# the block products of the cached 1024^2 pass's neighbour, the uncached pass: 4352 rows (4096 image +
+# 256 text) through each block matrix with the Q8_0 dequantised inside the product
+CFG1 = {"out": (4096, 4096), "gate_up": (2 * 12288, 4096), "down": (4096, 12288)}
+
+
+@pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])
+@pytest.mark.parametrize("which", list(CFG1))
+def test_block_products_at_4352_rows(ctx, which, resident):
+    """to_out (+ gated residual), gate_up (+ SwiGLU) and down (+ gated residual) at M = 4352 from
+    Q8_0 weights (the dequantisation inside the product) and from the resident bf16 expansion:
+    sampled rows against float64 on the same bf16 operands and against the fp32 oracle."""
+    N, K = CFG1[which]
+    M = 4352
+    say("block product", which, M, N, K, "resident" if resident else "q8_0")
+    rng = np.random.default_rng(N + K)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    xb = bf16(x)
+    seed, tid = 11, 300 + N // 4096 + K // 4096
+    w = X.Weight.synth(ctx, seed, tid, N, K)
+    if resident:
+        w.resident()
+    wf = xo.dequant_q8_0(*xo.q8_0_synth(seed, tid, N, K))
+    rows = np.r_[0:64, 2000:2064, M - 64:M]
+    xr = from_bf16(xb[rows]).astype(np.float64)
+    prod = xr @ from_bf16(bf16(wf)).T.astype(np.float64)
+    prod32 = x[rows] @ wf.T
+    if which == "gate_up":
+        w.pairs()
+        F = N // 2
+        ff = X.DevBuf(ctx, (M, F), np.uint16)
+        X.call("exn_mm_swiglu", ctx.h, w.h, dev(ctx, xb).h, ff.h, M)
+        got = from_bf16(ff.get()[rows])
+        want = prod[:, :F] / (1 + np.exp(-prod[:, :F])) * prod[:, F:]
+        e, e32 = xo.rel_l2(got, want), xo.rel_l2(got, xo.silu(prod32[:, :F]) * prod32[:, F:])
+        say("swiglu rows rel-L2 %.2e (bf16 operands), %.2e (fp32 oracle)" % (e, e32))
+        assert e < 4e-3 and e32 < 2e-2
+    else:
+        n0, p = 0, 256                          # the uncached pass: rows below 256 take the prompt's gate
+        resid = rng.normal(0, 1, (M, N)).astype(np.float32)
+        gate = rng.normal(0, 0.5, (2, 4 * N)).astype(np.float32)
+        r = dev(ctx, resid)
+        X.call("exn_mm_gate_add", ctx.h, w.h, dev(ctx, xb).h, M, r.h, n0, p, 4 * N, dev(ctx, gate).h)
+        g = np.tanh(gate[np.where(rows < p, 1, 0), :N].astype(np.float64))
+        got = r.get()[rows] - resid[rows]
+        e, e32 = xo.rel_l2(got, g * prod), xo.rel_l2(got, g * prod32)
+        say("gated residual rows rel-L2 %.2e (bf16 operands), %.2e (fp32 oracle)" % (e, e32))
+        assert e < 1e-5 and e32 < 1e-2
+    w.free()
 
 
 @pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])

@@ -326,3 +326,60 @@ def test_step_flops_match_the_cost_model():
     assert abs(c["total"] / 1e12 - 66.525) < 0.01
     u = xo.step_flops(4096, 256, cached=False)
     assert abs(u["total"] / 1e12 - 70.133) < 0.01
+
+
+# --- the edit assembly pinned by what the mask fixes --------------------------------------
+
+def _kept(wt, ctx, lat, ref):
+    """An uncached pass's kept prefix K/V, per layer (keys and values, rows 0..p-1)."""
+    cache = xo.PrefixCache()
+    xo.forward(wt, ctx, lat, 0.8, TINY, ref=ref, cache=cache, prefix_key="k")
+    return cache.kv
+
+
+def test_edit_with_an_empty_picture_is_the_plain_step():
+    """A reference picture of 0 x 0 puts nothing in the prefix: positions, mask and
+    rows are the plain step's, so the velocity is the same bits (src/host.lisp:37-50,
+    src/cuda-dit.lisp:179-187, src/cuda/dit.cu:60-66 with b0 = b1)."""
+    wt = xo.SynthWeights(21, TINY, gain=4.0)
+    ctx, lat = xo.synth_inputs(21, 6, 3, 4, TINY)
+    empty = np.zeros((64, 0, 0), np.float32)
+    plain = xo.forward(wt, ctx, lat, 0.7, TINY)
+    for a in (0, 2, 6):
+        assert np.array_equal(xo.forward(wt, ctx, lat, 0.7, TINY, ref=(a, empty)), plain)
+
+
+def test_edit_mask_fixes_what_each_prefix_row_sees():
+    """The prefix is [text 0..a-1 | picture a..a+nref-1 | text a+nref..p-1].  The text rows
+    are causal and the picture's rows see the whole picture and everything before it
+    (xa_lim, src/cuda/dit.cu:60-66), so in the kept K/V of every layer:
+      - the picture changes nothing in rows 0..a-1, and changes the text after it (from the
+        second layer on, once attention has mixed it in);
+      - the text after the picture changes nothing in rows 0..a+nref-1;
+      - the picture's first row sees its last one (the block is whole, not causal)."""
+    wt = xo.SynthWeights(22, TINY, gain=4.0)
+    a, rh, rw = 3, 2, 3
+    nref = rh * rw
+    ctx, lat, rl = xo.synth_inputs(22, 8, 3, 4, TINY, ref_hw=(rh, rw))
+    p = ctx.shape[0] + nref
+    base = _kept(wt, ctx, lat, (a, rl))
+    other_pic = _kept(wt, ctx, lat, (a, rl * 0.5 + 0.3))
+    ctx2 = ctx.copy()
+    ctx2[a:] = ctx2[a:] * -1.0 + 0.2
+    other_after = _kept(wt, ctx2, lat, (a, rl))
+    last = rl.copy()
+    last[:, rh - 1, rw - 1] += 3.0
+    other_last = _kept(wt, ctx, lat, (a, last))
+    for il in range(TINY.layers):
+        for kv in range(2):
+            b = base[il][kv]
+            assert b.shape[0] == p
+            assert np.array_equal(other_pic[il][kv][:a], b[:a])
+            assert np.array_equal(other_after[il][kv][:a + nref], b[:a + nref])
+            assert not np.array_equal(other_after[il][kv][a + nref:], b[a + nref:])
+            if il >= 1:
+                assert np.abs(other_pic[il][kv][a + nref:] - b[a + nref:]).max() > 1e-4
+                assert np.abs(other_last[il][kv][a] - b[a]).max() > 1e-4
+    # and the image rows' positions start after the text that follows the picture
+    pos = xo.positions(p, 3, 4, (a, rh, rw))
+    assert pos[p, 0] == a + max(rh, rw) + (p - a - nref)
