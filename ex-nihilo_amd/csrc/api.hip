@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -55,6 +56,7 @@ struct exn_ctx {
   hipStream_t stream = nullptr;
   void* tmp = nullptr;  // scratch of the op-level entry points (fp32 -> bf16 inputs)
   size_t tmp_bytes = 0;
+  void* scratch = nullptr;  // this device's static scratch array (exn_mm_noalloc)
 };
 
 struct exn_w {
@@ -100,6 +102,32 @@ static void dev_free(void* p) {
 static int use(exn_ctx* ctx) {
   if (!ctx) FAIL(EXN_EINVAL, "null context");
   HIPCHK(hipSetDevice(ctx->device));
+  return EXN_OK;
+}
+
+// --- the no-allocation product's scratch (exn_mm_noalloc) -----------------------------
+// A file-scope device array: every GPU the library runs on holds its own copy until the process
+// ends.  In host code the name `scratch` is a stand-in, not a device address: host code only ever
+// uses the address hipGetSymbolAddress gives for the current device, taken once a device by
+// exn_open and kept per device (g_scratch) and in the context.  Every call on one GPU shares
+// that GPU's array, so calls that overlap on one GPU (two streams, two threads) race.
+static const size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static std::mutex g_scratch_mu;
+static std::map<int, void*> g_scratch;
+
+// this device's scratch address (the device current)
+static int scratch_address(int device, void** out) {
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  auto it = g_scratch.find(device);
+  if (it != g_scratch.end()) {
+    *out = it->second;
+    return EXN_OK;
+  }
+  void* p = nullptr;
+  HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  g_scratch[device] = p;
+  *out = p;
   return EXN_OK;
 }
 
@@ -150,8 +178,13 @@ int exn_open(int device, exn_ctx** out) {
   HIPCHK(hipGetDeviceProperties(&prop, device));
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     FAIL(EXN_ENODEV, "device %d is %s; libexn-hip.so is built for gfx950 only", device, prop.gcnArchName);
+  // the device's scratch address, once a device; should it fail, exn_mm_noalloc tries again
+  // and reports why, and nothing else needs it
+  void* sp = nullptr;
+  if (scratch_address(device, &sp) != EXN_OK) sp = nullptr;
   exn_ctx* ctx = new exn_ctx();
   ctx->device = device;
+  ctx->scratch = sp;
   e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;
@@ -559,6 +592,19 @@ int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int yd
   void* t = nullptr;
   TRY(ctx_tmp(ctx, (size_t)(n * w->cols) * 2, &t));
   return mm_staged(ctx, w, (const float*)x, (uint16_t*)t, y, ydt, n);
+}
+
+int exn_mm_noalloc(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n) {
+  TRY(use(ctx));
+  if (!ctx->scratch) TRY(scratch_address(ctx->device, &ctx->scratch));
+  bool done = false;
+  if (w && n >= 0 && xdt == EXN_DT_F32 && w->kind != EXN_F32 && !(n <= 4 && ydt == EXN_DT_F32) &&
+      (size_t)n * (size_t)w->cols * 2 > kScratchBytes)
+    FAIL(EXN_EINVAL, "exn_mm_noalloc: %lld rows of %lld fp32 inputs need %zu bytes of bf16 staging, past the %zu-byte "
+         "scratch", (long long)n, (long long)w->cols, (size_t)n * (size_t)w->cols * 2, kScratchBytes);
+  TRY(mm_direct(ctx, w, x, xdt, y, ydt, n, &done));
+  if (done) return EXN_OK;
+  return mm_staged(ctx, w, (const float*)x, (uint16_t*)ctx->scratch, y, ydt, n);
 }
 
 int exn_mm_gate_add(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, float* resid, int n0, int p,

@@ -64,6 +64,7 @@ SIGNATURES = {
     "exn_weight_free": (c_int, [vp]),
     "exn_dequant": (c_int, [vp, vp, vp, vp]),
     "exn_mm": (c_int, [vp, vp, vp, c_int, vp, c_int, c_int64]),
+    "exn_mm_noalloc": (c_int, [vp, vp, vp, c_int, vp, c_int, c_int64]),
     "exn_mm_gate_add": (c_int, [vp, vp, vp, c_int64, vp, c_int, c_int, c_int, vp]),
     "exn_mm_swiglu": (c_int, [vp, vp, vp, vp, c_int64]),
     "exn_weight_pairs": (c_int, [vp, vp]),

@@ -103,6 +103,13 @@ int exn_weight_resident(exn_ctx* ctx, exn_w* w, int bf16);
  * An F32 matrix takes fp32 X and Y and multiplies in fp32 (d41_mm_f32); Q8_0 and BF16
  * matrices take bf16 operands (fp32 X rounded to bf16 in a buffer the context grows). */
 int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n);
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops): exn_mm with the same arguments and results,
+ * which calls no hipMalloc or hipFree.  The bf16 copy of fp32 X goes to a static device
+ * array of 64 MiB a GPU (held until the process ends) instead of a buffer the context grows:
+ * n x cols x 2 bytes past 64 MiB is EXN_EINVAL.  Every call on one GPU shares its array,
+ * so calls that overlap on one GPU (two streams or threads) race. */
+int exn_mm_noalloc(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n);
 /* mm, then x_gate_add fused into the product's store (src/cuda/dit.cu:34-41):
  * RESID[t] += tanh(GATE[row]) * (X W^T)[t]; sequence row N0 + t < P takes GATE + MSTRIDE */
 int exn_mm_gate_add(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, float* resid, int n0, int p,
