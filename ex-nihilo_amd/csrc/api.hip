@@ -83,6 +83,14 @@ static const uint16_t* wbf(const exn_w* w) {
   return nullptr;
 }
 
+// the operand a block product streams: the bf16 rows, else the Q8_0 codes and scales (dequantised
+// in the product); an F32 matrix has neither (its products run in fp32)
+static WOp wop(const exn_w* w) {
+  if (const uint16_t* b = wbf(w)) return WOp{b, nullptr, nullptr};
+  if (w->kind == EXN_Q8_0) return WOp{nullptr, w->qs, w->d};
+  return WOp{nullptr, nullptr, nullptr};
+}
+
 static int dev_alloc(void** p, size_t bytes) {
   *p = nullptr;
   if (bytes == 0) bytes = 256;
@@ -519,9 +527,8 @@ static const int64_t kSplitCap = (int64_t)256 * 256 * 256;
 // bits however the rows are tiled, so a cached pass's image rows match the uncached pass's.
 static hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, int64_t nh,
                            Epi epi, const EpiArgs& ea, float* part) {
-  if (nh > 0 && nh < n && nh <= 1024 && part && wbf(w)) {
-    const uint16_t* wb = wbf(w);
-    const hipError_t r = gemm_split_rows(s, x, lda, wb, nh, w->rows, w->cols, epi, ea, part, kSplitCap);
+  if (nh > 0 && nh < n && nh <= 1024 && part && w->kind != EXN_F32) {
+    const hipError_t r = gemm_split_rows(s, x, lda, wop(w), nh, w->rows, w->cols, epi, ea, part, kSplitCap);
     if (r == hipSuccess) {
       EpiArgs eb = ea;   // the remaining rows: every row pointer nh rows on
       eb.n0 = ea.n0 + (int)nh;
@@ -698,7 +705,7 @@ int exn_mm_qkv(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, 
   if (!x_bf16 || !wq || !wk || !cs || !q || !k || !vt) FAIL(EXN_EINVAL, "null pointer");
   if (w->rows != 3 * EXN_W || w->cols != EXN_W || w->pairs)
     FAIL(EXN_EINVAL, "exn_mm_qkv: the fused q | k | v matrix (12288 x 4096) only");
-  if (!wbf(w)) FAIL(EXN_EINVAL, "exn_mm_qkv: bf16 weights (BF16, or Q8_0 with exn_weight_resident) only");
+  if (w->kind == EXN_F32) FAIL(EXN_EINVAL, "exn_mm_qkv: a Q8_0 or BF16 matrix (bf16 products)");
   EpiArgs ea{};
   ea.n0 = (int)row0;
   ea.wq = wq;
@@ -710,7 +717,7 @@ int exn_mm_qkv(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, 
   ea.vt = vt;
   ea.lcap = lcap;
   if (row0 < 0 || row0 > INT32_MAX) FAIL(EXN_EINVAL, "row0");
-  const hipError_t r = gemm_qkv(ctx->stream, x_bf16, EXN_W, wbf(w), n, EXN_W, ea);
+  const hipError_t r = gemm_qkv(ctx->stream, x_bf16, EXN_W, wop(w), n, EXN_W, ea);
   if (r == hipErrorNotSupported)
     FAIL(EXN_EINVAL, "exn_mm_qkv: 16-byte aligned arrays, lcap a multiple of 64, row0 + n <= lcap");
   HIPCHK(r);
@@ -1506,11 +1513,12 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes);
       HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 0 * EXN_W, y, 1));
     }
-    // the QKV product with qk-norm, RoPE and the K/V^T stores in its epilogue (bf16 weights),
-    // else the product to fp16 rows and qkv_prep over them.  (Splitting an uncached pass's
+    // the QKV product with qk-norm, RoPE and the K/V^T stores in its epilogue (bf16 or Q8_0
+    // weights), else (shapes the fused path does not take) the product to fp16 rows and
+    // qkv_prep over them.  (Splitting an uncached pass's
     // prompt rows off, as the other products do, measured no faster here: 768 + 48 tiles.)
     bool fused = false;
-    if (wbf(L.qkv)) {
+    {
       ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
       ea = EpiArgs{};
       ea.n0 = n0;
@@ -1523,7 +1531,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ea.kc = d->kc[(size_t)il];
       ea.vt = d->vt[(size_t)il];
       ea.lcap = d->lcap;
-      const hipError_t r = gemm_qkv(s, y, EXN_W, wbf(L.qkv), n, EXN_W, ea);
+      const hipError_t r = gemm_qkv(s, y, EXN_W, wop(L.qkv), n, EXN_W, ea);
       if (r != hipErrorNotSupported) HIPCHK(r);
       fused = r == hipSuccess;
     }

@@ -42,15 +42,13 @@ __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u 
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
 
-// fp16 bits -> fp32, exact (subnormals included), without relying on the f16 denormal mode
+// fp16 bits -> fp32, exact (subnormals included), without relying on the f16 denormal mode;
+// selects, not branches, so that it can sit in a pipelined loop
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
   const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
-  if (e == 0) {
-    const float v = (float)m * 5.9604644775390625e-08f;   // m * 2^-24
-    return sign ? -v : v;
-  }
-  if (e == 31) return __uint_as_float(sign | 0x7F800000u | (m << 13));
-  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+  const float sub = __uint_as_float(sign | __float_as_uint((float)m * 5.9604644775390625e-08f));   // m * 2^-24
+  const uint32_t big = sign | (e == 31u ? 0x7F800000u : (e + 112u) << 23) | (m << 13);
+  return e == 0u ? sub : __uint_as_float(big);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -174,6 +172,14 @@ struct EpiArgs {
   int64_t qld;   // EPI_QKV: Q's rows a head (the pass's; 0: M)
 };
 
+// a weight matrix as a block product streams it: bf16 rows WB (N x K), or, when WB is null, Q8_0
+// codes QS (N x K int8) and scales QD (N x K/32 fp16), dequantised inside the product
+struct WOp {
+  const uint16_t* wb;
+  const int8_t* qs;
+  const uint16_t* qd;
+};
+
 // Y = X W^T with X bf16 (M x K, lda), W Q8_0 SoA (qs N x K int8, d N x K/32 fp16) or bf16 (N x K)
 hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d,
                    int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
@@ -182,11 +188,11 @@ hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint1
 // rows 0 .. M-1 of a product too short to fill the chip (a pass's prompt rows) with its K split
 // over S workgroups a tile into PART (S x M x N floats, at most PART_CAP), then the sums in
 // order through the epilogue: EPI_GATE_ADD, EPI_SWIGLU, EPI_F32, EPI_BF16 or EPI_F16; bf16 weights
-hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
+hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
                            int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap);
-// the QKV product with the q/k norm, RoPE and the K/V^T stores fused (EPI_QKV), bf16 weights;
-// hipErrorNotSupported when the shapes or alignments do not fit the fused path
-hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t K,
+// the QKV product with the q/k norm, RoPE and the K/V^T stores fused (EPI_QKV), bf16 or Q8_0
+// weights; hipErrorNotSupported when the shapes or alignments do not fit the fused path
+hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t K,
                     const EpiArgs& ea);
 // the edge products: Y = X W^T all fp32 on the SIMD lanes (K % 32 == 0); optional GELU-tanh on Y.
 // W is read from wf32 (fp32 rows) when given, else wbf16 (bf16 rows), else qs/d (Q8_0).

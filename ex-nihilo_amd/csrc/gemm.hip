@@ -17,6 +17,8 @@
 // resident bf16 weights (k_gemm_bt, below) is the one the step uses.
 #include "exn_common.h"
 
+#include <type_traits>
+
 namespace exn {
 
 #define BK 64
@@ -236,11 +238,6 @@ static hipError_t dispatch(hipStream_t s, const uint16_t* x, int64_t lda, const 
     case EPI_F16: return launch<256, 256, 128, 64, WBF16, EPI_F16>(s, x, lda, qs, d, wb, M, N, K, ea);
   }
   return hipErrorInvalidValue;
-}
-
-hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d, int64_t M,
-                   int64_t N, int64_t K, Epi epi, const EpiArgs& ea) {
-  return dispatch<false>(s, x, lda, qs, d, nullptr, M, N, K, epi, ea);
 }
 
 // --- bf16 weights: the pipelined kernel ----------------------------------------------
@@ -505,6 +502,26 @@ __device__ __forceinline__ void epilogue_swiglu(const f32x4 (&acc)[MI][NI], uint
   }
 }
 
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// A buffer resource (V#) for the assembly load below: BASE, no stride, EXTENT bytes (offsets past it
+// read as zeros), the flags the buffer builtins use
+__device__ __forceinline__ i32x4 buffer_desc(const void* base, uint32_t extent) {
+  const uint64_t a = (uint64_t)base;
+  return i32x4{(int32_t)(uint32_t)a, (int32_t)(uint32_t)((a >> 32) & 0xFFFFu), (int32_t)extent, 0x00020000};
+}
+
+// A 4-byte buffer load the compiler does not see as one: it tracks no result for it, and so
+// inserts no wait for it, where its model of the DMA counter is more careful than the schedule
+// needs (the kernel's own vmcnt waits cover the value before its use).  The destination stays
+// allocated to the value from the load to its last use; after the loop the kernel holds it
+// live until every load has landed.
+__device__ __forceinline__ uint32_t buffer_load_u32_untracked(i32x4 rsrc, uint32_t voff, uint32_t soff) {
+  uint32_t v;
+  asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rsrc), "s"(soff));
+  return v;
+}
+
 // One 16-byte DMA lane of a tile: the buffer's extent makes rows past the matrix read as zeros.
 __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
   __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
@@ -514,16 +531,32 @@ __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_
 // NW waves of 128 x (512 / NW) a 256 x 256 tile.  The launch uses 8 waves of 128 x 64, two a
 // SIMD.  4 waves of 128 x 128 (one a SIMD, a third less LDS read a FLOP) were slower under the
 // one-barrier schedule and spill their 256 accumulators under this one.
-template <int EPI, int NW>
+//
+// Q8: W is Q8_0 (qs int8 N x K, d fp16 N x K/32) and is dequantised inside the pipeline.  The
+// int8 codes go HBM -> LDS by the same DMA path into two 16 KB raw stages (so the LDS holds
+// 2 x 64 KB of bf16 stages + 2 x 16 KB of codes = 160 KB), each thread's fp16 scale by a 2-byte
+// buffer load into a register, and once a k-step the 512 threads turn one raw stage into the
+// bf16 W stage the MFMAs read: thread t takes tile row t/2, Q8_0 block t%2 -- 32 codes, two
+// 16-byte LDS reads -- and writes bf16(fp32(d) q) as four swizzled 16-byte rows.  The value is
+// fma(u, d, -128 d) with u = q + 128 the code's unsigned byte (v_cvt_f32_ubyte): u d - 128 d is
+// q d exactly (q d has at most 19 significant bits), rounded once, so the operand is the exact
+// dequantisation rounded to bf16, bit for bit the resident expansion's value for any finite d.
+template <int EPI, int NW, bool Q8>
 __global__ void __launch_bounds__(NW * 64)
-k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB, int64_t M, int64_t N,
-          int64_t K, EpiArgs ea) {
+k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB,
+          const int8_t* __restrict__ QS, const uint16_t* __restrict__ QD, int64_t M, int64_t N, int64_t K,
+          EpiArgs ea) {
   constexpr bool HEADS = EPI == EPI_QKV;   // a wave's columns one head of 128
   constexpr int WM = HEADS ? 64 : 128, WN = HEADS ? 128 : 512 / NW, MI = WM / 16, NI = WN / 16;
   constexpr int ROUNDS = 256 / (NW * 8);
   static_assert((256 / WM) * (256 / WN) == NW, "the waves tile 256 x 256");
-  constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = 2 * ROUNDS;
-  extern __shared__ __align__(1024) uint8_t smem[];   // 2 stages x (X tile 32 KB | W tile 32 KB)
+  static_assert(!Q8 || NW == 8, "the Q8_0 dequantisation maps 512 threads to 256 rows x 2 blocks");
+  // DMA instructions a k-step: X and W rounds (bf16), or X rounds only (Q8: the codes go apart)
+  constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = Q8 ? ROUNDS : 2 * ROUNDS;
+  // Q8: the codes' DMA (16 KB: 2 rounds of 8 waves x 1 KB) and the scale load, a k-step
+  constexpr int NRAW = 2, NQ = NRAW + 1;
+  // 2 stages x (X tile 32 KB | W tile 32 KB), then (Q8) 2 raw code stages x 16 KB
+  extern __shared__ __align__(1024) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS bases stay scalar
   const int wm = wave / (256 / WN), wn = wave % (256 / WN);
@@ -539,14 +572,17 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     bn = in / sz;
   }
   const int64_t m0 = (int64_t)bm * 256, n0 = (int64_t)bn * 256;
-  // split K (EPI_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1
+  // split K (EPI_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1 (Q8: in pairs, K % 128
+  // == 0, so that the main loop runs whole pairs of steps and no third copy of the step is live)
   const int KTT = (int)(K / 64), SK = gridDim.z, zk = blockIdx.z;
-  const int kt0 = (int)((int64_t)KTT * zk / SK), kt1 = (int)((int64_t)KTT * (zk + 1) / SK);
+  const int kt0 = Q8 ? 2 * (int)((int64_t)(KTT / 2) * zk / SK) : (int)((int64_t)KTT * zk / SK);
+  const int kt1 = Q8 ? 2 * (int)((int64_t)(KTT / 2) * (zk + 1) / SK) : (int)((int64_t)KTT * (zk + 1) / SK);
   // DMA: round i of wave w moves rows (i*8 + w)*8 .. +7 of a tile, lane l row +l/8, LDS chunk l%8
   // (global chunk (l%8) ^ swizzle); the k-step is the scalar offset
   const uint16_t* xbase = X + m0 * lda;
   const uint16_t* wbase = WB + n0 * K;
-  const uint32_t xext = (uint32_t)((M - m0) * lda * 2), wext = (uint32_t)(max((int64_t)0, N - n0) * K * 2);
+  const uint32_t xext = (uint32_t)((M - m0) * lda * 2);
+  const uint32_t wext = Q8 ? 0u : (uint32_t)(max((int64_t)0, N - n0) * K * 2);
   uint32_t xoff[ROUNDS], woff[ROUNDS];
 #pragma unroll
   for (int i = 0; i < ROUNDS; ++i) {
@@ -557,8 +593,50 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   }
   auto dma_part = [&](int t, int stage, int p) {   // part p < ROUNDS: X round p, else W round p - ROUNDS
     uint8_t* dst = smem + stage * 65536 + (p < ROUNDS ? 0 : 32768) + ((p % ROUNDS) * NW + wave) * 1024;
-    if (p < ROUNDS) tile_dma(xbase, xext, (lds_void*)dst, xoff[p % ROUNDS], t * 128);
+    if constexpr (Q8)   // round p's rows are round 0's plus p NW 8 (uniform): one offset register, not ROUNDS
+      tile_dma(xbase, xext, (lds_void*)dst, xoff[0], t * 128 + (int)(p * NW * 8 * lda * 2));
+    else if (p < ROUNDS) tile_dma(xbase, xext, (lds_void*)dst, xoff[p % ROUNDS], t * 128);
     else tile_dma(wbase, wext, (lds_void*)dst, woff[p % ROUNDS], t * 128);
+  };
+  // Q8: raw round i of wave w moves code rows (i*8 + w)*16 .. +15 (64 bytes a row), lane l row
+  // +l/4, bytes 16 (l%4) ..; the scales of tile row tid/2, both blocks of the k-step in one dword
+  // (rows past N read as zeros) -- a 32-bit value, so that no widening of it is hoisted to the
+  // loop's head, where it would wait for the load before its time
+  const int8_t* qbase = QS + n0 * K;
+  const uint32_t qext = Q8 ? (uint32_t)(max((int64_t)0, N - n0) * K) : 0u;
+
+  const i32x4 drsrc =
+      buffer_desc(QD + n0 * (K / 32), Q8 ? (uint32_t)(max((int64_t)0, N - n0) * (K / 32) * 2) : 0u);
+  const uint32_t roff0 = (uint32_t)((wave * 16 + (lane >> 2)) * K + 16 * (lane & 3));
+  const int dq_row = tid >> 1, dq_blk = tid & 1;
+  const uint32_t doff = (uint32_t)(dq_row * (K / 32) * 2);
+  auto raw_dma = [&](int t, int stage, int i) {
+    uint8_t* dst = smem + 131072 + stage * 16384 + (i * NW + wave) * 1024;
+    tile_dma(qbase, qext, (lds_void*)dst, roff0, t * 64 + (int)(i * NW * 16 * K));
+  };
+  auto scale_load = [&](int t) -> uint32_t { return buffer_load_u32_untracked(drsrc, doff, (uint32_t)(t * 4)); };
+  // Q8: the thread's 32 codes of raw stage rs into bf16 W stage ws, the block's fp16 scale the
+  // half dq_blk of DPAIR; parts 0 and 5 read 16 codes each, parts 1..4 and 6..9 convert one
+  // 4-code word each and store its 8 bytes of bf16
+  u32x4 dq_q;
+  float dq_d = 0.f, dq_nd = 0.f;
+  auto dequant = [&](int part, int rs, int ws, uint32_t dpair) {
+    const uint8_t* src = smem + 131072 + rs * 16384 + tid * 32;
+    if (part == 0 || part == 5) {
+      dq_q = *(const u32x4*)(src + (part == 5 ? 16 : 0));
+      if (part == 0) {
+        dq_d = f16_to_f32((dpair >> (16 * dq_blk)) & 0xFFFFu);
+        dq_nd = -128.f * dq_d;
+      }
+      return;
+    }
+    const int j = part < 5 ? part - 1 : part - 2;
+    const uint32_t u = dq_q[j & 3];
+    const float f0 = (float)(int8_t)(u & 0xFFu) * dq_d, f1 = (float)(int8_t)((u >> 8) & 0xFFu) * dq_d;
+    const float f2 = (float)(int8_t)((u >> 16) & 0xFFu) * dq_d, f3 = (float)(int8_t)(u >> 24) * dq_d;
+    const int c = (4 * dq_blk + (j >> 1)) ^ chunk_swz(dq_row);
+    *(u32x2*)(smem + ws * 65536 + 32768 + dq_row * 128 + c * 16 + 8 * (j & 1)) =
+        u32x2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
   };
   // v_mfma_f32_16x16x32_bf16 operands: lane l holds row l%16, k = 8*(l/16) .. +7 of a slice of 32
   const int lo = lane & 15, q4 = lane >> 4, fs = chunk_swz(lo);
@@ -586,9 +664,25 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   //   MFMAs B2 .. B2+NRD-1 read step t+1's first-slice fragments (stage cur^1) into F0.
   // The DMA then has from B1 of one step to B2 of the next to land (about 1.6 steps), and the
   // barrier before the DMA waits on no memory.
+  // Q8 adds: after B1, the dequantisation of step t+2's codes (raw stage cur, landed: B1 waits
+  // for them) into the freed W stage cur, spread over MFMAs DQ0 .. DQ0+18 of the second slice,
+  // when this step's first-slice fragments are dead (their registers hold it); at DQ0+1, the
+  // load of step t+3's scales into the register part 0 has just read; after B2, the codes' DMA
+  // of step t+4 into raw stage cur (free: every wave's dequantisation reads of it are behind
+  // B2), so the codes have about 1.5 steps to land and the scales about one.  The X DMA of step
+  // t+2 goes out in four parts, at B1 and after the scale load (DQ0+3, +5, +7).  So B1's wait
+  // leaves out the 3 X parts and 2 code DMAs issued after the scales it needs (the X part at
+  // B1 of the step before must have landed too), and B2's the codes of step t+3, the X DMA of
+  // step t+2 and the scale load between its parts.  The dequantisation's stores are done
+  // (lgkmcnt 0) at the next B1, a step before anything reads them.
   constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DSPREAD = NMF;
+  constexpr int DQ0 = NMF;
+  constexpr int B1_VM = Q8 ? (NDMA - 1) + NRAW : 63, B2_VM = Q8 ? NRAW + NDMA + 1 : NDMA;
   // B2 lets this step's NDMA DMA parts stay outstanding, and no more: they must all be out
   static_assert(B1 >= NRD && B1 + DSPREAD <= B2 && B2 + NRD <= 2 * NMF, "step schedule");
+  static_assert(!Q8 || (DQ0 > B1 && DQ0 + 18 < B2), "the dequantisation fits between the barriers");
+  // Q8: the scales of the k-step the next dequantisation takes (both blocks of each tile row)
+  uint32_t sc = 0;
   auto step = [&](Frag& F0, Frag& F1, int t) {
     const int cur = (t - kt0) & 1, nx = min(t + 2, kt1 - 1);
     // MFMA position x of the step: a lambda unrolled over two loops of NMF, each small
@@ -597,13 +691,16 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     auto pos = [&](const int x) {
       if (x == B1) {
         asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));   // LDS reads done
+        __builtin_amdgcn_s_waitcnt((B1_VM & 15) | (0x7 << 4) | (0x0 << 8) | ((B1_VM >> 4) << 14));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
+        // Q8: the scale load is invisible to the compiler; this marks its register as written
+        // here, after the wait that covers it, so that no use of it moves above the wait
+        if constexpr (Q8) asm volatile("" : "+v"(sc));
       }
       if (x == B2) {
         asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt((NDMA & 15) | (0x7 << 4) | (0x0 << 8) | ((NDMA >> 4) << 14));
+        __builtin_amdgcn_s_waitcnt((B2_VM & 15) | (0x7 << 4) | (0x0 << 8) | ((B2_VM >> 4) << 14));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
       }
@@ -616,10 +713,22 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
             __builtin_amdgcn_mfma_f32_16x16x32_bf16(F1.v[y / NI], F1.v[MI + y % NI], acc[y / NI][y % NI], 0, 0, 0);
       if (x < NRD) rd1(F1, cur, 1, x);
       if (x >= B2 && x < B2 + NRD) rd1(F0, cur ^ 1, 0, x - B2);
-      if (x >= B1 && x < B1 + DSPREAD) {
+      if constexpr (Q8) {
+        static_assert(NDMA == 4, "X parts at B1, DQ0+3, DQ0+5, DQ0+7");
+        if (x == B1) dma_part(nx, cur, 0);
+        if (x == DQ0 + 3 || x == DQ0 + 5 || x == DQ0 + 7) dma_part(nx, cur, (x - DQ0 - 1) / 2);
+      } else if (x >= B1 && x < B1 + DSPREAD) {
 #pragma unroll
         for (int p = ((x - B1) * NDMA) / DSPREAD; p < ((x - B1 + 1) * NDMA) / DSPREAD && p < NDMA; ++p)
           dma_part(nx, cur, p);
+      }
+      if constexpr (Q8) {
+        if (x >= DQ0 && x <= DQ0 + 18 && (x - DQ0) % 2 == 0) dequant((x - DQ0) / 2, cur, cur, sc);
+        const int nq = min(t + 4, kt1 - 1);   // the codes' step
+        if (x == B2 + 1) raw_dma(nq, cur, 0);
+        if (x == B2 + 4) raw_dma(nq, cur, 1);
+        // the next step's scales, into the register part 0 of the dequantisation has just read
+        if (x == DQ0 + 1) sc = scale_load(min(t + 3, kt1 - 1));
       }
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -629,17 +738,48 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     for (int x = NMF; x < 2 * NMF; ++x) pos(x);
   };
   Frag F0, F1;
+  if constexpr (Q8) {
+    // stages 0, 1 of steps kt0, kt0 + 1: codes, scales and X by DMA, then both dequantised
+    const int t1 = min(kt0 + 1, kt1 - 1);
+    raw_dma(kt0, 0, 0);
+    raw_dma(kt0, 0, 1);
+    raw_dma(t1, 1, 0);
+    raw_dma(t1, 1, 1);
+    uint32_t sa = scale_load(kt0), sb = scale_load(t1);
 #pragma unroll
-  for (int p = 0; p < NDMA; ++p) dma_part(kt0, 0, p);
-  LDS_VMCNT0_BARRIER();
+    for (int p = 0; p < NDMA; ++p) dma_part(kt0, 0, p);
+    LDS_VMCNT0_BARRIER();
+    asm volatile("" : "+v"(sa), "+v"(sb));   // the scales' uses stay after the wait (see B1)
 #pragma unroll
-  for (int p = 0; p < NDMA; ++p) dma_part(min(kt0 + 1, kt1 - 1), 1, p);
+    for (int part = 0; part <= 9; ++part) dequant(part, 0, 0, sa);
 #pragma unroll
-  for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
-  // past the end the DMA re-reads the last step into the free stage, and nothing reads it:
-  // no branch, so the order holds
-  for (int t = kt0; t < kt1; ++t) step(F0, F1, t);
+    for (int part = 0; part <= 9; ++part) dequant(part, 1, 1, sb);
+    LDS_VMCNT0_BARRIER();   // the codes read, stages 0 and 1 of W written
+    // in the order the loop's waits count: codes of kt0 + 2, X of kt0 + 1, codes of kt0 + 3
+    raw_dma(min(kt0 + 2, kt1 - 1), 0, 0);
+    raw_dma(min(kt0 + 2, kt1 - 1), 0, 1);
+    sc = scale_load(min(kt0 + 2, kt1 - 1));
+#pragma unroll
+    for (int p = 0; p < NDMA; ++p) dma_part(t1, 1, p);
+    raw_dma(min(kt0 + 3, kt1 - 1), 1, 0);
+    raw_dma(min(kt0 + 3, kt1 - 1), 1, 1);
+#pragma unroll
+    for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
+    for (int t = kt0; t < kt1; ++t) step(F0, F1, t);
+  } else {
+#pragma unroll
+    for (int p = 0; p < NDMA; ++p) dma_part(kt0, 0, p);
+    LDS_VMCNT0_BARRIER();
+#pragma unroll
+    for (int p = 0; p < NDMA; ++p) dma_part(min(kt0 + 1, kt1 - 1), 1, p);
+#pragma unroll
+    for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
+    // past the end the DMA re-reads the last step into the free stage, and nothing reads it:
+    // no branch, so the order holds
+    for (int t = kt0; t < kt1; ++t) step(F0, F1, t);
+  }
   LDS_VMCNT0_BARRIER();   // the last DMA has landed before the epilogue takes the LDS over
+  if constexpr (Q8) asm volatile("" ::"v"(sc));   // the last scale load has landed too
   if constexpr (HEADS)
     epilogue_qkv<MI, NI>(acc, (float*)smem + wave * (16 * 132), m0 + wm * WM, n0 + wn * WN, lane, M, ea);
   else if constexpr (EPI == EPI_SWIGLU)
@@ -648,12 +788,14 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
-template <int EPI>
+// bf16 weights WB, or (Q8) Q8_0 weights QS/QD dequantised in the pipeline
+template <int EPI, bool Q8 = false>
 static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* wb, int64_t M, int64_t N,
-                            int64_t K, const EpiArgs& ea, int split = 1) {
-  const size_t shm = 2 * 65536;
+                            int64_t K, const EpiArgs& ea, int split = 1, const int8_t* qs = nullptr,
+                            const uint16_t* qd = nullptr) {
+  const size_t shm = Q8 ? 2 * 65536 + 2 * 16384 : 2 * 65536;
   constexpr int NW = 8;
-  auto kern = k_gemm_bt<EPI, NW>;
+  auto kern = k_gemm_bt<EPI, NW, Q8>;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
@@ -661,8 +803,43 @@ static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const
     attr = true;
   }
   dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256), (unsigned)split);
-  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, M, N, K, ea);
+  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, qs, qd, M, N, K, ea);
   return hipGetLastError();
+}
+
+// the LDS-DMA pipeline's conditions on X and the output (16-byte chunks of X rows, 4-column
+// stores, buffer extents within 31 bits) and on the weight (bf16 rows or Q8_0 codes)
+static bool dma_fits(const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K,
+                     const EpiArgs& ea) {
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  // Q8_0 codes: K % 128 == 0 (the kernel runs k-steps in pairs)
+  const bool wok = w.wb ? (a16(w.wb) && N * K < (int64_t)1 << 30)
+                        : (w.qs && w.qd && a16(w.qs) && ((uintptr_t)w.qd & 1) == 0 && N * K < (int64_t)1 << 31 &&
+                           K % 128 == 0);
+  return wok && K % 64 == 0 && lda % 8 == 0 && a16(x) && M * lda < (int64_t)1 << 30 && N % 4 == 0 &&
+         ea.ldy % 4 == 0 && a16(ea.y) && a16(ea.resid) && a16(ea.gate) && ea.mstride % 4 == 0;
+}
+
+template <int EPI>
+static hipError_t launch_w(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
+                           int64_t K, const EpiArgs& ea, int split = 1) {
+  if (w.wb) return launch_bt<EPI, false>(s, x, lda, w.wb, M, N, K, ea, split);
+  return launch_bt<EPI, true>(s, x, lda, nullptr, M, N, K, ea, split, w.qs, w.qd);
+}
+
+hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d, int64_t M,
+                   int64_t N, int64_t K, Epi epi, const EpiArgs& ea) {
+  const WOp w{nullptr, qs, d};
+  if (!dma_fits(x, lda, w, M, N, K, ea)) return dispatch<false>(s, x, lda, qs, d, nullptr, M, N, K, epi, ea);
+  switch (epi) {
+    case EPI_F32: return launch_w<EPI_F32>(s, x, lda, w, M, N, K, ea);
+    case EPI_BF16: return launch_w<EPI_BF16>(s, x, lda, w, M, N, K, ea);
+    case EPI_GATE_ADD: return launch_w<EPI_GATE_ADD>(s, x, lda, w, M, N, K, ea);
+    case EPI_SWIGLU: return launch_w<EPI_SWIGLU>(s, x, lda, w, M, N, K, ea);
+    case EPI_GELU_BF16: return launch_w<EPI_GELU_BF16>(s, x, lda, w, M, N, K, ea);
+    case EPI_F16: return launch_w<EPI_F16>(s, x, lda, w, M, N, K, ea);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 // the S partial sums of a split product in order, through the epilogue: 4 output columns a
@@ -704,7 +881,7 @@ k_split_sum(int S, int64_t M, int64_t N, const float* __restrict__ part, EpiArgs
   }
 }
 
-hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
+hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
                            int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap) {
   if (M == 0) return hipSuccess;
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -716,14 +893,13 @@ hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const 
   if (S > K / 64 / 4) S = K / 64 / 4;
   if (S > 8) S = 8;
   if (S < 1) S = 1;
-  const bool ok = K % 64 == 0 && lda % 8 == 0 && N % 256 == 0 && a16(x) && a16(w) && a16(part) &&
-                  M * lda < (int64_t)1 << 30 && N * K < (int64_t)1 << 30 && S * M * N <= part_cap &&
-                  (epi == EPI_GATE_ADD || epi == EPI_SWIGLU || epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_F16);
-  if (!ok) return hipErrorNotSupported;
   EpiArgs pa{};
   pa.y = part;
   pa.ldy = N;
-  hipError_t e = launch_bt<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
+  const bool ok = N % 256 == 0 && a16(part) && S * M * N <= part_cap && dma_fits(x, lda, w, M, N, K, pa) &&
+                  (epi == EPI_GATE_ADD || epi == EPI_SWIGLU || epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_F16);
+  if (!ok) return hipErrorNotSupported;
+  hipError_t e = launch_w<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
   if (e != hipSuccess) return e;
   const int64_t threads = M * (epi == EPI_SWIGLU ? N / 2 : N) / 4;
   const dim3 g((unsigned)((threads + 255) / 256));
@@ -737,38 +913,33 @@ hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const 
   return hipGetLastError();
 }
 
-hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t K,
+hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t K,
                     const EpiArgs& ea) {
   const int64_t N = 3 * EXN_W;
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  // the DMA path's conditions, and 16-byte rows of q, k, V^T, the weights and the cos/sin table
-  const bool ok = K % 64 == 0 && lda % 8 == 0 && a16(x) && a16(w) && M * lda < (int64_t)1 << 30 &&
-                  N * K < (int64_t)1 << 30 && a16(ea.q) && a16(ea.kc) && a16(ea.vt) && a16(ea.wq) && a16(ea.wk) &&
-                  a16(ea.cs) && ea.lcap % 64 == 0 && ea.n0 >= 0 && ea.n0 + M <= ea.lcap;
+  // the DMA path's conditions, and 16-byte rows of q, k, V^T, the norm weights and the cos/sin table
+  EpiArgs pa{};
+  pa.ldy = 4;
+  const bool ok = dma_fits(x, lda, w, M, N, K, pa) && a16(ea.q) && a16(ea.kc) && a16(ea.vt) && a16(ea.wq) &&
+                  a16(ea.wk) && a16(ea.cs) && ea.lcap % 64 == 0 && ea.n0 >= 0 && ea.n0 + M <= ea.lcap;
   if (!ok) return hipErrorNotSupported;
   if (M == 0) return hipSuccess;
-  return launch_bt<EPI_QKV>(s, x, lda, w, M, N, K, ea);
+  return launch_w<EPI_QKV>(s, x, lda, w, M, N, K, ea);
 }
 
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
                       int64_t K, Epi epi, const EpiArgs& ea) {
-  // the DMA path moves 16-byte chunks: rows of X and W must start 16-byte aligned
-  // and the epilogue stores 4 columns at once: N, the output's row stride and base aligned to 4 values
-  // and the buffer extents (bytes from a tile's first row to the matrix's end) fit 31 bits
-  const bool dma_ok = K % 64 == 0 && lda % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
-                      M * lda < (int64_t)1 << 30 && N * K < (int64_t)1 << 30 &&
-                      N % 4 == 0 && ea.ldy % 4 == 0 && ((uintptr_t)ea.y & 15) == 0 && ((uintptr_t)ea.resid & 15) == 0 &&
-                      ((uintptr_t)ea.gate & 15) == 0 && ea.mstride % 4 == 0;
-  if (!dma_ok) return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
+  const WOp wo{w, nullptr, nullptr};
+  if (!dma_fits(x, lda, wo, M, N, K, ea)) return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
   switch (epi) {
-    case EPI_F32: return launch_bt<EPI_F32>(s, x, lda, w, M, N, K, ea);
-    case EPI_BF16: return launch_bt<EPI_BF16>(s, x, lda, w, M, N, K, ea);
-    case EPI_GATE_ADD: return launch_bt<EPI_GATE_ADD>(s, x, lda, w, M, N, K, ea);
-    case EPI_SWIGLU: return launch_bt<EPI_SWIGLU>(s, x, lda, w, M, N, K, ea);
-    case EPI_GELU_BF16: return launch_bt<EPI_GELU_BF16>(s, x, lda, w, M, N, K, ea);
-    case EPI_F16: return launch_bt<EPI_F16>(s, x, lda, w, M, N, K, ea);
+    case EPI_F32: return launch_w<EPI_F32>(s, x, lda, wo, M, N, K, ea);
+    case EPI_BF16: return launch_w<EPI_BF16>(s, x, lda, wo, M, N, K, ea);
+    case EPI_GATE_ADD: return launch_w<EPI_GATE_ADD>(s, x, lda, wo, M, N, K, ea);
+    case EPI_SWIGLU: return launch_w<EPI_SWIGLU>(s, x, lda, wo, M, N, K, ea);
+    case EPI_GELU_BF16: return launch_w<EPI_GELU_BF16>(s, x, lda, wo, M, N, K, ea);
+    case EPI_F16: return launch_w<EPI_F16>(s, x, lda, wo, M, N, K, ea);
+    default: return hipErrorInvalidValue;
   }
-  return hipErrorInvalidValue;
 }
 
 // --- the edge products in fp32 -------------------------------------------------------

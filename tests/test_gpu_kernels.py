@@ -397,16 +397,18 @@ def test_qkv_prep(ctx):
     assert sorted(vt_pos(np.arange(lcap))) == list(range(lcap))  # a permutation inside each 16 keys
 
 
+@pytest.mark.parametrize("resident", [True, False], ids=["resident_bf16", "q8_0"])
 @pytest.mark.parametrize("n,row0,lcap", [(300, 37, 384), (512, 256, 832), (257, 0, 320)])
-def test_mm_qkv_fused(ctx, n, row0, lcap):
+def test_mm_qkv_fused(ctx, n, row0, lcap, resident):
     """exn_mm_qkv: the QKV product with x_qk_norm_rope and the K/V^T stores in its epilogue,
     against the unfused pair (exn_mm to fp16 rows, then exn_qkv_prep) on the same operands --
     V^T bit-exact (the same fp32 sums, rounded once), q and k within fp16 rounding -- and
     against float64 on three heads.  row0 37: V^T key by key; 256: 16 keys at once; n 257:
-    a last tile of one row.  K rows and V^T columns outside row0 .. row0+n-1 stay as they were."""
-    say("mm_qkv n", n, "row0", row0, "lcap", lcap)
+    a last tile of one row.  K rows and V^T columns outside row0 .. row0+n-1 stay as they were.
+    From the resident bf16 expansion or from Q8_0 dequantised in the product."""
+    say("mm_qkv n", n, "row0", row0, "lcap", lcap, "resident" if resident else "q8_0")
     rng = np.random.default_rng(n + row0)
-    w = X.Weight.synth(ctx, 9, 400, 3 * 4096, 4096).resident()
+    w = X.Weight.synth(ctx, 9, 400, 3 * 4096, 4096).resident(resident)
     x = rng.normal(0, 1, (n, 4096)).astype(np.float32)
     xb = bf16(x)
     wq = (1 + 0.1 * rng.normal(0, 1, 128)).astype(np.float32)
