@@ -17,7 +17,14 @@ WRITE_SIZE (profiles/), or null.
 
 cpu_baseline: the oracle (oracle/exn_oracle.py, numpy fp32) timed on this
 host for blocks 0..4 of the same cached workload, their mean x 32 blocks
-(extrapolated).
+(extrapolated); beside it the single-block workload (1024 image + 64 text rows,
+uncached) as the median of 3, and the host's CPU model, cores and BLAS.
+
+q8_0: the same cached step with the block matrices multiplied from Q8_0, the
+codes dequantised inside the products (no resident bf16 copy), with its gate_up
+roofline.  cfg3_1536x1024 / cfg4_edit: cached and uncached steps of the
+1536 x 1024 workload (6144 image + 256 text rows) and of the edit workload
+(512 text rows + a 64 x 64 reference picture + a 64 x 64 image: 8704 keys).
 
 vae_decode_1024sq: the VAE decoder (synthetic bf16 weights) on the 8-step loop's
 final latent, 64 x 64 -> a 1024 x 1024 RGBA picture, the mean of 5 decodes.
@@ -55,14 +62,45 @@ def gemm_flops_per_row():
     return 2 * (4 * Wd * Wd + Wd * 2 * F + F * Wd)
 
 
-def step_flops(cached):
-    n = H * W if cached else P + H * W
-    l = P + H * W
-    n0 = P if cached else 0
-    pairs = sum((l if g >= P else g + 1) for g in range(n0, n0 + n))
+def step_flops(cached, nimg=H * W, ptext=P, nref=0, a=0):
+    """Block products and attention of one step: the prefix is PTEXT text rows and NREF rows
+    of a reference picture after the first A of them; attention counts the (query, key)
+    pairs the mask leaves visible (image rows: all keys; the picture's rows: the picture and
+    what is before it; text rows: causal)."""
+    p = ptext + nref
+    n = nimg if cached else p + nimg
+    l = p + nimg
+    n0 = p if cached else 0
+    b0, b1 = a, a + nref
+    pairs = 0
+    for g in range(n0, n0 + n):
+        pairs += l if g >= p else (b1 if b0 <= g < b1 else g + 1)
     gemm = LAYERS * n * gemm_flops_per_row()
     att = LAYERS * 4 * 128 * 32 * pairs
     return gemm, att, gemm + att
+
+
+def host_info():
+    """The host the CPU baseline ran on: model, usable cores, BLAS and its thread settings."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    blas = None
+    try:
+        cfg = np.show_config(mode="dicts")
+        b = cfg.get("Build Dependencies", {}).get("blas", {})
+        blas = "%s %s" % (b.get("name", "?"), b.get("version", ""))
+    except Exception:
+        pass
+    return {"cpu_model": model, "cpu_count": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "blas": blas, "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+            "OPENBLAS_NUM_THREADS": os.environ.get("OPENBLAS_NUM_THREADS")}
 
 
 def cpu_baseline(blocks=5):
@@ -90,12 +128,23 @@ def cpu_baseline(blocks=5):
         x = xo.block(wt, layer, x, mod, cos, sin, kf, vf, P, P, 0, 0)
         times.append(time.perf_counter() - t0)
     dt = float(np.mean(times))
+    # the single-block workload: 1024 image rows (32 x 32) and 64 text rows, uncached, sigma 0.5
+    c0, l0 = xo.synth_inputs(0, 64, 32, 32)
+    b_times = []
+    for r in range(4):   # one warm-up (dequantisation of block 0's weights), then the median of 3
+        t0 = time.perf_counter()
+        xo.forward(wt, c0, l0, 0.5, layers=1)
+        b_times.append(time.perf_counter() - t0)
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     threads = int(os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS") or cores)
     return {"value": round(dt * 1e3 * LAYERS, 1), "unit": "ms/step", "cores": min(cores, threads), "kind": "port",
             "sample": "blocks 0..%d of the cached 1024^2 step (4096 image rows over 4352 keys) in numpy fp32, "
                       "%.1f s of block time (%s s each), mean x 32 blocks: an extrapolated step"
-                      % (blocks - 1, sum(times), "/".join("%.1f" % t for t in times))}
+                      % (blocks - 1, sum(times), "/".join("%.1f" % t for t in times)),
+            "one_block_1088_rows_ms": round(float(np.median(b_times[1:])) * 1e3, 1),
+            "one_block_sample": "the single-block workload (1024 image + 64 text rows, uncached, sigma 0.5, "
+                                "with the edge products and the velocity), median of 3 after a warm-up",
+            "host": host_info()}
 
 
 def traffic_from(fetch_db, write_db):
@@ -115,7 +164,8 @@ def traffic_from(fetch_db, write_db):
 
     f, w = per_kernel(fetch_db, "FETCH_SIZE"), per_kernel(write_db, "WRITE_SIZE")
     copy = [k for k in f if "copyBuffer" in k]
-    gemm = [k for k in f if "k_gemm_bt<3>" in k or "k_gemm_bt<3," in k]   # EPI_SWIGLU, any wave count
+    # EPI_SWIGLU on bf16 weights (the Q8_0 variant of the kernel, <3, 8, true>, runs in the q8_0 section)
+    gemm = [k for k in f if ("k_gemm_bt<3>" in k or "k_gemm_bt<3," in k) and "true" not in k]
     if not copy or not gemm:
         sys.exit("bench.py: the databases hold no copy probe or no gate_up product")
     big = lambda v: max(v)                                   # the probe is the largest copy
@@ -198,14 +248,17 @@ def main():
     import exn_hip as X
     ctx = X.Context(0)
     d = X.Dit(ctx, LAYERS)
+    ctx.sync()
     t0 = time.perf_counter()
-    d.synth(SEED)
+    d.synth(SEED)   # synchronous: returns once the weights are made
     d.check()
     t1 = time.perf_counter()
-    d.resident(True)
+    d.resident(True)   # synchronous too
+    t2 = time.perf_counter()
     w_bytes, _ = d.memory()
-    print("bench: synthetic 7B Q8_0 DiT on the device in %.1f s, block matrices expanded to resident bf16 in %.1f s "
-          "(%.1f GB of weights)" % (t1 - t0, time.perf_counter() - t1, w_bytes / 1e9), file=sys.stderr, flush=True)
+    print("bench: synthetic 7B Q8_0 DiT made on the device in %.1f ms, block matrices expanded to resident bf16 in "
+          "%.1f ms (%.1f GB of weights)" % ((t1 - t0) * 1e3, (t2 - t1) * 1e3, w_bytes / 1e9), file=sys.stderr,
+          flush=True)
     if a.copy_probe:
         src = X.DevBuf(ctx, (a.copy_probe << 20,), np.uint8)
         dst = X.DevBuf(ctx, (a.copy_probe << 20,), np.uint8)
@@ -307,6 +360,73 @@ def main():
     vae_w, vae_s = vae.memory()
     vae.destroy()
 
+    # the 1536 x 1024 and edit workloads on the same weights: cached and uncached steps
+    def workload_times(hh, ww, ptext, ref, reps=3):
+        r2 = np.random.default_rng(hh * ww + ptext)
+        cx = X.DevBuf.of(ctx, r2.normal(0, 1, (ptext, 4096)).astype(np.float32))
+        zc = X.DevBuf.of(ctx, r2.normal(0, 1, (64, hh, ww)).astype(np.float32))
+        vc = X.DevBuf(ctx, (64, hh, ww), np.float32)
+        if ref:
+            ra, rh, rw = ref
+            rl = X.DevBuf.of(ctx, r2.normal(0, 1, (64, rh, rw)).astype(np.float32))
+            refargs = (ra, rl.h, rh, rw)
+        else:
+            refargs = (0, None, 0, 0)
+
+        def vel(k, s):
+            X.call("exn_dit_velocity_dev", d.h, cx.h, ptext, zc.h, hh, ww, s, k, *refargs, vc.h)
+
+        vel(900, sig[0])              # the shape's workspace and K/V arrays allocated
+        ctx.sync()
+        t0 = time.perf_counter()
+        for r in range(reps):         # uncached: a fresh key each call
+            vel(901 + r, sig[0])
+        ctx.sync()
+        t_unc = (time.perf_counter() - t0) / reps
+        vel(950, sig[0])              # the prompt's K/V kept under 950
+        ctx.sync()
+        t0 = time.perf_counter()
+        for r in range(reps):
+            vel(950, sig[1 + r % 7])
+        ctx.sync()
+        t_c = (time.perf_counter() - t0) / reps
+        ok = bool(np.isfinite(vc.get()).all())
+        nref = ref[1] * ref[2] if ref else 0
+        fa = ref[0] if ref else 0
+        fc = step_flops(True, hh * ww, ptext, nref, fa)[2]
+        fu = step_flops(False, hh * ww, ptext, nref, fa)[2]
+        return {"image_rows": hh * ww, "text_rows": ptext, "reference_rows": nref, "keys": ptext + nref + hh * ww,
+                "cached_ms": round(t_c * 1e3, 2), "cached_tflop": round(fc / 1e12, 2),
+                "cached_tflops": round(fc / t_c / 1e12, 1),
+                "uncached_ms": round(t_unc * 1e3, 2), "uncached_tflop": round(fu / 1e12, 2),
+                "uncached_tflops": round(fu / t_unc / 1e12, 1), "velocity_finite": ok}
+
+    workloads = {"cfg3_1536x1024": workload_times(96, 64, 256, None),
+                 "cfg4_edit_1024sq": workload_times(64, 64, 512, (8, 64, 64))}
+
+    # the same cached 1024^2 step with the block matrices multiplied from Q8_0: the codes
+    # dequantised inside the products' pipeline, the resident bf16 copies dropped (the change of
+    # product path drops the kept K/V too, so the first step recomputes them)
+    d.resident(False)
+    q8_w_bytes, _ = d.memory()
+    for i in range(1 + a.warmup):
+        step(1 + i, key)
+    ctx.sync()
+    d.profile(True, classes=["gate_up"], every=4)
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        step(1 + i, key)
+    ctx.sync()
+    t_q8 = (time.perf_counter() - t0) / a.steps
+    d.profile(False)
+    q8_gu = d.profile_read()["gate_up"]
+    d.profile(True, every=1)
+    for i in range(BREAKDOWN):
+        step(1 + i, key)
+    ctx.sync()
+    d.profile(False)
+    q8prof = d.profile_read()
+
     gemm_f, att_f, tot_f = step_flops(True)
     tflops = tot_f / (ms * 1e-3) / 1e12
     gu_ms, gu_n, gu_f, gu_b = gu_timed
@@ -315,29 +435,53 @@ def main():
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         traffic = json.load(open(TRAFFIC_FILE)).get("bytes_per_launch")
-    gemm_ms = sum(prof[c][0] for c in ("qkv", "out", "gate_up", "down"))
-    gemm_flops = sum(prof[c][2] for c in ("qkv", "out", "gate_up", "down"))
-    kernels = {c: {"ms_per_step": round(prof[c][0] / BREAKDOWN, 3), "launches_per_step": prof[c][1] // BREAKDOWN,
-                   **({"tflops": round(prof[c][2] / (prof[c][0] * 1e-3) / 1e12, 1)} if prof[c][2] else {}),
-                   **({"gbs": round(prof[c][3] / (prof[c][0] * 1e-3) / 1e9, 1)} if prof[c][3] and not prof[c][2]
-                      else {})}
-               for c in X.Dit.PROFILE_CLASSES if prof[c][1]}
+    def breakdown(pr):
+        return {c: {"ms_per_step": round(pr[c][0] / BREAKDOWN, 3), "launches_per_step": pr[c][1] // BREAKDOWN,
+                    **({"tflops": round(pr[c][2] / (pr[c][0] * 1e-3) / 1e12, 1)} if pr[c][2] else {}),
+                    **({"gbs": round(pr[c][3] / (pr[c][0] * 1e-3) / 1e9, 1)} if pr[c][3] and not pr[c][2] else {})}
+                for c in X.Dit.PROFILE_CLASSES if pr[c][1]}
+
+    def gemm_rate(pr):
+        g_ms = sum(pr[c][0] for c in ("qkv", "out", "gate_up", "down"))
+        g_f = sum(pr[c][2] for c in ("qkv", "out", "gate_up", "down"))
+        return g_f / (g_ms * 1e-3) / 1e12 if g_ms else None
+
+    kernels = breakdown(prof)
+    gemm_tf = gemm_rate(prof)
+    q8_gu_avg = q8_gu[0] / max(q8_gu[1], 1)
+    q8_gu_tf = (q8_gu[2] / max(q8_gu[1], 1)) / (q8_gu_avg * 1e-3) / 1e12 if q8_gu[1] else None
+    q8_gemm_tf = gemm_rate(q8prof)
+    q8 = {"ms_per_step": round(t_q8 * 1e3, 3), "tflops": round(tot_f / t_q8 / 1e12, 1),
+          "mfma_peak_frac": round(tot_f / t_q8 / 1e12 / PEAK_TFLOPS, 4),
+          "vs_resident_bf16": round(t_q8 * 1e3 / ms, 3),
+          "weights_gb": round(q8_w_bytes / 1e9, 2),
+          "gemm_tflops": round(q8_gemm_tf, 1) if q8_gemm_tf else None,
+          "gemm_peak_frac": round(q8_gemm_tf / PEAK_TFLOPS, 4) if q8_gemm_tf else None,
+          "gate_up": {"kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, Q8_0 weights dequantised in the pipeline",
+                      "achieved": round(q8_gu_tf, 1) if q8_gu_tf else None, "unit": "TFLOP/s",
+                      "frac": round(q8_gu_tf / PEAK_TFLOPS, 4) if q8_gu_tf else None,
+                      "avg_launch_ms": round(q8_gu_avg, 4), "launches_timed": q8_gu[1]},
+          "kernels": breakdown(q8prof)}
     out = {
         "metric": METRIC, "value": round(ms, 3), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "dit-euler-step-1024x1024", "image_rows": H * W, "text_rows": P, "blocks": LAYERS,
-                   "weights": "Q8_0 synthetic (7.0B block + 0.14B edge parameters)",
+                   "weights": "Q8_0 synthetic (7.0B block + 0.14B edge parameters); the block products stream "
+                              "each matrix's resident bf16 expansion bf16(fp32(d) q), 14 GB beside the 7.4 GB "
+                              "of Q8_0 (the q8_0 key: the same step from Q8_0 alone)",
                    "step": "cached: image rows over kept prompt K/V, + Euler update", "seed": SEED},
         "tflops": round(tflops, 1), "mfma_peak_frac": round(tflops / PEAK_TFLOPS, 4),
         "step_tflop": round(tot_f / 1e12, 3),
-        "gemm_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
-        "gemm_peak_frac": round(gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_TFLOPS, 4) if gemm_ms else None,
+        "gemm_tflops": round(gemm_tf, 1) if gemm_tf else None,
+        "gemm_peak_frac": round(gemm_tf / PEAK_TFLOPS, 4) if gemm_tf else None,
         "first_call_ms": round(t_first * 1e3, 2), "uncached_step_ms": round(t_uncached * 1e3, 2),
         "euler_8_steps_ms": round(t_8 * 1e3, 1),
         "host_boundary_velocity_ms": round(t_host, 3),
         "final_latent_finite": finite, "ref_rtx3090_ms_per_step": 1187.5,
         "kernels": kernels,
+        "q8_0": q8,
+        "workloads": workloads,
         "vae_decode_1024sq": {"ms": round(t_vae * 1e3, 2), "tflop": round(VAE_FLOP / 1e12, 2),
                               "tflops": round(VAE_FLOP / t_vae / 1e12, 1),
                               "mfma_peak_frac": round(VAE_FLOP / t_vae / 1e12 / PEAK_TFLOPS, 4),
