@@ -11,7 +11,7 @@ and generate's Euler loop (src/generate.lisp:112-137) calls it.  This module
 mirrors those names, argument meanings and error behaviour (a failed call
 raises ExnError carrying the library's message, as the reference signals a
 Lisp error) for hosts that are not SBCL -- the tests and the benchmark.  The
-SBCL binding is lisp/hip-dit.lisp.  There is no CPU fallback: without the
+SBCL binding is ../lisp/hip-dit.lisp.  There is no CPU fallback: without the
 built library or a GPU every entry point raises.
 """
 from __future__ import annotations

@@ -1,0 +1,90 @@
+;;;; hip-dit.lisp -- ex-nihilo's DiT backend on an AMD MI355X through libexn-hip.so
+;;;;
+;;;; The backend trio of src/cuda-dit.lisp (upload-dit :52, dit-velocity :137, dit-release :99)
+;;;; with the same signatures, so load-engine, generate, edit and decode-latent
+;;;; (src/generate.lisp:37,96,102,134) run unchanged.  Listed in ex-nihilo.asd in place of
+;;;; cuda-dit on an MI355X host:
+;;;;   (:file "hip-dit" :if-feature (:and :sbcl :linux :exn-hip))
+;;;; The C side is include/exn_hip.h; every status other than 0 becomes a Lisp error carrying
+;;;; exn_last_error().  The library adds txt_in.text_norm's 1 itself, so the vectors go as read.
+
+(in-package #:ex-nihilo)
+
+(sb-alien:load-shared-object
+ (or (uiop:getenv "EXN_HIP_LIB")
+     (namestring (asdf:system-relative-pathname "ex-nihilo" "lib/libexn-hip.so"))))
+
+(sb-alien:define-alien-routine ("exn_last_error" %exn-last-error) sb-alien:c-string)
+(sb-alien:define-alien-routine ("exn_open" %exn-open) sb-alien:int
+  (device sb-alien:int) (out sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_dit_create" %exn-dit-create) sb-alien:int
+  (ctx sb-sys:system-area-pointer) (layers sb-alien:int) (out sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_dit_set" %exn-dit-set) sb-alien:int
+  (d sb-sys:system-area-pointer) (name sb-alien:c-string) (kind sb-alien:int)
+  (data sb-sys:system-area-pointer) (d0 (sb-alien:signed 64)) (d1 (sb-alien:signed 64)))
+(sb-alien:define-alien-routine ("exn_dit_check" %exn-dit-check) sb-alien:int (d sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_dit_velocity" %exn-dit-velocity) sb-alien:int
+  (d sb-sys:system-area-pointer) (context sb-sys:system-area-pointer) (p sb-alien:int)
+  (latent sb-sys:system-area-pointer) (h sb-alien:int) (w sb-alien:int) (sigma sb-alien:double)
+  (prefix-key (sb-alien:unsigned 64)) (ref-a sb-alien:int) (ref-latent sb-sys:system-area-pointer)
+  (rh sb-alien:int) (rw sb-alien:int) (v sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_dit_release" %exn-dit-release) sb-alien:int (d sb-sys:system-area-pointer))
+
+(defconstant +exn-q8-0+ 8)
+(defconstant +exn-f32+ 0)
+(defconstant +exn-bf16+ 30)
+
+(defmacro exn-check (form)
+  `(let ((status ,form))
+     (unless (zerop status) (error "libexn-hip: ~A" (%exn-last-error)))))
+
+(defun exn-out-pointer (fn &rest args)
+  "Call FN with ARGS and a pointer cell; the cell's pointer."
+  (let ((cell (make-array 1 :element-type '(unsigned-byte 64))))
+    (sb-sys:with-pinned-objects (cell)
+      (exn-check (apply fn (append args (list (sb-sys:vector-sap cell))))))
+    (sb-sys:int-sap (aref cell 0))))
+
+(defstruct (hdit (:constructor %make-hdit)) ctx handle gguf
+  (keys (make-hash-table :test 'equal)))   ; prefix keys (EQUAL Lisp objects) -> 64-bit ids
+
+(defun upload-dit (path &key (device 0))
+  "The DiT in the GGUF at PATH on HIP device DEVICE."
+  (let* ((g (open-dit path)) (file (il::map-file-vector path))
+         (ctx (exn-out-pointer #'%exn-open device))
+         (d (%make-hdit :ctx ctx :handle (exn-out-pointer #'%exn-dit-create ctx 32) :gguf g)))
+    (dolist (name (gguf-tensor-order g))
+      (let* ((ti (gguf-tensor g name)) (short (subseq name (length +dit-prefix+)))
+             (dims (tensor-info-dims ti))
+             (src (sb-sys:sap+ (sb-sys:vector-sap file) (+ (il::gguf-data-offset g) (il::tensor-info-offset ti)))))
+        (sb-sys:with-pinned-objects (file)
+          (if (null (rest dims))
+              (let ((v (il::load-f32 g name)))          ; norm vectors as floats; the library adds text_norm's 1
+                (sb-sys:with-pinned-objects (v)
+                  (exn-check (%exn-dit-set (hdit-handle d) short +exn-f32+ (sb-sys:vector-sap v) (length v) 1))))
+              (exn-check (%exn-dit-set (hdit-handle d) short
+                                       (ecase (tensor-info-type ti) (:q8_0 +exn-q8-0+) (:f32 +exn-f32+) (:bf16 +exn-bf16+))
+                                       src (first dims) (reduce #'* (rest dims))))))))
+    (exn-check (%exn-dit-check (hdit-handle d)))
+    d))
+
+(defun dit-velocity (d context p latent h w sigma &key (prefix-key nil) ref)
+  "cuda-dit.lisp's dit-velocity on the MI355X: the same arguments, the same result."
+  (let ((v (f32vec (* 64 h w)))
+        (key (if prefix-key
+                 (or (gethash prefix-key (hdit-keys d))
+                     (setf (gethash prefix-key (hdit-keys d)) (1+ (hash-table-count (hdit-keys d)))))
+                 0))
+        (ref-latent (and ref (second ref))))
+    (sb-sys:with-pinned-objects (context latent v ref-latent)
+      (exn-check (%exn-dit-velocity (hdit-handle d) (sb-sys:vector-sap context) p (sb-sys:vector-sap latent) h w
+                                    (coerce sigma 'double-float) key
+                                    (if ref (first ref) 0)
+                                    (if ref (sb-sys:vector-sap ref-latent) (sb-sys:int-sap 0))
+                                    (if ref (third ref) 0) (if ref (fourth ref) 0)
+                                    (sb-sys:vector-sap v))))
+    v))
+
+(defun dit-release (d)
+  "D's scratch and kept prompt keys and values freed (the weights stay)."
+  (exn-check (%exn-dit-release (hdit-handle d))))

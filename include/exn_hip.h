@@ -7,7 +7,7 @@
  * il::cuda-upload, il::cuda-download, il::cuda-copy-dd, il::launch) and the
  * kernels they launch (src/cuda/dit.cu; illatio's repack_q8, quant_q8,
  * MM_Q8_MMA2, d4_mm_q8_0, g53_mm_bf16, d41_mm_f32, v_rms).  A host binds it
- * with any C FFI (sb-alien in lisp/hip-dit.lisp, ctypes in exn_hip).
+ * with any C FFI (sb-alien in ex-nihilo_amd/lisp/hip-dit.lisp, ctypes in exn_hip).
  *
  * Conventions:
  *   - Every call returns an int status, EXN_OK (0) or an EXN_E* code; the

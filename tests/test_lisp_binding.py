@@ -1,0 +1,120 @@
+"""The SBCL binding (ex-nihilo_amd/lisp/hip-dit.lisp, hip-vae.lisp) against the C ABI, without
+SBCL (neither this image nor the GPU host has it): every define-alien-routine names a function
+that include/exn_hip.h declares, with its arity and, argument by argument, a Lisp alien type
+that passes the C type (int, 64-bit integers, double, pointers, C strings); and the backend trio
+keeps the reference's lambda lists (src/cuda-dit.lisp:52,137,99; src/cuda-vae.lisp:15,94,28)."""
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LISP = os.path.join(REPO, "ex-nihilo_amd", "lisp")
+HEADER = os.path.join(REPO, "include", "exn_hip.h")
+
+
+def prototypes():
+    """name -> (return type, [parameter types]) from the header."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(int|const char\*)\s+(exn_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.M | re.S):
+        ret, name, params = m.group(1), m.group(2), " ".join(m.group(3).split())
+        types = []
+        if params and params != "void":
+            for p in params.split(","):
+                p = p.strip()
+                t = re.sub(r"\s*\b\w+$", "", p) if not p.endswith("*") else p   # drop the parameter name
+                types.append(t.replace(" *", "*").strip())
+        out[name] = (ret, types)
+    return out
+
+
+def sexprs(text):
+    """The top-level forms of a Lisp file as nested lists of atoms (strings)."""
+    # strings first (a ';' inside a docstring starts no comment), then comments, parens, atoms
+    tokens = [t for t in re.findall(r'"(?:\\.|[^"])*"|;[^\n]*|[()]|[^\s()]+', text) if not t.startswith(";")]
+    stack, top = [], []
+    for t in tokens:
+        if t == "(":
+            stack.append([])
+        elif t == ")":
+            f = stack.pop()
+            (stack[-1] if stack else top).append(f)
+        else:
+            (stack[-1] if stack else top).append(t)
+    assert not stack, "unbalanced parentheses"
+    return top
+
+
+def forms(name):
+    return sexprs(open(os.path.join(LISP, name)).read())
+
+
+def alien_routines():
+    out = {}
+    for f in ("hip-dit.lisp", "hip-vae.lisp"):
+        for form in forms(f):
+            if isinstance(form, list) and form and form[0] == "sb-alien:define-alien-routine":
+                cname = form[1][0].strip('"')
+                out[cname] = (form[2], [a[1] for a in form[3:]])
+    return out
+
+
+def passes(lisp_type, c_type):
+    """Whether the alien type carries the C type across the call."""
+    if isinstance(lisp_type, list):
+        kind, bits = lisp_type[0], int(lisp_type[1])
+        return bits == 64 and ((kind == "sb-alien:signed" and c_type == "int64_t") or
+                               (kind == "sb-alien:unsigned" and c_type in ("uint64_t", "size_t")))
+    if lisp_type == "sb-alien:int":
+        return c_type == "int"
+    if lisp_type == "sb-alien:double":
+        return c_type == "double"
+    if lisp_type == "sb-alien:float":
+        return c_type == "float"
+    if lisp_type == "sb-alien:c-string":
+        return c_type == "const char*"
+    if lisp_type == "sb-sys:system-area-pointer":
+        return c_type.endswith("*")
+    return False
+
+
+def test_every_alien_routine_matches_the_header():
+    protos = prototypes()
+    routines = alien_routines()
+    assert len(routines) >= 10
+    for cname, (ret, args) in routines.items():
+        assert cname in protos, cname
+        cret, cargs = protos[cname]
+        assert len(args) == len(cargs), (cname, args, cargs)
+        assert passes(ret, "const char*" if cret == "const char*" else "int"), (cname, ret, cret)
+        for i, (la, ca) in enumerate(zip(args, cargs)):
+            assert passes(la, ca), (cname, i, la, ca)
+
+
+def test_the_trio_keeps_the_reference_lambda_lists():
+    defs = {}
+    for f in ("hip-dit.lisp", "hip-vae.lisp"):
+        for form in forms(f):
+            if isinstance(form, list) and form and form[0] == "defun":
+                defs[form[1]] = form[2]
+    assert defs["upload-dit"] == ["path", "&key", ["device", "0"]]
+    assert defs["dit-velocity"] == ["d", "context", "p", "latent", "h", "w", "sigma", "&key", ["prefix-key", "nil"],
+                                    "ref"]
+    assert defs["dit-release"] == ["d"]
+    assert defs["upload-vae"] == ["path", "&key", ["device", "0"]]
+    assert defs["vae-decode"] == ["v", "latent", "h", "w"]
+    assert defs["vae-release"] == ["v"]
+
+
+def test_the_header_parse_sees_the_trio():
+    p = prototypes()
+    assert p["exn_dit_velocity"][1] == ["exn_dit*", "const float*", "int", "const float*", "int", "int", "double",
+                                        "uint64_t", "int", "const float*", "int", "int", "float*"]
+    assert p["exn_last_error"] == ("const char*", [])
+
+
+@pytest.mark.parametrize("name", ["hip-dit.lisp", "hip-vae.lisp"])
+def test_files_parse_and_stay_in_the_package(name):
+    fs = forms(name)
+    assert fs[0] == ["in-package", "#:ex-nihilo"]
