@@ -53,6 +53,7 @@ P = 256                       # text rows
 LAYERS = 32
 SEED = 2
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_1024sq_traffic.json")
+TRAFFIC_FILE_Q8 = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_q8_0_1024sq_traffic.json")
 PROBE_BYTES = 1 << 30         # --copy-probe 1024
 VAE_FLOP = 17.03e12           # one decode of a 64 x 64 latent: every convolution and the attention's products
 
@@ -147,10 +148,11 @@ def cpu_baseline(blocks=5):
             "host": host_info()}
 
 
-def traffic_from(fetch_db, write_db):
+def traffic_from(fetch_db, write_db, q8=False):
     """HBM bytes a launch of the gate_up product moves, from rocprofv3 --pmc FETCH_SIZE and
     WRITE_SIZE runs (KiB a dispatch) of `bench.py --copy-probe MIB`, each counter scaled by
-    what it reads for the probe's device-to-device copy of a known size."""
+    what it reads for the probe's device-to-device copy of a known size.  Q8: the product on
+    Q8_0 weights (`bench.py --q8-only --copy-probe MIB`), else on the resident bf16 ones."""
     import sqlite3
 
     def per_kernel(db, counter):
@@ -164,8 +166,8 @@ def traffic_from(fetch_db, write_db):
 
     f, w = per_kernel(fetch_db, "FETCH_SIZE"), per_kernel(write_db, "WRITE_SIZE")
     copy = [k for k in f if "copyBuffer" in k]
-    # EPI_SWIGLU on bf16 weights (the Q8_0 variant of the kernel, <3, 8, true>, runs in the q8_0 section)
-    gemm = [k for k in f if ("k_gemm_bt<3>" in k or "k_gemm_bt<3," in k) and "true" not in k]
+    # EPI_SWIGLU on bf16 weights, <3, 8, false>, or on Q8_0 ones, <3, 8, true>
+    gemm = [k for k in f if ("k_gemm_bt<3>" in k or "k_gemm_bt<3," in k) and (("true" in k) == q8)]
     if not copy or not gemm:
         sys.exit("bench.py: the databases hold no copy probe or no gate_up product")
     big = lambda v: max(v)                                   # the probe is the largest copy
@@ -174,21 +176,56 @@ def traffic_from(fetch_db, write_db):
     wf = big(w[kc]) / PROBE_BYTES
     fetch = float(np.median(f[gemm[0]])) / rf
     write = float(np.median(w[gemm[0]])) / wf
-    algo = 2 * (4096 * 4096 + 24576 * 4096 + 4096 * 12288)
-    rec = {"kernel": "%s: gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights" % gemm[0].split("(")[0].replace("void ", ""),
+    # X and Y in bf16 once; W in bf16 (2 bytes a weight) or Q8_0 (34 bytes a block of 32)
+    algo = 2 * (4096 * 4096 + 4096 * 12288) + (24576 * 4096 * 34 // 32 if q8 else 2 * 24576 * 4096)
+    run = "--q8-only " if q8 else ""
+    fd, wd = os.path.relpath(os.path.dirname(os.path.abspath(fetch_db))), os.path.relpath(os.path.dirname(os.path.abspath(write_db)))
+    rec = {"kernel": "%s: gate_up + SwiGLU, 4096 x 24576 x 4096, %s weights"
+                     % (gemm[0].split("(")[0].replace("void ", ""), "Q8_0" if q8 else "bf16"),
            "bytes_per_launch": round(fetch + write), "fetch_bytes": round(fetch), "write_bytes": round(write),
            "algorithmic_bytes": algo, "copy_probe_bytes": PROBE_BYTES,
            "fetch_factor": round(rf, 4), "write_factor": round(wf, 4),
            "launches": len(f[gemm[0]]),
-           "commands": ["rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o p -- python3 bench.py --steps 1 "
-                        "--warmup 0 --no-cpu --copy-probe %d" % (PROBE_BYTES >> 20),
-                        "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o p -- python3 bench.py --steps 1 "
-                        "--warmup 0 --no-cpu --copy-probe %d" % (PROBE_BYTES >> 20),
-                        "python3 bench.py --traffic-from gpurun_out/pmc_fetch/p_results.db "
-                        "gpurun_out/pmc_write/p_results.db"]}
-    with open(TRAFFIC_FILE, "w") as fh:
+           "commands": ["rocprofv3 --pmc FETCH_SIZE -d %s -o p -- python3 bench.py %s--steps 1 "
+                        "--warmup 0 --no-cpu --copy-probe %d" % (fd, run, PROBE_BYTES >> 20),
+                        "rocprofv3 --pmc WRITE_SIZE -d %s -o p -- python3 bench.py %s--steps 1 "
+                        "--warmup 0 --no-cpu --copy-probe %d" % (wd, run, PROBE_BYTES >> 20),
+                        "python3 bench.py %s--traffic-from %s %s" % (run, os.path.relpath(fetch_db),
+                                                                     os.path.relpath(write_db))]}
+    with open(TRAFFIC_FILE_Q8 if q8 else TRAFFIC_FILE, "w") as fh:
         json.dump(rec, fh, indent=1)
     print(json.dumps(rec))
+
+
+def pmc_summary(dbs):
+    """A markdown table from rocprofv3 --pmc databases: per kernel, its dispatches, mean duration,
+    the clock (GRBM_GUI_ACTIVE, summed over the 8 XCDs, over the duration) and the MFMA pipe's busy
+    fraction (SQ_VALU_MFMA_BUSY_CYCLES over the 1024 SIMDs' cycles), with any other counter's mean."""
+    import sqlite3
+    acc = {}
+    for db in dbs:
+        c = sqlite3.connect(db)
+        for kn, cn, v, t0, t1 in c.execute("select kernel_name, counter_name, value, start, end "
+                                          "from counters_collection"):
+            k = kn.split("(")[0].replace("void ", "")
+            d = acc.setdefault(k, {})
+            d.setdefault(cn, []).append(float(v))
+            d.setdefault("_dur", []).append((t1 - t0) / 1e3)
+    print("| kernel | dispatches | mean µs | GHz | MFMA busy | counters (mean a dispatch) |")
+    print("|---|---:|---:|---:|---:|---|")
+    for k, d in sorted(acc.items(), key=lambda kv: -sum(kv[1]["_dur"])):
+        dur = float(np.mean(d["_dur"]))
+        g = float(np.mean(d["GRBM_GUI_ACTIVE"])) if "GRBM_GUI_ACTIVE" in d else None
+        # GRBM_GUI_ACTIVE sums the 8 XCDs' cycles; it also counts the dispatch's set-up and
+        # drain, so under about 50 µs the clock and the busy fraction say little
+        g = g if g and dur >= 50 else None
+        clk = g / 8 / dur / 1e3 if g else None
+        busy = float(np.mean(d["SQ_VALU_MFMA_BUSY_CYCLES"])) / (1024 * g / 8) if g and "SQ_VALU_MFMA_BUSY_CYCLES" in d else None
+        rest = ", ".join("%s %.4g" % (cn, float(np.mean(v))) for cn, v in sorted(d.items())
+                         if cn not in ("_dur", "GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES"))
+        n = len(d["_dur"]) // max(1, len([c for c in d if c != "_dur"]))
+        print("| `%s` | %d | %.1f | %s | %s | %s |" % (k, n, dur, "%.2f" % clk if clk else "-",
+                                                      "%.3f" % busy if busy is not None else "-", rest))
 
 
 def vae_only(steps, warmup):
@@ -232,10 +269,18 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="copy MIB MiB device to device after the set-up (the traffic counters' calibration)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
-                    help="turn two rocprofv3 --pmc databases of a --copy-probe run into " + TRAFFIC_FILE)
+                    help="turn two rocprofv3 --pmc databases of a --copy-probe run into " + TRAFFIC_FILE +
+                         " (with --q8-only: of the Q8_0 product, into " + TRAFFIC_FILE_Q8 + ")")
+    ap.add_argument("--q8-only", action="store_true",
+                    help="time only the cached step from Q8_0 weights (no resident bf16 copies, no VAE)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DB",
+                    help="print per-kernel clock and MFMA busy from rocprofv3 --pmc databases")
     a = ap.parse_args()
     if a.traffic_from:
-        traffic_from(*a.traffic_from)
+        traffic_from(*a.traffic_from, q8=a.q8_only)
+        return
+    if a.pmc_summary:
+        pmc_summary(a.pmc_summary)
         return
     if a.gpus != 1:
         print("bench.py: the step runs on one GPU; --gpus %d is not supported (a split of the image rows "
@@ -253,12 +298,12 @@ def main():
     d.synth(SEED)   # synchronous: returns once the weights are made
     d.check()
     t1 = time.perf_counter()
-    d.resident(True)   # synchronous too
+    d.resident(not a.q8_only)   # synchronous too
     t2 = time.perf_counter()
     w_bytes, _ = d.memory()
-    print("bench: synthetic 7B Q8_0 DiT made on the device in %.1f ms, block matrices expanded to resident bf16 in "
-          "%.1f ms (%.1f GB of weights)" % ((t1 - t0) * 1e3, (t2 - t1) * 1e3, w_bytes / 1e9), file=sys.stderr,
-          flush=True)
+    print("bench: synthetic 7B Q8_0 DiT made on the device in %.1f ms%s (%.1f GB of weights)"
+          % ((t1 - t0) * 1e3, "" if a.q8_only else ", block matrices expanded to resident bf16 in %.1f ms"
+             % ((t2 - t1) * 1e3), w_bytes / 1e9), file=sys.stderr, flush=True)
     if a.copy_probe:
         src = X.DevBuf(ctx, (a.copy_probe << 20,), np.uint8)
         dst = X.DevBuf(ctx, (a.copy_probe << 20,), np.uint8)
@@ -278,6 +323,24 @@ def main():
         s, s2 = sig[i % 8], sig[i % 8 + 1]
         X.call("exn_dit_velocity_dev", d.h, context.h, P, z.h, H, W, s, k, 0, None, 0, 0, v.h)
         X.call("exn_euler", ctx.h, 64 * H * W, z.h, v.h, np.float32(s2 - s))
+
+    if a.q8_only:   # the cached step from Q8_0 alone, for the profiles of that path
+        for i in range(1 + a.warmup):
+            step(i, key)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for i in range(a.steps):
+            step(1 + i, key)
+        ctx.sync()
+        t = (time.perf_counter() - t0) / a.steps
+        tot = step_flops(True)[2]
+        print(json.dumps({"metric": "DiT Euler step ms @1024² from Q8_0 weights (dequantised in the products)",
+                          "value": round(t * 1e3, 3), "unit": "ms/step", "steps": a.steps, "warmup": a.warmup,
+                          "tflops": round(tot / t / 1e12, 1), "mfma_peak_frac": round(tot / t / 1e12 / PEAK_TFLOPS, 4),
+                          "weights_gb": round(w_bytes / 1e9, 2)}), flush=True)
+        d.destroy()
+        ctx.close()
+        return
 
     # the first call (the pass's workspace allocated), then an uncached step under the timed
     # key: the prompt rows too, their K/V kept (the cache holds one prefix, so the first
