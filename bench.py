@@ -148,7 +148,7 @@ def cpu_baseline(blocks=5):
             "host": host_info()}
 
 
-def traffic_from(fetch_db, write_db, q8=False):
+def traffic_from(fetch_db, write_db, q8=False, bf16_only=False):
     """HBM bytes a launch of the gate_up product moves, from rocprofv3 --pmc FETCH_SIZE and
     WRITE_SIZE runs (KiB a dispatch) of `bench.py --copy-probe MIB`, each counter scaled by
     what it reads for the probe's device-to-device copy of a known size.  Q8: the product on
@@ -178,7 +178,7 @@ def traffic_from(fetch_db, write_db, q8=False):
     write = float(np.median(w[gemm[0]])) / wf
     # X and Y in bf16 once; W in bf16 (2 bytes a weight) or Q8_0 (34 bytes a block of 32)
     algo = 2 * (4096 * 4096 + 4096 * 12288) + (24576 * 4096 * 34 // 32 if q8 else 2 * 24576 * 4096)
-    run = "--q8-only " if q8 else ""
+    run = "--q8-only " if q8 else ("--bf16-only " if bf16_only else "")
     fd, wd = os.path.relpath(os.path.dirname(os.path.abspath(fetch_db))), os.path.relpath(os.path.dirname(os.path.abspath(write_db)))
     rec = {"kernel": "%s: gate_up + SwiGLU, 4096 x 24576 x 4096, %s weights"
                      % (gemm[0].split("(")[0].replace("void ", ""), "Q8_0" if q8 else "bf16"),
@@ -228,6 +228,56 @@ def pmc_summary(dbs):
                                                       "%.3f" % busy if busy is not None else "-", rest))
 
 
+def smi_sample():
+    """Socket power (W) and the 8 XCDs' GFX clocks (MHz) from one `amd-smi metric -p -c`."""
+    import re
+    import subprocess
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-p", "-c", "-g", "0"], capture_output=True, text=True, timeout=20)
+    except (OSError, subprocess.TimeoutExpired):
+        return None, []
+    pw = re.search(r"SOCKET_POWER:\s*([\d.]+)\s*W", r.stdout)
+    clk = [int(c) for c in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*(\d+)\s*MHz", r.stdout)]
+    return (float(pw.group(1)) if pw else None), clk
+
+
+def power_run(seconds, step, ctx, z, latent, weights):
+    """The cached step looped for SECONDS (8 steps from the same latent a round) while a thread
+    samples amd-smi: the socket power and clocks the step runs at."""
+    import threading
+    idle = smi_sample()
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            samples.append((time.perf_counter(),) + smi_sample())
+            stop.wait(0.25)
+
+    th = threading.Thread(target=sampler)
+    t0 = time.perf_counter()
+    th.start()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        z.upload(latent)
+        for i in range(8):
+            step(i, 7)
+        n += 8
+        ctx.sync()
+    dt = time.perf_counter() - t0
+    stop.set()
+    th.join()
+    late = [s for s in samples if s[0] - t0 > 1.0 and s[1] is not None]   # past the first second's ramp
+    pw = [s[1] for s in late]
+    clk = [c for s in late for c in s[2]]
+    stat = lambda v: {"median": float(np.median(v)), "min": float(min(v)), "max": float(max(v))} if v else None
+    print(json.dumps({"metric": "socket power and GFX clocks during the cached 1024² step loop, 1 GPU",
+                      "weights": weights, "seconds": round(dt, 2), "steps": n,
+                      "ms_per_step": round(dt / n * 1e3, 3), "samples": len(late),
+                      "socket_power_w": stat(pw), "idle_socket_power_w": idle[0],
+                      "gfx_clock_mhz": stat(clk), "peak_clock_mhz": 2400,
+                      "source": "amd-smi metric -p -c -g 0, every 0.25 s from a thread"}), flush=True)
+
+
 def vae_only(steps, warmup):
     """The VAE decoder alone: a seeded 64 x 64 latent in HBM -> a 1024 x 1024 RGBA picture."""
     import exn_hip as X
@@ -273,11 +323,16 @@ def main():
                          " (with --q8-only: of the Q8_0 product, into " + TRAFFIC_FILE_Q8 + ")")
     ap.add_argument("--q8-only", action="store_true",
                     help="time only the cached step from Q8_0 weights (no resident bf16 copies, no VAE)")
+    ap.add_argument("--bf16-only", action="store_true",
+                    help="time only the cached step from the resident bf16 expansion (no other workloads, no VAE)")
+    ap.add_argument("--power", type=float, default=0, metavar="SECONDS",
+                    help="loop the cached step for SECONDS while sampling amd-smi's power and clocks "
+                         "(with --q8-only: from Q8_0 weights)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DB",
                     help="print per-kernel clock and MFMA busy from rocprofv3 --pmc databases")
     a = ap.parse_args()
     if a.traffic_from:
-        traffic_from(*a.traffic_from, q8=a.q8_only)
+        traffic_from(*a.traffic_from, q8=a.q8_only, bf16_only=a.bf16_only)
         return
     if a.pmc_summary:
         pmc_summary(a.pmc_summary)
@@ -324,7 +379,15 @@ def main():
         X.call("exn_dit_velocity_dev", d.h, context.h, P, z.h, H, W, s, k, 0, None, 0, 0, v.h)
         X.call("exn_euler", ctx.h, 64 * H * W, z.h, v.h, np.float32(s2 - s))
 
-    if a.q8_only:   # the cached step from Q8_0 alone, for the profiles of that path
+    if a.power:
+        for i in range(1 + a.warmup):
+            step(i, key)
+        ctx.sync()
+        power_run(a.power, step, ctx, z, latent, "Q8_0" if a.q8_only else "resident bf16 expansion")
+        d.destroy()
+        ctx.close()
+        return
+    if a.q8_only or a.bf16_only:   # the cached step alone, for the profiles of one weight path
         for i in range(1 + a.warmup):
             step(i, key)
         ctx.sync()
@@ -334,7 +397,8 @@ def main():
         ctx.sync()
         t = (time.perf_counter() - t0) / a.steps
         tot = step_flops(True)[2]
-        print(json.dumps({"metric": "DiT Euler step ms @1024² from Q8_0 weights (dequantised in the products)",
+        print(json.dumps({"metric": "DiT Euler step ms @1024² from " + ("Q8_0 weights (dequantised in the products)"
+                                                                   if a.q8_only else "the resident bf16 expansion"),
                           "value": round(t * 1e3, 3), "unit": "ms/step", "steps": a.steps, "warmup": a.warmup,
                           "tflops": round(tot / t / 1e12, 1), "mfma_peak_frac": round(tot / t / 1e12 / PEAK_TFLOPS, 4),
                           "weights_gb": round(w_bytes / 1e9, 2)}), flush=True)

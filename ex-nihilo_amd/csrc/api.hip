@@ -5,6 +5,7 @@
 #include "../../include/exn_hip.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -1642,7 +1643,7 @@ int exn_dit_generate_dev(exn_dit* d, const float* context, int p, float* z, int 
   if (!d) FAIL(EXN_EINVAL, "null model");
   TRY(use(d->ctx));
   if (!z || !sigmas || nsig < 2) FAIL(EXN_EINVAL, "generate: %d sigmas", nsig);
-  static uint64_t counter = 0;
+  static std::atomic<uint64_t> counter{0};
   const uint64_t key = 0x6765000000000000ull + (++counter);  // a fresh key, as edit's (:edit k) is
   const int64_t count = (int64_t)h * w * EXN_LAT;
   float* v = nullptr;

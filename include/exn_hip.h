@@ -194,7 +194,8 @@ int exn_dit_velocity(exn_dit* d, const float* context, int p, const float* laten
 int exn_dit_velocity_dev(exn_dit* d, const float* context, int p, const float* latent, int h, int w, double sigma,
                          uint64_t prefix_key, int ref_a, const float* ref_latent, int rh, int rw, float* v);
 /* generate's loop (src/generate.lisp:133-135) on the device: Z (device, 64 x H x W) through
- * the NSIG - 1 Euler steps of SIGMAS, the prompt's K/V kept under PREFIX_KEY (0: a fresh key) */
+ * the NSIG - 1 Euler steps of SIGMAS; the prompt's K/V are made at the first step under a key
+ * of the loop's own and kept for the rest */
 int exn_dit_generate_dev(exn_dit* d, const float* context, int p, float* z, int h, int w, const double* sigmas,
                          int nsig, int ref_a, const float* ref_latent, int rh, int rw);
 /* *dit-trace* (src/metal-dit.lisp:114-124), as a copy: while BUF (device, fp32) is set,

@@ -379,3 +379,52 @@ def test_cfg2_eight_steps_full_depth(ctx):
     say("cfg2: step-0 velocity rel-L2 %.2e, final latent rel-L2 %.2e" % (e0, ez))
     assert e0 < 1e-2 and ez < 2e-2
     d.destroy()
+
+
+WORKLOADS = {  # name: (seed, text rows, image h, w, reference picture (a, rh, rw) or None)
+    "cfg3_1536x1024": (6, 256, 96, 64, None),
+    "cfg4_edit_1024sq": (7, 512, 64, 64, (8, 64, 64)),
+}
+
+
+@pytest.mark.parametrize("case", list(WORKLOADS))
+def test_workloads_eight_steps_full_depth(ctx, case):
+    """The 1536 x 1024 workload (6144 image rows over 256 text rows) and the edit workload
+    (512 text rows with a 64 x 64 reference picture after the first 8, then a 64 x 64 image:
+    8704 keys) end to end, 32 blocks: the first step uncached and again on the kept prefix K/V
+    (one velocity, <= 1e-5); the 8 Turbo steps of the host loop (exn_dit_velocity and the
+    Euler update in numpy) and of the device loop (exn_dit_generate_dev) give one latent
+    (<= 1e-5), every value finite."""
+    seed, p, h, w, ref = WORKLOADS[case]
+    say(case, "32 blocks, p", p, "image", h, "x", w, "ref", ref, "8 steps")
+    d = model(ctx, 32, seed)
+    if ref is None:
+        ctxa, lat = xo.synth_inputs(seed, p, h, w)
+        refarg, rl = None, None
+    else:
+        a, rh, rw = ref
+        ctxa, lat, rl = xo.synth_inputs(seed, p, h, w, ref_hw=(rh, rw))
+        refarg = (a, rl, rh, rw)
+    sig = xo.TURBO_SIGMAS
+    v0 = X.dit_velocity(d, ctxa, p, lat, h, w, sig[0], prefix_key="k", ref=refarg)
+    v0c = X.dit_velocity(d, ctxa, p, lat, h, w, sig[0], prefix_key="k", ref=refarg)
+    e01 = xo.rel_l2(v0c, v0)
+    say("%s: step 0 cached vs uncached rel-L2 %.2e" % (case, e01))
+    assert np.isfinite(v0).all() and e01 < 1e-5
+    z = lat.copy()
+    for i, (s, s2) in enumerate(zip(sig[:-1], sig[1:])):
+        v = v0c if i == 0 else X.dit_velocity(d, ctxa, p, z, h, w, s, prefix_key="k", ref=refarg)
+        assert np.isfinite(v).all()
+        z = z + np.float32(s2 - s) * v
+    zd, cd = X.DevBuf.of(ctx, lat), X.DevBuf.of(ctx, ctxa)
+    rd = X.DevBuf.of(ctx, rl) if rl is not None else None
+    sg = np.array(sig, np.float64)
+    if ref is None:
+        X.call("exn_dit_generate_dev", d.h, cd.h, p, zd.h, h, w, X.ptr(sg), len(sg), 0, None, 0, 0)
+    else:
+        X.call("exn_dit_generate_dev", d.h, cd.h, p, zd.h, h, w, X.ptr(sg), len(sg), ref[0], rd.h, ref[1], ref[2])
+    zg = zd.get()
+    ez = xo.rel_l2(zg, z)
+    say("%s: final latent, device loop vs host loop rel-L2 %.2e, |z| %.4f" % (case, ez, float(np.sqrt((z * z).mean()))))
+    assert np.isfinite(zg).all() and ez < 1e-5
+    d.destroy()
