@@ -2,19 +2,20 @@
 //
 // X: bf16 rows (M x K, lda apart).  W: Q8_0 as SoA -- qs (N x K int8, a row's
 // K/32 blocks of 32 contiguous) and d (N x K/32 fp16) -- or plain bf16 (N x K).
-// The Q8_0 tile is dequantised on its way into LDS: each thread takes one
-// 32-value block, converts fp32(d) * q (exact) to bf16 (round to nearest
-// even) and stores 64 bytes; the MFMAs then read X and W tiles alike.
+// A Q8_0 weight enters the MFMAs as bf16(fp32(d) * q): the product of an fp16
+// and an int8 is exact in fp32 and is rounded once, to nearest even.
 // This replaces the reference's mm dispatch (src/cuda-dit.lisp:115-130) and
 // illatio's Q8_0 products behind it; the epilogues fuse the reference's
 // x_gate_add (src/cuda/dit.cu:34-41), x_swiglu2 (:186-192) and x_gelu_tanh
 // (:194-199) into the product's store.
 //
-// The Q8_0 kernel (k_gemm): BM x BN per workgroup, BK = 64 (two Q8_0 blocks)
-// per step, waves of WM x WN, each a grid of 32x32 accumulators
-// (v_mfma_f32_32x32x16_bf16); LDS is double-buffered, the next step's global
-// loads are in registers while the current step's MFMAs run.  The kernel on
-// resident bf16 weights (k_gemm_bt, below) is the one the step uses.
+// k_gemm_bt (below) is the block products' kernel, on bf16 rows or on Q8_0
+// dequantised inside its LDS-DMA pipeline.  k_gemm is the fallback for shapes
+// and alignments that pipeline does not take: BM x BN per workgroup, BK = 64
+// (two Q8_0 blocks) per step, waves of WM x WN, each a grid of 32x32
+// accumulators (v_mfma_f32_32x32x16_bf16); LDS is double-buffered, the next
+// step's global loads are in registers while the current step's MFMAs run,
+// and each thread dequantises one 32-value block on its way into LDS.
 #include "exn_common.h"
 
 #include <type_traits>
@@ -236,8 +237,8 @@ static hipError_t dispatch(hipStream_t s, const uint16_t* x, int64_t lda, const 
     case EPI_SWIGLU: return launch<256, 256, 128, 64, WBF16, EPI_SWIGLU>(s, x, lda, qs, d, wb, M, N, K, ea);
     case EPI_GELU_BF16: return launch<256, 256, 128, 64, WBF16, EPI_GELU_BF16>(s, x, lda, qs, d, wb, M, N, K, ea);
     case EPI_F16: return launch<256, 256, 128, 64, WBF16, EPI_F16>(s, x, lda, qs, d, wb, M, N, K, ea);
+    default: return hipErrorInvalidValue;   // the fused QKV and split sums run on k_gemm_bt only
   }
-  return hipErrorInvalidValue;
 }
 
 // --- bf16 weights: the pipelined kernel ----------------------------------------------
@@ -537,10 +538,9 @@ __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_
 // 2 x 64 KB of bf16 stages + 2 x 16 KB of codes = 160 KB), each thread's fp16 scale by a 2-byte
 // buffer load into a register, and once a k-step the 512 threads turn one raw stage into the
 // bf16 W stage the MFMAs read: thread t takes tile row t/2, Q8_0 block t%2 -- 32 codes, two
-// 16-byte LDS reads -- and writes bf16(fp32(d) q) as four swizzled 16-byte rows.  The value is
-// fma(u, d, -128 d) with u = q + 128 the code's unsigned byte (v_cvt_f32_ubyte): u d - 128 d is
-// q d exactly (q d has at most 19 significant bits), rounded once, so the operand is the exact
-// dequantisation rounded to bf16, bit for bit the resident expansion's value for any finite d.
+// 16-byte LDS reads -- and writes bf16(fp32(d) q) as four swizzled 16-byte rows: a signed byte
+// conversion and one multiply a value (q d has at most 18 significant bits, exact in fp32),
+// rounded once, so the operand is bit for bit the resident expansion's value.
 template <int EPI, int NW, bool Q8>
 __global__ void __launch_bounds__(NW * 64)
 k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB,
@@ -554,7 +554,7 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // DMA instructions a k-step: X and W rounds (bf16), or X rounds only (Q8: the codes go apart)
   constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = Q8 ? ROUNDS : 2 * ROUNDS;
   // Q8: the codes' DMA (16 KB: 2 rounds of 8 waves x 1 KB) and the scale load, a k-step
-  constexpr int NRAW = 2, NQ = NRAW + 1;
+  constexpr int NRAW = 2;
   // 2 stages x (X tile 32 KB | W tile 32 KB), then (Q8) 2 raw code stages x 16 KB
   extern __shared__ __align__(1024) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -619,15 +619,12 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // half dq_blk of DPAIR; parts 0 and 5 read 16 codes each, parts 1..4 and 6..9 convert one
   // 4-code word each and store its 8 bytes of bf16
   u32x4 dq_q;
-  float dq_d = 0.f, dq_nd = 0.f;
+  float dq_d = 0.f;
   auto dequant = [&](int part, int rs, int ws, uint32_t dpair) {
     const uint8_t* src = smem + 131072 + rs * 16384 + tid * 32;
     if (part == 0 || part == 5) {
       dq_q = *(const u32x4*)(src + (part == 5 ? 16 : 0));
-      if (part == 0) {
-        dq_d = f16_to_f32((dpair >> (16 * dq_blk)) & 0xFFFFu);
-        dq_nd = -128.f * dq_d;
-      }
+      if (part == 0) dq_d = f16_to_f32((dpair >> (16 * dq_blk)) & 0xFFFFu);
       return;
     }
     const int j = part < 5 ? part - 1 : part - 2;
