@@ -42,13 +42,10 @@ __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u 
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
 
-// fp16 bits -> fp32, exact (subnormals included), without relying on the f16 denormal mode;
-// selects, not branches, so that it can sit in a pipelined loop
+// fp16 bits (the low 16 of H) -> fp32 by v_cvt_f32_f16: exact, subnormals included (the
+// kernels run in the default mode, which keeps fp16 denormals); one instruction, no branch
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
-  const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
-  const float sub = __uint_as_float(sign | __float_as_uint((float)m * 5.9604644775390625e-08f));   // m * 2^-24
-  const uint32_t big = sign | (e == 31u ? 0x7F800000u : (e + 112u) << 23) | (m << 13);
-  return e == 0u ? sub : __uint_as_float(big);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
