@@ -20,6 +20,9 @@ host for blocks 0..4 of the same cached workload, their mean x 32 blocks
 (extrapolated); beside it the single-block workload (1024 image + 64 text rows,
 uncached) as the median of 3, and the host's CPU model, cores and BLAS.
 
+w8a8: the same cached step in the reference's default int8 mode (exn_dit_w8a8:
+activations quantised to Q8_0 by blocks of 32, int8 products), with its breakdown.
+
 q8_0: the same cached step with the block matrices multiplied from Q8_0, the
 codes dequantised inside the products (no resident bf16 copy), with its gate_up
 roofline.  cfg3_1536x1024 / cfg4_edit: cached and uncached steps of the
@@ -323,6 +326,8 @@ def main():
                          " (with --q8-only: of the Q8_0 product, into " + TRAFFIC_FILE_Q8 + ")")
     ap.add_argument("--q8-only", action="store_true",
                     help="time only the cached step from Q8_0 weights (no resident bf16 copies, no VAE)")
+    ap.add_argument("--w8a8-only", action="store_true",
+                    help="time only the cached step in the reference's int8 mode (exn_dit_w8a8)")
     ap.add_argument("--bf16-only", action="store_true",
                     help="time only the cached step from the resident bf16 expansion (no other workloads, no VAE)")
     ap.add_argument("--power", type=float, default=0, metavar="SECONDS",
@@ -387,7 +392,9 @@ def main():
         d.destroy()
         ctx.close()
         return
-    if a.q8_only or a.bf16_only:   # the cached step alone, for the profiles of one weight path
+    if a.w8a8_only:
+        d.w8a8(True)
+    if a.q8_only or a.bf16_only or a.w8a8_only:   # the cached step alone, for the profiles of one path
         for i in range(1 + a.warmup):
             step(i, key)
         ctx.sync()
@@ -397,8 +404,9 @@ def main():
         ctx.sync()
         t = (time.perf_counter() - t0) / a.steps
         tot = step_flops(True)[2]
-        print(json.dumps({"metric": "DiT Euler step ms @1024² from " + ("Q8_0 weights (dequantised in the products)"
-                                                                   if a.q8_only else "the resident bf16 expansion"),
+        what = ("Q8_0 weights (dequantised in the products)" if a.q8_only else
+                "the reference's int8 products (exn_dit_w8a8)" if a.w8a8_only else "the resident bf16 expansion")
+        print(json.dumps({"metric": "DiT Euler step ms @1024² from " + what,
                           "value": round(t * 1e3, 3), "unit": "ms/step", "steps": a.steps, "warmup": a.warmup,
                           "tflops": round(tot / t / 1e12, 1), "mfma_peak_frac": round(tot / t / 1e12 / PEAK_TFLOPS, 4),
                           "weights_gb": round(w_bytes / 1e9, 2)}), flush=True)
@@ -554,6 +562,26 @@ def main():
     d.profile(False)
     q8prof = d.profile_read()
 
+    # the reference's default *int8* products (exn_dit_w8a8), on the same Q8_0 weights: the
+    # activations quantised to Q8_0 by blocks of 32 and multiplied on the int8 MFMA (the mode's
+    # change drops the kept K/V, so the first step recomputes them)
+    d.w8a8(True)
+    for i in range(2):
+        step(1 + i, key)
+    ctx.sync()
+    n8 = max(2, a.steps // 2)
+    t0 = time.perf_counter()
+    for i in range(n8):
+        step(1 + i, key)
+    ctx.sync()
+    t_i8 = (time.perf_counter() - t0) / n8
+    d.profile(True, every=1)
+    step(1, key)
+    ctx.sync()
+    d.profile(False)
+    i8prof = d.profile_read()
+    d.w8a8(False)
+
     gemm_f, att_f, tot_f = step_flops(True)
     tflops = tot_f / (ms * 1e-3) / 1e12
     gu_ms, gu_n, gu_f, gu_b = gu_timed
@@ -562,8 +590,8 @@ def main():
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         traffic = json.load(open(TRAFFIC_FILE)).get("bytes_per_launch")
-    def breakdown(pr):
-        return {c: {"ms_per_step": round(pr[c][0] / BREAKDOWN, 3), "launches_per_step": pr[c][1] // BREAKDOWN,
+    def breakdown(pr, steps=BREAKDOWN):
+        return {c: {"ms_per_step": round(pr[c][0] / steps, 3), "launches_per_step": pr[c][1] // steps,
                     **({"tflops": round(pr[c][2] / (pr[c][0] * 1e-3) / 1e12, 1)} if pr[c][2] else {}),
                     **({"gbs": round(pr[c][3] / (pr[c][0] * 1e-3) / 1e9, 1)} if pr[c][3] and not pr[c][2] else {})}
                 for c in X.Dit.PROFILE_CLASSES if pr[c][1]}
@@ -589,6 +617,13 @@ def main():
                       "frac": round(q8_gu_tf / PEAK_TFLOPS, 4) if q8_gu_tf else None,
                       "avg_launch_ms": round(q8_gu_avg, 4), "launches_timed": q8_gu[1]},
           "kernels": breakdown(q8prof)}
+    i8_gemm_tf = gemm_rate(i8prof)
+    w8a8 = {"ms_per_step": round(t_i8 * 1e3, 3), "tflops": round(tot_f / t_i8 / 1e12, 1),
+            "vs_resident_bf16": round(t_i8 * 1e3 / ms, 3),
+            "gemm_tops": round(i8_gemm_tf, 1) if i8_gemm_tf else None,
+            "note": "the reference's default *int8* products: activations quantised to Q8_0 by blocks of 32, "
+                    "int8 MFMA with an fp32 rescale a block (VALU-bound on gfx950)",
+            "kernels": breakdown(i8prof, 1)}
     out = {
         "metric": METRIC, "value": round(ms, 3), "unit": "ms/step", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak",
@@ -608,6 +643,7 @@ def main():
         "final_latent_finite": finite, "ref_rtx3090_ms_per_step": 1187.5,
         "kernels": kernels,
         "q8_0": q8,
+        "w8a8": w8a8,
         "workloads": workloads,
         "vae_decode_1024sq": {"ms": round(t_vae * 1e3, 2), "tflop": round(VAE_FLOP / 1e12, 2),
                               "tflops": round(VAE_FLOP / t_vae / 1e12, 1),

@@ -736,6 +736,22 @@ int exn_attend(exn_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_
   return EXN_OK;
 }
 
+int exn_quant_q8(exn_ctx* ctx, const void* x, int xdt, int64_t ldx, int64_t n, int64_t k, int8_t* q, uint16_t* d) {
+  TRY(use(ctx));
+  if (!x || !q || !d || n < 0 || k <= 0 || k % 32 || ldx < k || (xdt != EXN_DT_F32 && xdt != EXN_DT_BF16))
+    FAIL(EXN_EINVAL, "quant_q8: n %lld, k %lld, ldx %lld, dtype %d", (long long)n, (long long)k, (long long)ldx, xdt);
+  HIPCHK(quant_q8(ctx->stream, x, xdt == EXN_DT_BF16, ldx, n, k, q, d));
+  return EXN_OK;
+}
+
+int exn_mm_w8a8(exn_ctx* ctx, const exn_w* w, const int8_t* xq, const uint16_t* xd, int64_t n, void* y, int ydt) {
+  TRY(use(ctx));
+  if (!w || w->kind != EXN_Q8_0 || w->dense || !w->qs) FAIL(EXN_EINVAL, "mm_w8a8: the matrix is not Q8_0");
+  if (!xq || !xd || !y || n < 0 || (ydt != EXN_DT_F32 && ydt != EXN_DT_F16)) FAIL(EXN_EINVAL, "mm_w8a8 arguments");
+  HIPCHK(gemm_w8a8(ctx->stream, xq, xd, n, w->qs, w->d, w->rows, w->cols, y, w->rows, ydt == EXN_DT_F16));
+  return EXN_OK;
+}
+
 int exn_euler(exn_ctx* ctx, int64_t count, float* z, const float* v, float ds) {
   TRY(use(ctx));
   if (count < 0 || !z || !v) FAIL(EXN_EINVAL, "euler arguments");
@@ -807,6 +823,7 @@ struct exn_dit {
   std::vector<Layer> L;
   int32_t* pair_map = nullptr;  // device row map of the gate_up interleave
   bool bf16 = true;             // block matrices run from resident bf16 expansions (exn_dit_resident)
+  bool int8 = false;            // the reference's *int8* products (exn_dit_w8a8)
   // scratch
   std::map<std::string, Buf> bufs;
   // kept prompt K/V: per layer K [32][lcap][128] and V^T [32][128][lcap], bf16
@@ -1272,6 +1289,13 @@ int exn_dit_resident(exn_dit* d, int bf16) {
   return EXN_OK;
 }
 
+int exn_dit_w8a8(exn_dit* d, int on) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  if (d->int8 != (on != 0)) d->kept = false;   // other products: K/V recomputed
+  d->int8 = on != 0;
+  return EXN_OK;
+}
+
 int exn_dit_check(exn_dit* d) {
   if (!d) FAIL(EXN_EINVAL, "null model");
   std::string missing;
@@ -1453,9 +1477,27 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   const int64_t epart_cap = 8 * std::max<int64_t>(nimg, 256) * EXN_LAT;
   TRY(dit_buf(d, "epart", (size_t)epart_cap * 4, (void**)&epart));
 
+  // the int8 mode (exn_dit_w8a8) takes a Q8_0 matrix's products of at least 16 rows the
+  // reference's int8 way (src/cuda-dit.lisp:119-124): the fp32 activations quantised to Q8_0
+  // (xq, xd), then the int8 product with per-block scales
+  auto int8_ok = [&](const exn_w* W, int64_t m) {
+    return d->int8 && W && W->kind == EXN_Q8_0 && !W->dense && W->qs && m >= 16;
+  };
+  int8_t* xq = nullptr;
+  uint16_t* xd = nullptr;
+  if (d->int8) {
+    TRY(dit_buf(d, "i8q", (size_t)(std::max<int64_t>(l, 256) * EXN_F), (void**)&xq));
+    TRY(dit_buf(d, "i8d", (size_t)(std::max<int64_t>(l, 256) * (EXN_F / 32)) * 2, (void**)&xd));
+  }
   // an edge product in fp32: Y (m rows, ldy apart) = X (m rows of the matrix's inputs) W^T
   auto edge_mm = [&](int e, const float* xin, int64_t m, float* yout, int gelu) {
     const exn_w* W = d->edge[e];
+    if (int8_ok(W, m)) {
+      hipError_t r = quant_q8(s, xin, 0, W->cols, m, W->cols, xq, xd);
+      if (r == hipSuccess) r = gemm_w8a8(s, xq, xd, m, W->qs, W->d, W->rows, W->cols, yout, W->rows, 0);
+      if (r == hipSuccess && gelu) r = gelu_tanh(s, m * W->rows, yout);
+      return r;
+    }
     return gemm_f32(s, xin, W->cols, W->qs, W->d, W->wb, W->wf, m, W->rows, W->cols, yout, W->rows, gelu, epart,
                     epart_cap);
   };
@@ -1508,8 +1550,63 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   const double ln_bytes = nd * Wd * (4 + 2), qkv_bytes = nd * 3 * Wd * 2 * 2 + nd * 128 * 4;
   if (d->trace && n * EXN_W <= d->trace_cap)
     HIPCHK(hipMemcpyAsync(d->trace, x, (size_t)(n * EXN_W) * 4, hipMemcpyDeviceToDevice, s));
+  float *a32 = nullptr, *h32 = nullptr, *gu32 = nullptr, *ff32 = nullptr;   // the int8 block's fp32 rows
   for (int il = 0; il < d->layers; ++il) {
     Layer& L = d->L[(size_t)il];
+    if (int8_ok(L.qkv, n) && int8_ok(L.out, n) && int8_ok(L.gate_up, n) && int8_ok(L.down, n) && L.gate_up->pairs) {
+      // the reference's *int8* block (src/cuda-dit.lisp:196-231 with mm at :119-124): each
+      // product's fp32 input quantised, the int8 product to fp32 (QKV: fp16 rows for qkv_prep),
+      // and the elementwise steps apart, as the reference runs them
+      if (!a32) {
+        TRY(dit_buf(d, "a32", (size_t)(l * EXN_W) * 4, (void**)&a32));
+        TRY(dit_buf(d, "h32", (size_t)(l * EXN_W) * 4, (void**)&h32));
+        TRY(dit_buf(d, "gu32", (size_t)(l * 2 * EXN_F) * 4, (void**)&gu32));
+        TRY(dit_buf(d, "ff32", (size_t)(l * EXN_F) * 4, (void**)&ff32));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_LN_MOD, 0, nd * Wd * 8);
+        HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 0 * EXN_W, a32, 0));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 5 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
+        HIPCHK(quant_q8(s, a32, 0, EXN_W, n, EXN_W, xq, xd));
+        HIPCHK(gemm_w8a8(s, xq, xd, n, L.qkv->qs, L.qkv->d, 3 * EXN_W, EXN_W, qkv, 3 * EXN_W, 1));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_QKV_PREP, 0, qkv_bytes);
+        HIPCHK(qkv_prep(s, qkv, n, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap, n));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_ATTEND, 4.0 * EXN_HD * EXN_H * pairs, nd * Wd * 2 * 3 + 2.0 * l * Wd * 2);
+        HIPCHK(attend(s, q, d->kc[(size_t)il], d->vt[(size_t)il], a32, (int)n, n0, p, (int)l, d->lcap, b0, b1, 1.f, 1));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_OUT, 2 * nd * Wd * Wd, nd * Wd * 5 + Wd * Wd * 1.0625 + nd * Wd * 4 * 4);
+        HIPCHK(quant_q8(s, a32, 0, EXN_W, n, EXN_W, xq, xd));
+        HIPCHK(gemm_w8a8(s, xq, xd, n, L.out->qs, L.out->d, EXN_W, EXN_W, h32, EXN_W, 0));
+        HIPCHK(gate_add(s, n * EXN_W, EXN_W, n0, p, ms, x, h32, mod + 1 * EXN_W));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_LN_MOD, 0, nd * Wd * 8);
+        HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 2 * EXN_W, a32, 0));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_GATE_UP, 2 * nd * Wd * 2 * Fd, nd * Wd * 5 + 2 * Fd * Wd * 1.0625 + nd * Fd * 16);
+        HIPCHK(quant_q8(s, a32, 0, EXN_W, n, EXN_W, xq, xd));
+        HIPCHK(gemm_w8a8(s, xq, xd, n, L.gate_up->qs, L.gate_up->d, 2 * EXN_F, EXN_W, gu32, 2 * EXN_F, 0));
+        HIPCHK(swiglu_pairs(s, n, EXN_F, gu32, ff32));
+      }
+      {
+        ProfScope ps(d, EXN_PROF_DOWN, 2 * nd * Fd * Wd, nd * Fd * 5 + Fd * Wd * 1.0625 + nd * Wd * 4 * 4);
+        HIPCHK(quant_q8(s, ff32, 0, EXN_F, n, EXN_F, xq, xd));
+        HIPCHK(gemm_w8a8(s, xq, xd, n, L.down->qs, L.down->d, EXN_W, EXN_F, h32, EXN_W, 0));
+        HIPCHK(gate_add(s, n * EXN_W, EXN_W, n0, p, ms, x, h32, mod + 3 * EXN_W));
+      }
+      if (d->trace && (int64_t)(il + 2) * n * EXN_W <= d->trace_cap)
+        HIPCHK(hipMemcpyAsync(d->trace + (int64_t)(il + 1) * n * EXN_W, x, (size_t)(n * EXN_W) * 4,
+                              hipMemcpyDeviceToDevice, s));
+      continue;
+    }
     {
       ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes);
       HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 0 * EXN_W, y, 1));

@@ -13,7 +13,8 @@
 // Layouts: Q [32 heads][n][128] (query t = sequence row q0 + t), pre-scaled
 // so that scores come out in log2 units; K [32][lcap][128]; V^T [32][128][lcap]
 // with the keys of every aligned group of 16 stored in the order of
-// vt_pos() below; all fp16.  out [n][4096] bf16 (the next product's input).
+// vt_pos() below; all fp16.  out [n][4096] bf16 (the next product's input), or fp32 (the
+// int8 mode quantises it).
 //
 // The products are taken transposed so that no register shuffles are needed:
 // S^T = K Q^T puts one query in a lane's column (its 32 of a 64-key tile's
@@ -65,10 +66,11 @@ __device__ __forceinline__ float xsum32(float v) {
   return a + b;
 }
 
-// grid (ceil(n/128), 32 heads), block 256
+// grid (ceil(n/128), 32 heads), block 256; O bf16, or fp32 when OF32
+template <bool OF32>
 __global__ void __launch_bounds__(256, 2)
 k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vt,
-         uint16_t* __restrict__ O, int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
+         void* __restrict__ O, int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
   // Two rings, one tile apart: K stage s (64 keys x 256 B) at s * 16 KB, V^T stage s (128 dims x
   // 128 B) at 32 KB + s * 16 KB.  Step t reads K of tile t+1 and V^T of tile t, so the DMA of K
   // t+2 and V^T t+1 go into the stages step t-1 read.
@@ -299,26 +301,33 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 
   const float inv = 1.f / xsum32(lrun);
   if (tq < n) {
-    uint16_t* orow = O + (int64_t)tq * 4096 + h * 128 + 4 * hi;
+    const int64_t o0 = (int64_t)tq * 4096 + h * 128 + 4 * hi;
 #pragma unroll
     for (int d = 0; d < 4; ++d)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int dim = 32 * d + 8 * r4;
-        *(u32x2*)(orow + dim) = u32x2{pack_bf16x2(o[d][4 * r4] * inv, o[d][4 * r4 + 1] * inv),
-                                      pack_bf16x2(o[d][4 * r4 + 2] * inv, o[d][4 * r4 + 3] * inv)};
+        if constexpr (OF32)
+          *(f32x4*)((float*)O + o0 + dim) = f32x4{o[d][4 * r4] * inv, o[d][4 * r4 + 1] * inv, o[d][4 * r4 + 2] * inv,
+                                                  o[d][4 * r4 + 3] * inv};
+        else
+          *(u32x2*)((uint16_t*)O + o0 + dim) = u32x2{pack_bf16x2(o[d][4 * r4] * inv, o[d][4 * r4 + 1] * inv),
+                                                     pack_bf16x2(o[d][4 * r4 + 2] * inv, o[d][4 * r4 + 3] * inv)};
       }
   }
 }
 
-hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out, int n,
-                  int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
+hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, void* out, int n,
+                  int q0, int p, int l, int64_t lcap, int b0, int b1, float scale, int of32) {
   if (n <= 0) return hipSuccess;
   // the DMA reads whole 64-key tiles: keys up to roundup(l, 64) - 1 must lie inside lcap
   // and a head's K (or V^T) is one buffer of lcap * 256 bytes
   if (lcap % AK || l > lcap || l <= 0 || lcap > (1 << 22)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attend, dim3((unsigned)((n + AQ - 1) / AQ), 32), dim3(256), 0, s, q, k, vt, out, n, q0, p, l,
-                     lcap, b0, b1, scale);
+  const dim3 grid((unsigned)((n + AQ - 1) / AQ), 32);
+  if (of32)
+    hipLaunchKernelGGL(k_attend<true>, grid, dim3(256), 0, s, q, k, vt, out, n, q0, p, l, lcap, b0, b1, scale);
+  else
+    hipLaunchKernelGGL(k_attend<false>, grid, dim3(256), 0, s, q, k, vt, out, n, q0, p, l, lcap, b0, b1, scale);
   return hipGetLastError();
 }
 

@@ -6,7 +6,8 @@
 //   rms_norm    x / rms(x) * w (txt_in's text_norm, w = 1 + weight) -- illatio's
 //               v_rms at src/cuda-dit.lisp:176
 //   gate_add    x += tanh(gate[row]) * h -- src/cuda/dit.cu:34-41
-//   swiglu      silu(gu[:, :F]) * gu[:, F:] -- src/cuda/dit.cu:186-192
+//   swiglu      silu(gu[:, :F]) * gu[:, F:] -- src/cuda/dit.cu:186-192 (and swiglu_pairs:
+//               fp32, on gate and up columns interleaved by 32)
 //   gelu_tanh   src/cuda/dit.cu:194-199;  silu  src/cuda/dit.cu:201-206
 //   qkv_prep    per head: RMSNorm * w, then the interleaved RoPE (src/cuda/dit.cu:
 //               43-58) of q and k, and v transposed, into the attention's layouts
@@ -151,6 +152,27 @@ hipError_t swiglu(hipStream_t s, int64_t n, int f, const uint16_t* gu, uint16_t*
   if (f % 8) return hipErrorInvalidValue;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(k_swiglu, dim3(grid_of(n * f / 8, 256)), dim3(256), 0, s, n * f / 8, f, gu, out);
+  return hipGetLastError();
+}
+
+// x_swiglu2 in fp32 on a gate_up product whose columns hold gate and up interleaved by 32 (the
+// device order of the paired gate_up rows): out [n][f] = silu(gate) * up, 4 columns a thread
+__global__ void k_swiglu_pairs(int64_t count4, int f, const float* __restrict__ gu, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count4) return;
+  const int64_t e = 4 * i, t = e / f, c = e % f;
+  const float* r = gu + t * 2 * f + 64 * (c >> 5) + (c & 31);   // gate of column c; up 32 on
+  const f32x4 g = *(const f32x4*)r, u = *(const f32x4*)(r + 32);
+  f32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = silu_f(g[k]) * u[k];
+  *(f32x4*)(out + e) = o;
+}
+
+hipError_t swiglu_pairs(hipStream_t s, int64_t n, int f, const float* gu, float* out) {
+  if (f % 32) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_swiglu_pairs, dim3(grid_of(n * f / 4, 256)), dim3(256), 0, s, n * f / 4, f, gu, out);
   return hipGetLastError();
 }
 

@@ -12,6 +12,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t int32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -217,6 +218,7 @@ hipError_t rms_norm(hipStream_t s, int n, int width, float eps, const float* x, 
 hipError_t gate_add(hipStream_t s, int64_t count, int width, int n0, int p, int mstride, float* x, const float* h,
                     const float* gate);
 hipError_t swiglu(hipStream_t s, int64_t n, int f, const uint16_t* gu, uint16_t* out);
+hipError_t swiglu_pairs(hipStream_t s, int64_t n, int f, const float* gu, float* out);
 hipError_t gelu_tanh(hipStream_t s, int64_t count, float* x);
 hipError_t silu(hipStream_t s, int64_t count, float* x);
 hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk,
@@ -225,8 +227,13 @@ hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* 
 hipError_t latent_rows(hipStream_t s, const float* latent, int64_t nimg, float* rows);
 hipError_t rows_to_latent(hipStream_t s, const float* rows, int64_t nimg, float* latent);
 hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float ds);
-hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, uint16_t* out,
-                  int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale);
+// W8A8 (w8a8.hip): activation rows to Q8_0, and the int8 product with per-block scales
+hipError_t quant_q8(hipStream_t s, const void* x, int xbf16, int64_t ldx, int64_t n, int64_t K, int8_t* q,
+                    uint16_t* d);
+hipError_t gemm_w8a8(hipStream_t s, const int8_t* xq, const uint16_t* xd, int64_t M, const int8_t* wq,
+                     const uint16_t* wd, int64_t N, int64_t K, void* y, int64_t ldy, int f16out);
+hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, void* out,
+                  int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale, int of32 = 0);
 
 // the VAE decoder (vae.hip).  vae_conv's outputs: fp32 (+ bias, + res when given), bf16 (+ bias,
 // + res when given), fp32 (+ bias) clamped to -1 .. 1, fp32 (+ bias, + DupUp3D of keep: kcin

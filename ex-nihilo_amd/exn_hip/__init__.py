@@ -27,7 +27,7 @@ LIB_PATH = os.path.join(os.path.dirname(HERE), "libexn-hip.so")
 
 OK, ENODEV, EINVAL, ENOMEM, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
 Q8_0, F32, BF16 = 8, 0, 30
-DT_F32, DT_BF16 = 0, 1
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 WIDTH, HEADS, HEAD_DIM, FFN, LATENT = 4096, 32, 128, 12288, 64
 # Qwen-Image-2.1-Turbo's schedule (src/generate.lisp:7-9)
 TURBO_SIGMAS = (1.0, 0.978453, 0.95418, 0.926626, 0.89508, 0.845148, 0.704534, 0.414568, 0.0)
@@ -65,6 +65,8 @@ SIGNATURES = {
     "exn_dequant": (c_int, [vp, vp, vp, vp]),
     "exn_mm": (c_int, [vp, vp, vp, c_int, vp, c_int, c_int64]),
     "exn_mm_noalloc": (c_int, [vp, vp, vp, c_int, vp, c_int, c_int64]),
+    "exn_quant_q8": (c_int, [vp, vp, c_int, c_int64, c_int64, c_int64, vp, vp]),
+    "exn_mm_w8a8": (c_int, [vp, vp, vp, vp, c_int64, vp, c_int]),
     "exn_mm_gate_add": (c_int, [vp, vp, vp, c_int64, vp, c_int, c_int, c_int, vp]),
     "exn_mm_swiglu": (c_int, [vp, vp, vp, vp, c_int64]),
     "exn_weight_pairs": (c_int, [vp, vp]),
@@ -84,6 +86,7 @@ SIGNATURES = {
     "exn_dit_synth": (c_int, [vp, c_uint64]),
     "exn_dit_check": (c_int, [vp]),
     "exn_dit_resident": (c_int, [vp, c_int]),
+    "exn_dit_w8a8": (c_int, [vp, c_int]),
     "exn_dit_velocity": (c_int, [vp, vp, c_int, vp, c_int, c_int, c_double, c_uint64, c_int, vp, c_int, c_int, vp]),
     "exn_dit_velocity_dev": (c_int, [vp, vp, c_int, vp, c_int, c_int, c_double, c_uint64, c_int, vp, c_int, c_int,
                                      vp]),
@@ -299,6 +302,11 @@ class Dit:
     def resident(self, bf16: bool = True):
         """Block matrices from resident bf16 expansions (the default) or from Q8_0."""
         call("exn_dit_resident", self.h, 1 if bf16 else 0)
+
+    def w8a8(self, on: bool = True):
+        """The reference's *int8* products (its default) for every Q8_0 matrix with at least 16
+        rows, or (off, this library's default) the bf16 products."""
+        call("exn_dit_w8a8", self.h, 1 if on else 0)
 
     def prefix_key(self, key) -> int:
         """A 64-bit key for a Lisp-style prefix key (EQUAL objects -> one key)."""

@@ -29,6 +29,14 @@
   (prefix-key (sb-alien:unsigned 64)) (ref-a sb-alien:int) (ref-latent sb-sys:system-area-pointer)
   (rh sb-alien:int) (rw sb-alien:int) (v sb-sys:system-area-pointer))
 (sb-alien:define-alien-routine ("exn_dit_release" %exn-dit-release) sb-alien:int (d sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_dit_w8a8" %exn-dit-w8a8) sb-alien:int
+  (d sb-sys:system-area-pointer) (on sb-alien:int))
+
+(defvar *int8* nil
+  "cuda-dit.lisp's switch (src/cuda-dit.lisp:110-113): true takes every Q8_0 product of 16 rows
+   or more as int8 activations (quant_q8 by blocks of 32, the int8 MFMA) -- the CUDA backend's
+   default numerics; false (here the default: several times faster on the MI355X, and nearer the
+   float reference) multiplies bf16 activations by the exact bf16 dequantisation.")
 
 (defconstant +exn-q8-0+ 8)
 (defconstant +exn-f32+ 0)
@@ -76,6 +84,7 @@
                      (setf (gethash prefix-key (hdit-keys d)) (1+ (hash-table-count (hdit-keys d)))))
                  0))
         (ref-latent (and ref (second ref))))
+    (exn-check (%exn-dit-w8a8 (hdit-handle d) (if *int8* 1 0)))
     (sb-sys:with-pinned-objects (context latent v ref-latent)
       (exn-check (%exn-dit-velocity (hdit-handle d) (sb-sys:vector-sap context) p (sb-sys:vector-sap latent) h w
                                     (coerce sigma 'double-float) key

@@ -110,6 +110,16 @@ int exn_mm(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int yd
  * n x cols x 2 bytes past 64 MiB is EXN_EINVAL.  Every call on one GPU shares its array,
  * so calls that overlap on one GPU (two streams or threads) race. */
 int exn_mm_noalloc(exn_ctx* ctx, const exn_w* w, const void* x, int xdt, void* y, int ydt, int64_t n);
+/* the reference's default *int8* products (src/cuda-dit.lisp:110-126), whose kernels live in
+ * illatio, after ggml's: quant_q8 (:120-123) takes N rows of K activations (fp32 or bf16,
+ * EXN_DT_F32 / EXN_DT_BF16, LDX apart) to Q8_0 by blocks of 32, Q int8 [n][K] and D fp16
+ * [n][K/32], d = amax / 127 and q = round(x / d) half away from zero */
+int exn_quant_q8(exn_ctx* ctx, const void* x, int xdt, int64_t ldx, int64_t n, int64_t k, int8_t* q, uint16_t* d);
+/* the int8 product behind mm (:119-124, illatio's MM_Q8_MMA2): a Q8_0 matrix W (rows x cols)
+ * with N rows from exn_quant_q8, per 32-block the exact integer dot product, then
+ * y = fma(float(isum), dx * dw, y) in fp32 over the blocks in order; Y [n][rows] fp32 or fp16
+ * (EXN_DT_F32 / EXN_DT_F16) */
+int exn_mm_w8a8(exn_ctx* ctx, const exn_w* w, const int8_t* xq, const uint16_t* xd, int64_t n, void* y, int ydt);
 /* mm, then x_gate_add fused into the product's store (src/cuda/dit.cu:34-41):
  * RESID[t] += tanh(GATE[row]) * (X W^T)[t]; sequence row N0 + t < P takes GATE + MSTRIDE */
 int exn_mm_gate_add(exn_ctx* ctx, const exn_w* w, const uint16_t* x_bf16, int64_t n, float* resid, int n0, int p,
@@ -182,6 +192,11 @@ int exn_dit_check(exn_dit* d);
  * present and at the next step for any set later; 0 drops them and runs from Q8_0 with the
  * dequantisation inside the product.  A change drops the kept prompt K/V. */
 int exn_dit_resident(exn_dit* d, int bf16);
+/* *int8* (src/cuda-dit.lisp:110-113): ON = 1 takes every product of a Q8_0 matrix with at
+ * least 16 rows the reference's int8 way (exn_quant_q8, exn_mm_w8a8; a block's four when all
+ * four qualify) -- the reference's default numerics; 0, this library's default, the bf16
+ * products.  A change drops the kept prompt K/V. */
+int exn_dit_w8a8(exn_dit* d, int on);
 /* dit-velocity (src/cuda-dit.lisp:137-243): CONTEXT (P x 4096 fp32, the encoder's states),
  * LATENT (64 x H x W fp32, channel-major) -> V (64 x H x W), host memory, synchronous.
  * SIGMA is a double, as the reference's schedule (src/generate.lisp:7-9); t = 1000 sigma.
@@ -215,7 +230,7 @@ int exn_dit_trace(exn_dit* d, float* buf, int64_t cap);
 #define EXN_PROF_GATE_UP 3  /* LayerNormed rows x gate_up, SwiGLU fused */
 #define EXN_PROF_DOWN 4     /* SwiGLU rows x img_mlp.out, gated residual fused */
 #define EXN_PROF_LN_MOD 5   /* LayerNorm x (1 + scale) */
-#define EXN_PROF_QKV_PREP 6 /* QK RMSNorm + RoPE, V transposed (Q8_0 weights only) */
+#define EXN_PROF_QKV_PREP 6 /* QK RMSNorm + RoPE, V transposed (when the QKV product does not fuse them) */
 #define EXN_PROF_EDGE 7     /* timestep, txt_in, img_in, proj_out and the rest */
 #define EXN_PROF_CLASSES 8
 int exn_dit_profile(exn_dit* d, int on);

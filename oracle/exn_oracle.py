@@ -14,7 +14,15 @@ It restates, function by function (citations are into the reference tree):
     cached pass runs the image rows only against the kept prompt K/V) and
     the edit insertion of the reference picture's rows;
   - src/generate.lisp:7-9,133-135: the Turbo sigma list and the Euler update;
-  - src/weights.lisp:19-45: tensor names and ggml dims.
+  - src/weights.lisp:19-45: tensor names and ggml dims;
+  - src/cuda-dit.lisp:110-126: the int8 product of the reference's default
+    *int8* mode (Q8_0 matrices times activations quantised to Q8_0 by blocks
+    of 32, n >= 16 rows).  Its kernels (quant_q8, MM_Q8_MMA2) live in illatio,
+    which the reference does not vendor and pins to no version; quant_q8_0 and
+    linear_w8a8 restate ggml's published CUDA forms (the activation quantiser
+    of its batched Q8_0 product and the Q8_0 block dot product), which the
+    reference's note names as their model ("ggml's way for a batch",
+    :111-113).  Against illatio's own arithmetic this is parity unpinned;
 and the synthetic inputs (a counter-based generator, defined in synth.c),
 whose C twin is oracle/liboracle.so.
 
@@ -184,6 +192,51 @@ def dequant_q8_0(qs: np.ndarray, d: np.ndarray) -> np.ndarray:
     return (q * d.astype(np.float32).reshape(rows, -1, 1)).reshape(qs.shape)
 
 
+# --- the W8A8 product (src/cuda-dit.lisp:110-126) ------------------------------------
+
+def quant_q8_0(x):
+    """Activations to Q8_0 by blocks of 32, as quant_q8 does ahead of the reference's int8
+    products (src/cuda-dit.lisp:120-123), after ggml's CUDA activation quantiser: amax = max |x|
+    over the block, d = amax / 127, q = round(x / d) half away from zero (0 when amax is 0), the
+    divisions float32 and correctly rounded; d is kept as fp16 and the products use that.
+    X: (n, K) float32, K a multiple of 32.  Returns (q int8 (n, K), d float16 (n, K / 32))."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, K = x.shape
+    b = x.reshape(n, K // 32, 32)
+    amax = np.abs(b).max(axis=2)
+    d = (amax / np.float32(127)).astype(np.float32)
+    safe = np.where(amax != 0, d, np.float32(1)).astype(np.float32)
+    v = (b / safe[:, :, None]).astype(np.float32)
+    q = np.sign(v) * np.floor(np.abs(v.astype(np.float64)) + 0.5)      # half away from zero, exact
+    q = np.where(amax[:, :, None] != 0, q, 0)
+    return q.astype(np.int8).reshape(n, K), d.astype(np.float16)
+
+
+def linear_w8a8(x, qs, d, gain=1.0):
+    """Y = X W^T the reference's int8 way (src/cuda-dit.lisp:119-124: quant_q8, then illatio's
+    MM_Q8_MMA2 after ggml's Q8_0 x Q8_0 dot product): X quantised by quant_q8_0; per 32-block
+    the integer dot product, exact; then y = fma(float(isum), dx * dw, y) in float32 over the
+    blocks in order, the scale product (exact: 11 x 11 bits) rounded, the fused multiply-add
+    rounded once (the C twin's fmaf).  W: Q8_0 SoA (qs int8 (N, K), d float16 (N, K / 32));
+    GAIN, a power of two, scales dw."""
+    lib = clib()
+    if lib is None:
+        raise RuntimeError("linear_w8a8 takes its fused multiply-adds from oracle/liboracle.so (make -C oracle)")
+    xq, xd = quant_q8_0(x)
+    n, K = xq.shape
+    xqf, wqf = xq.astype(np.float32), np.asarray(qs).astype(np.float32)
+    dx = xd.astype(np.float32)
+    dw = (np.asarray(d).astype(np.float32) * np.float32(gain)).astype(np.float32)
+    N = wqf.shape[0]
+    y = np.zeros((n, N), np.float32)
+    for blk in range(K // 32):
+        c = slice(32 * blk, 32 * blk + 32)
+        isum = np.ascontiguousarray(xqf[:, c] @ wqf[:, c].T, dtype=np.float32)   # exact: below 2^20
+        lib.exo_w8a8_fma(_ptr(isum), _ptr(np.ascontiguousarray(dx[:, blk])), _ptr(np.ascontiguousarray(dw[:, blk])),
+                         n, N, _ptr(y))
+    return y
+
+
 def bf16_bits(x: np.ndarray) -> np.ndarray:
     """fp32 -> bf16 bit patterns (uint16), round to nearest even, NaN quiet."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
@@ -225,6 +278,7 @@ def clib():
         lib.exo_normal.argtypes = [u64, u64, i64, vp]
         lib.exo_dequant_q8_0_blocks.argtypes = [vp, i64, vp]
         lib.exo_dequant_q8_0.argtypes = [vp, vp, i64, vp]
+        lib.exo_w8a8_fma.argtypes = [vp, vp, vp, i64, i64, vp]
         _LIB = lib
     return _LIB
 
@@ -322,6 +376,16 @@ def synth_inputs(seed: int, p: int, h: int, w: int, shape: Shape = Shape(), ref_
 def linear(x, w):
     """Y = X W^T, w (out, in) -- inspect/ref_dit.py:33-34."""
     return x @ w.T
+
+
+def mm(wt, name, x, w8a8=False):
+    """The reference's product dispatch for matrix NAME (src/cuda-dit.lisp:115-126): with W8A8
+    (its default *int8*), a Q8_0 matrix (WT has its codes) times at least 16 rows goes the int8
+    way (linear_w8a8); everything else is linear(x, wt(name))."""
+    if w8a8 and x.shape[0] >= 16 and hasattr(wt, "q8"):
+        qs, d = wt.q8(name)
+        return linear_w8a8(x, qs, d, getattr(wt, "gain", 1.0))
+    return linear(x, wt(name))
 
 
 def layernorm(x, eps=EPS):
@@ -455,36 +519,37 @@ def modulation(wt, sigma, shape=Shape()):
     return emb, mod, sc
 
 
-def block(wt, il, x, mod_rows, cos, sin, kfull, vfull, q0, p, b0, b1, shape=Shape()):
+def block(wt, il, x, mod_rows, cos, sin, kfull, vfull, q0, p, b0, b1, shape=Shape(), w8a8=False):
     """One block (inspect/ref_dit.py:132-148): X's rows are sequence rows
     q0..q0+n-1; MOD_ROWS (n, 4W) their modulation rows; KFULL/VFULL receive
-    this pass's K, V at rows q0.. and hold the kept prefix below.  Returns the
-    new X (float32)."""
+    this pass's K, V at rows q0.. and hold the kept prefix below.  W8A8: the
+    products as the reference's int8 mode takes them (mm).  Returns the new X
+    (float32)."""
     W, H, HD, F = shape.width, shape.heads, shape.head_dim, shape.ffn
     n = x.shape[0]
     scale1, gate1, scale2, gate2 = (mod_rows[:, i * W:(i + 1) * W] for i in range(4))
     b = "transformer_blocks.%d." % il
     y = layernorm(x) * (1.0 + scale1)
-    q = linear(y, wt(b + "attn.to_q.weight")).reshape(n, H, HD)
-    k = linear(y, wt(b + "attn.to_k.weight")).reshape(n, H, HD)
-    v = linear(y, wt(b + "attn.to_v.weight")).reshape(n, H, HD)
+    q = mm(wt, b + "attn.to_q.weight", y, w8a8).reshape(n, H, HD)
+    k = mm(wt, b + "attn.to_k.weight", y, w8a8).reshape(n, H, HD)
+    v = mm(wt, b + "attn.to_v.weight", y, w8a8).reshape(n, H, HD)
     q = rope(rmsnorm(q, wt(b + "attn.norm_q.weight")), cos, sin)
     k = rope(rmsnorm(k, wt(b + "attn.norm_k.weight")), cos, sin)
     kfull[q0:q0 + n] = k
     vfull[q0:q0 + n] = v
     a = attention(q, kfull, vfull, q0, p, b0, b1).reshape(n, W)
-    x = x + np.tanh(gate1) * linear(a, wt(b + "attn.to_out.0.weight"))
+    x = x + np.tanh(gate1) * mm(wt, b + "attn.to_out.0.weight", a, w8a8)
     y = layernorm(x) * (1.0 + scale2)
-    gu = linear(y, wt(b + "img_mlp.gate_up.weight"))
+    gu = mm(wt, b + "img_mlp.gate_up.weight", y, w8a8)
     y = silu(gu[:, :F]) * gu[:, F:]
-    x = x + np.tanh(gate2) * linear(y, wt(b + "img_mlp.out.weight"))
+    x = x + np.tanh(gate2) * mm(wt, b + "img_mlp.out.weight", y, w8a8)
     return x.astype(np.float32)
 
 
-def prompt_rows(wt, ctx, shape=Shape()):
+def prompt_rows(wt, ctx, shape=Shape(), w8a8=False):
     """txt_in: RMSNorm with (1 + w), linear, GELU-tanh, linear (inspect/ref_dit.py:120-121)."""
     txt = rmsnorm(ctx, 1.0 + wt("txt_in.text_norm.weight"))
-    return linear(gelu_tanh(linear(txt, wt("txt_in.in_layer.weight"))), wt("txt_in.out_layer.weight"))
+    return mm(wt, "txt_in.out_layer.weight", gelu_tanh(mm(wt, "txt_in.in_layer.weight", txt, w8a8)), w8a8)
 
 
 def tokens(latent):
@@ -494,7 +559,7 @@ def tokens(latent):
 
 
 def forward(wt, ctx, latent, sigma, shape=Shape(), ref=None, cache: PrefixCache | None = None,
-            prefix_key=None, dump=None, layers=None):
+            prefix_key=None, dump=None, layers=None, w8a8=False):
     """The velocity at SIGMA, dit-velocity's contract (src/cuda-dit.lisp:137-144):
     CTX the encoder's P x context states, LATENT (64, h, w) channel-major.
     REF = (a, ref_latent (64, rh, rw)): an edit's reference picture, put in the
@@ -502,7 +567,9 @@ def forward(wt, ctx, latent, sigma, shape=Shape(), ref=None, cache: PrefixCache 
     call keeps each layer's prefix K/V and a later call with the same key and
     prefix length runs only the image rows.  DUMP (a dict) receives 'txt'
     (the prompt rows, uncached pass only) and 'blk' (x after each block).
-    Without REF and CACHE this is ref_dit.forward, step for step."""
+    W8A8: every product of a Q8_0 matrix with at least 16 rows the reference's
+    int8 way (mm; src/cuda-dit.lisp:110-126).  Without REF, CACHE and W8A8
+    this is ref_dit.forward, step for step."""
     W, H, HD = shape.width, shape.heads, shape.head_dim
     L = shape.layers if layers is None else layers
     ptext = ctx.shape[0]
@@ -515,17 +582,17 @@ def forward(wt, ctx, latent, sigma, shape=Shape(), ref=None, cache: PrefixCache 
     n0 = p if cached else 0
     l = p + nimg
     emb, mod, sc = modulation(wt, sigma, shape)
-    img = linear(tokens(latent), wt("img_in.weight"))
+    img = mm(wt, "img_in.weight", tokens(latent), w8a8)
     if cached:
         x = img.astype(np.float32)
     else:
-        txt = prompt_rows(wt, ctx, shape)
+        txt = prompt_rows(wt, ctx, shape, w8a8)
         if dump is not None:
             dump["txt"] = txt.astype(np.float32)
         if ref is None:
             pre = txt
         else:
-            rimg = linear(tokens(ref[1]), wt("img_in.weight"))
+            rimg = mm(wt, "img_in.weight", tokens(ref[1]), w8a8)
             pre = np.concatenate([txt[:a], rimg, txt[a:]])
         x = np.concatenate([pre, img]).astype(np.float32)
     n = x.shape[0]
@@ -543,7 +610,7 @@ def forward(wt, ctx, latent, sigma, shape=Shape(), ref=None, cache: PrefixCache 
         vfull = np.zeros((l, H, HD), dtype=np.float32)
         if cached:
             kfull[:p], vfull[:p] = cache.kv[il]
-        x = block(wt, il, x, mod_rows, cos, sin, kfull, vfull, n0, p, b0, b1, shape)
+        x = block(wt, il, x, mod_rows, cos, sin, kfull, vfull, n0, p, b0, b1, shape, w8a8)
         if cache is not None and prefix_key is not None and not cached:
             cache.kv[il] = (kfull[:p].copy(), vfull[:p].copy())
         if dump is not None:
@@ -552,19 +619,19 @@ def forward(wt, ctx, latent, sigma, shape=Shape(), ref=None, cache: PrefixCache 
         cache.key, cache.length = prefix_key, p
     xi = x[p - n0:]
     xi = layernorm(xi) * (1.0 + sc)
-    v = linear(xi, wt("proj_out.weight"))                    # (h*w) x 64
+    v = mm(wt, "proj_out.weight", xi, w8a8)                  # (h*w) x 64
     return v.T.reshape(c, h, w).astype(np.float32)
 
 
 def euler(wt, ctx, latent, shape=Shape(), sigmas=TURBO_SIGMAS, ref=None, prefix_key="prompt",
-          layers=None, on_step=None):
+          layers=None, on_step=None, w8a8=False):
     """The Turbo schedule's Euler loop: z <- z + (s' - s) v, (s' - s) as a
     single float (src/generate.lisp:133-135; edit: :95-97).  The prefix cache
     is used as generate uses it (:prefix-key prompt)."""
     z = latent.astype(np.float32).copy()
     cache = PrefixCache()
     for s, s2 in zip(sigmas[:-1], sigmas[1:]):
-        v = forward(wt, ctx, z, s, shape, ref=ref, cache=cache, prefix_key=prefix_key, layers=layers)
+        v = forward(wt, ctx, z, s, shape, ref=ref, cache=cache, prefix_key=prefix_key, layers=layers, w8a8=w8a8)
         z = z + np.float32(s2 - s) * v
         if on_step is not None:
             on_step(s, v, z)

@@ -12,6 +12,9 @@
  *   - fp32 -> bf16 round-to-nearest-even, the rounding of a dequantised
  *     weight into a bf16 MFMA operand.
  *   - fp32 -> fp16 round-to-nearest-even (subnormals kept).
+ *   - the accumulation of the int8 product (the reference's *int8* mode,
+ *     src/cuda-dit.lisp:110-126; ggml's Q8_0 block product, compiled with a
+ *     fused multiply-add): acc = fmaf(isum, dx * dw, acc), one rounding.
  *   - the counter-based synthetic generator that makes the same weights on
  *     the host and on the GPU.  It has no counterpart in the reference
  *     (whose weights come from a GGUF file); its definition is the one the
@@ -160,4 +163,16 @@ void exo_dequant_q8_0_blocks(const uint8_t* blocks, int64_t nblocks, float* out)
 void exo_dequant_q8_0(const int8_t* qs, const uint16_t* d, int64_t n, float* out) {
 #pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < n; ++i) out[i] = exo_f16_to_f32(d[i / 32]) * (float)qs[i];
+}
+
+/* the int8 product's accumulation over one 32-block: acc[i][j] = fmaf(isum[i][j], dx[i] * dw[j],
+ * acc[i][j]) for an n x m tile of exact integer sums (held as floats), the scale product rounded
+ * to fp32 and the fused multiply-add rounded once (C99's fmaf is exact) */
+void exo_w8a8_fma(const float* isum, const float* dx, const float* dw, int64_t n, int64_t m, float* acc) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t j = 0; j < m; ++j) {
+      const float sc = dx[i] * dw[j];
+      acc[i * m + j] = fmaf(isum[i * m + j], sc, acc[i * m + j]);
+    }
 }

@@ -428,3 +428,30 @@ def test_workloads_eight_steps_full_depth(ctx, case):
     say("%s: final latent, device loop vs host loop rel-L2 %.2e, |z| %.4f" % (case, ez, float(np.sqrt((z * z).mean()))))
     assert np.isfinite(zg).all() and ez < 1e-5
     d.destroy()
+
+
+def test_w8a8_mode(ctx):
+    """The reference's default *int8* products (exn_dit_w8a8; src/cuda-dit.lisp:110-126): 2 blocks,
+    40 text rows and a 16 x 16 image (every block product, txt_in, img_in and proj_out of at
+    least 16 rows go the int8 way), against the oracle's forward in its int8 mode (<= 1e-2, and
+    nearer to it than to the oracle's bf16-free forward); the cached pass equals the uncached
+    one bit for bit; switching the mode off gives the bf16 products' velocity back, bit for bit."""
+    say("int8 mode, 2 blocks")
+    seed, p, h, w = 9, 40, 16, 16
+    d = model(ctx, 2, seed)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    v_bf = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7)
+    d.w8a8(True)
+    v8 = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7, prefix_key="k")
+    v8c = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7, prefix_key="k")
+    wt = xo.SynthWeights(seed)
+    want = xo.forward(wt, ctxa, lat, 0.7, layers=2, w8a8=True)
+    plain = xo.forward(wt, ctxa, lat, 0.7, layers=2)
+    e, e_plain, e_mode = xo.rel_l2(v8, want), xo.rel_l2(v8, plain), xo.rel_l2(want, plain)
+    say("int8 velocity rel-L2: against the int8 oracle %.2e, against the plain oracle %.2e; the oracle's "
+        "two modes differ by %.2e; cached vs uncached %.2e" % (e, e_plain, e_mode, xo.rel_l2(v8c, v8)))
+    assert e < 1e-2 and e < e_plain
+    assert np.array_equal(v8c, v8)
+    d.w8a8(False)
+    assert np.array_equal(X.dit_velocity(d, ctxa, p, lat, h, w, 0.7), v_bf)
+    d.destroy()

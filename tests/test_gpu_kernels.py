@@ -525,3 +525,58 @@ def test_attention_prescaled(ctx, n, q0, p, l, b0, b1):
     got, want = _attend_case(ctx, n, q0, p, l, b0, b1, 7 + n, prescaled=True)
     assert np.abs(got - want).max() < 3e-3 + 2 ** -9
     assert xo.rel_l2(got, want) < 3e-3
+
+
+# --- the int8 products (src/cuda-dit.lisp:110-126) ------------------------------------------
+
+def test_quant_q8_bit_exact(ctx):
+    """exn_quant_q8 against the oracle's quant_q8_0, code for code and scale for scale: rows at
+    magnitudes 1e-3 .. 1e3, a zero block, a block whose x / d lands half-way (away from zero),
+    from fp32 rows and from bf16 rows, with a row stride past K."""
+    rng = np.random.default_rng(21)
+    n, K, ld = 300, 4096, 4096 + 64
+    x = (rng.normal(0, 1, (n, ld)) * rng.uniform(1e-3, 1e3, (n, 1))).astype(np.float32)
+    x[5, 64:96] = 0
+    x[7, :32] = 0
+    x[7, :5] = [0.5, 2.5, -1.5, 126.5, 127.0]
+    for dt in (X.DT_F32, X.DT_BF16):
+        xin = x if dt == X.DT_F32 else bf16(x)
+        want = x[:, :K] if dt == X.DT_F32 else from_bf16(bf16(x))[:, :K]
+        q = X.DevBuf(ctx, (n, K), np.int8)
+        dd = X.DevBuf(ctx, (n, K // 32), np.uint16)
+        X.call("exn_quant_q8", ctx.h, dev(ctx, xin).h, dt, ld, n, K, q.h, dd.h)
+        wq, wd = xo.quant_q8_0(want)
+        gq, gd = q.get(), dd.get()
+        say("quant_q8 from %s: codes equal %s, scales equal %s" % ("fp32" if dt == X.DT_F32 else "bf16",
+                                                                 np.array_equal(gq, wq), np.array_equal(gd, wd.view(np.uint16))))
+        assert np.array_equal(gq, wq) and np.array_equal(gd, wd.view(np.uint16))
+        if dt == X.DT_F32:
+            assert list(gq[7, :5]) == [1, 3, -2, 127, 127] and not gq[5, 64:96].any() and gd[5, 2] == 0
+
+
+W8A8_CASES = [(64, 256, 4096), (300, 4096, 4096), (77, 12288, 4096), (128, 4096, 12288), (40, 4096, 64)]
+
+
+@pytest.mark.parametrize("M,N,K", W8A8_CASES)
+def test_mm_w8a8_bit_exact(ctx, M, N, K):
+    """exn_mm_w8a8 on exn_quant_q8's codes against the oracle's linear_w8a8, bit for bit (the
+    same exact integer block sums and the same float32 products and sums in the same order):
+    partial tiles in M and N, K of 2 to 384 blocks; fp16 out equal to the fp32 result rounded."""
+    say("mm_w8a8", M, N, K)
+    rng = np.random.default_rng(M + N + K)
+    x = (rng.normal(0, 1, (M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
+    seed, tid = 12, 400 + N // 64 + K // 64
+    w = X.Weight.synth(ctx, seed, tid, N, K)
+    qs, d = xo.q8_0_synth(seed, tid, N, K)
+    q = X.DevBuf(ctx, (M, K), np.int8)
+    dd = X.DevBuf(ctx, (M, K // 32), np.uint16)
+    X.call("exn_quant_q8", ctx.h, dev(ctx, x).h, X.DT_F32, K, M, K, q.h, dd.h)
+    y = X.DevBuf(ctx, (M, N), np.float32)
+    X.call("exn_mm_w8a8", ctx.h, w.h, q.h, dd.h, M, y.h, X.DT_F32)
+    got, want = y.get(), xo.linear_w8a8(x, qs, d)
+    say("bit-exact %s, rel-L2 %.2e; against the unquantised product %.2e" %
+        (np.array_equal(got, want), xo.rel_l2(got, want), xo.rel_l2(got, x @ xo.dequant_q8_0(qs, d).T)))
+    assert np.array_equal(got, want)
+    y16 = X.DevBuf(ctx, (M, N), np.uint16)
+    X.call("exn_mm_w8a8", ctx.h, w.h, q.h, dd.h, M, y16.h, X.DT_F16)
+    assert np.array_equal(y16.get(), want.astype(np.float16).view(np.uint16))

@@ -383,3 +383,113 @@ def test_edit_mask_fixes_what_each_prefix_row_sees():
     # and the image rows' positions start after the text that follows the picture
     pos = xo.positions(p, 3, 4, (a, rh, rw))
     assert pos[p, 0] == a + max(rh, rw) + (p - a - nref)
+
+
+# --- the W8A8 product (src/cuda-dit.lisp:110-126) ------------------------------------------
+
+def test_quant_q8_0_closed_forms():
+    """Blocks whose quantisation the definition fixes: values on the grid of d come back as
+    their integers; a value x with x / d half-way between two integers goes away from zero
+    (0.5 -> 1, 2.5 -> 3, -1.5 -> -2, where half-to-even would give 0, 2, -2); the block's
+    largest magnitude maps to +-127; an all-zero block gives d = 0 and zeros; d is amax / 127
+    rounded to fp16."""
+    k = np.arange(-127, 128, 8, dtype=np.float32)                    # 32 integers, 127 among them
+    k = np.concatenate([k, np.zeros(32 - k.size, np.float32)])[:32]
+    k[0] = -127.0
+    half = np.full(32, 0.0, np.float32)
+    half[:4] = [0.5, 2.5, -1.5, 126.5]
+    half[4] = 127.0                                                  # amax 127 -> d = 1
+    x = np.stack([k * np.float32(0.125), half, np.zeros(32, np.float32),
+                  np.linspace(-3, 7, 32, dtype=np.float32)])
+    q, d = xo.quant_q8_0(x)
+    assert np.array_equal(q[0], k.astype(np.int8)) and d[0] == np.float16(0.125)
+    assert list(q[1, :5]) == [1, 3, -2, 127, 127] and d[1] == np.float16(1.0)
+    assert not q[2].any() and d[2] == 0
+    assert q[3].max() == 127 and np.argmax(q[3]) == 31
+    assert d[3] == np.float16(np.float32(7) / np.float32(127))
+
+
+def test_quant_q8_0_error_bound():
+    """Every value within half a step of d q (plus the fp16 rounding of d), |q| <= 127."""
+    rng = np.random.default_rng(3)
+    x = (rng.normal(0, 1, (64, 256)) * rng.uniform(1e-3, 1e3, (64, 1))).astype(np.float32)
+    q, d = xo.quant_q8_0(x)
+    df = np.repeat(d.astype(np.float64), 32, axis=1)
+    err = np.abs(x.astype(np.float64) - df * q)
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    assert (err <= 0.5 * df * (1 + 1e-3) + 127 * df * 2.0 ** -11).all()
+
+
+def test_linear_w8a8_is_the_product_of_the_dequantised_operands():
+    """Per block, dx dw sum(qx qw) is the product of the dequantised operands summed over the
+    block, so linear_w8a8 equals (dx qx) (dw qw)^T up to float32 rounding (a wrong block index
+    or scale fails at 1e-2), against float64 brute force over the blocks too; and it stays within
+    the activations' quantisation error of the unquantised product."""
+    rng = np.random.default_rng(4)
+    x = rng.normal(0, 1, (40, 256)).astype(np.float32)
+    qs, d = xo.q8_0_synth(2, 7, 48, 256)
+    y = xo.linear_w8a8(x, qs, d)
+    xq, xd = xo.quant_q8_0(x)
+    deq = xo.dequant_q8_0(xq, xd).astype(np.float64) @ xo.dequant_q8_0(qs, d).astype(np.float64).T
+    brute = np.zeros((40, 48))
+    for b in range(8):
+        c = slice(32 * b, 32 * b + 32)
+        brute += (xd[:, b:b + 1].astype(np.float64) * d[:, b].astype(np.float64)[None, :]) * \
+            (xq[:, c].astype(np.int64) @ qs[:, c].astype(np.int64).T)
+    assert xo.rel_l2(y, deq) < 1e-6 and xo.rel_l2(y, brute) < 1e-6
+    assert xo.rel_l2(deq, brute) < 1e-12
+    e = xo.rel_l2(y, x @ xo.dequant_q8_0(qs, d).T)
+    assert 1e-4 < e < 2e-2
+
+
+
+def _f32_round(q):
+    """The float32 nearest the rational Q, ties to even, by exact comparison."""
+    from fractions import Fraction
+    f = np.float32(float(q))
+    lo, hi = (np.nextafter(f, np.float32(-np.inf)), f) if Fraction(float(f)) > q else (f, np.nextafter(f, np.float32(np.inf)))
+    dlo, dhi = q - Fraction(float(lo)), Fraction(float(hi)) - q
+    if dlo != dhi:
+        return lo if dlo < dhi else hi
+    return lo if (int(np.float32(lo).view(np.uint32)) & 1) == 0 else hi
+
+
+def test_linear_w8a8_accumulates_with_single_rounding_fmas():
+    """Each block adds float(isum) * (dx * dw) to the sum with one rounding (a fused multiply-add
+    on the rounded scale product): rebuilt here in exact rational arithmetic on a small product,
+    every step rounded to float32 where the definition rounds, and equal bit for bit; a product
+    then a sum, each rounded, differs somewhere."""
+    from fractions import Fraction
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, (6, 256)).astype(np.float32)
+    qs, d = xo.q8_0_synth(3, 9, 5, 256)
+    y = xo.linear_w8a8(x, qs, d)
+    xq, xd = xo.quant_q8_0(x)
+    acc = [[np.float32(0)] * 5 for _ in range(6)]
+    two = [[np.float32(0)] * 5 for _ in range(6)]
+    for b in range(8):
+        c = slice(32 * b, 32 * b + 32)
+        isum = xq[:, c].astype(np.int64) @ qs[:, c].astype(np.int64).T
+        for i in range(6):
+            for j in range(5):
+                sc = np.float32(xd[i, b]) * np.float32(d[j, b])      # float32 product, rounded
+                exact = Fraction(int(isum[i, j])) * Fraction(float(sc)) + Fraction(float(acc[i][j]))
+                acc[i][j] = _f32_round(exact)
+                two[i][j] = np.float32(two[i][j] + np.float32(np.float32(isum[i, j]) * sc))
+    want, sep = np.array(acc, np.float32), np.array(two, np.float32)
+    assert np.array_equal(y, want)
+    assert not np.array_equal(sep, want) and xo.rel_l2(sep, want) < 1e-6
+
+
+def test_forward_w8a8_routes_q8_0_products_of_16_rows_or_more():
+    """The int8 mode changes the velocity by about the activations' quantisation error and
+    leaves a pass of fewer than 16 rows (every product through linear) exactly as it was."""
+    seed, p, h, w = 3, 8, 4, 4
+    wt = xo.SynthWeights(seed, TINY, gain=4.0)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w, TINY)
+    v = xo.forward(wt, ctxa, lat, 0.7, TINY)
+    v8 = xo.forward(wt, ctxa, lat, 0.7, TINY, w8a8=True)
+    e = xo.rel_l2(v8, v)
+    assert 1e-5 < e < 5e-2
+    small = xo.forward(wt, ctxa[:4], lat[:, :2, :2], 0.7, TINY, w8a8=True)
+    assert np.array_equal(small, xo.forward(wt, ctxa[:4], lat[:, :2, :2], 0.7, TINY))
