@@ -9,11 +9,11 @@
 //            in fp32, blocks in order: the scale product rounded, the fused multiply-add
 //            rounded once (ggml's sum += d * sumi as its CUDA compiler fuses it).
 //
-// On gfx950 the per-32 rescale, not the int8 MFMA, sets the pace: every 16x16x32 MFMA leaves
-// 4 int32 sums a lane that each take a conversion, the scale product and a fused multiply-add,
-// and the kernel runs at the VALU's issue rate.  The operands therefore come straight from L2
-// into the MFMA registers (no LDS stage would shorten the VALU work); only the scales are
-// staged through LDS, 8 blocks at a time.
+// On gfx950 the per-32 rescale, not the int8 MFMA, bounds the product: every 16x16x32 MFMA
+// leaves 4 int32 sums a lane that each take a conversion, the scale product and a fused
+// multiply-add.  k_gemm_w8a8_dma (below) is the product the model runs; k_gemm_w8a8, whose
+// operands come straight from L2 into the MFMA registers, takes the shapes the DMA path does
+// not (K not a multiple of 64, unaligned rows).
 #include "exn_common.h"
 
 namespace exn {
@@ -192,15 +192,189 @@ k_gemm_w8a8(const int8_t* __restrict__ xq, const uint16_t* __restrict__ xd, cons
     }
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// one lane of a DMA into LDS: BYTES (4 or 16) from base + voff + soff, zeros where voff passes
+// the extent (every offset here stays inside its row, so soff never carries a read past it)
+__device__ __forceinline__ void dma16(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t extent, lds_void* dst, uint32_t voff, int soff) {
+  __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)extent, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, voff, soff, 0, 0);
+}
+
+// The same product with its operands moved HBM/L2 -> LDS by the DMA path, NS stages of a chunk
+// (2 blocks: 64 bytes of K) ahead (3 stages, 51 KB: three workgroups a CU; 4 stages, two
+// workgroups, ran 17% slower, and loads straight from L2 into registers twice as slow again): per stage the tile's 128 code rows of X and of W (8 KB each,
+// row r's 16-byte chunk c stored at c ^ (r / 4 % 4), so the fragment reads are conflict-free)
+// and their fp16 scales of the two blocks (512 bytes each).  A wave's DMA a chunk is five
+// instructions (2 X, 2 W, 1 scales), so waiting for chunk c while the NS - 2 after it are out
+// is vmcnt(5 (NS - 2)).  Rows past M or N read as zeros (the buffer extents) and are not
+// stored.  K a multiple of 64, ldx-free: X and W rows K bytes apart.
+#define W8_NS 3
+template <bool F16OUT>
+__global__ void __launch_bounds__(256)
+k_gemm_w8a8_dma(const int8_t* __restrict__ xq, const uint16_t* __restrict__ xd, const int8_t* __restrict__ wq,
+                const uint16_t* __restrict__ wd, int64_t M, int64_t N, int64_t K, void* __restrict__ y, int64_t ldy) {
+  // stage s: X codes at s * 17 KB, W codes + 8 KB, X scales + 16 KB, W scales + 16.5 KB
+  extern __shared__ __align__(1024) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, g = lane >> 4;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int64_t tm = (int64_t)blockIdx.y * 128, tn = (int64_t)blockIdx.x * 128;
+  const int KB = (int)(K / 32), KC = KB / 2;
+  const uint32_t xext = (uint32_t)(max((int64_t)0, M - tm) * K), wext = (uint32_t)(max((int64_t)0, N - tn) * K);
+  const uint32_t xsext = (uint32_t)(max((int64_t)0, M - tm) * KB * 2), wsext = (uint32_t)(max((int64_t)0, N - tn) * KB * 2);
+  const int8_t* xbase = xq + tm * K;
+  const int8_t* wbase = wq + tn * K;
+  const uint16_t* xsbase = xd + tm * KB;
+  const uint16_t* wsbase = wd + tn * KB;
+  // code DMA: instruction i (0, 1) of wave w moves rows (2w + i) * 16 + l / 4, LDS chunk l % 4
+  uint32_t coff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (2 * wave + i) * 16 + (lane >> 2);
+    coff[i] = (uint32_t)(r * K + 16 * ((lane & 3) ^ ((r >> 2) & 3)));
+  }
+  // scale DMA: wave w moves 4 bytes (the chunk's two fp16 scales) of row (w & 1) * 64 + l, of X
+  // (waves 0, 1) or W (waves 2, 3)
+  const int srow = (wave & 1) * 64 + lane;
+  const uint32_t soff = (uint32_t)(srow * KB * 2);
+  auto issue = [&](int c) {
+    uint8_t* st = smem + (c % W8_NS) * 17408;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma16(xbase, xext, (lds_void*)(st + (2 * wave + i) * 1024), coff[i], c * 64);
+      dma16(wbase, wext, (lds_void*)(st + 8192 + (2 * wave + i) * 1024), coff[i], c * 64);
+    }
+    if (wave < 2) dma4(xsbase, xsext, (lds_void*)(st + 16384 + (wave & 1) * 256), soff, c * 4);
+    else dma4(wsbase, wsext, (lds_void*)(st + 16896 + (wave & 1) * 256), soff, c * 4);
+  };
+  // fragment reads: row tile i (or column tile j) of the wave, block bb of the chunk: LDS row r,
+  // chunk 2 bb + g / 2 at its swizzled place, 8 bytes at 8 (g % 2)
+  int rdx[4], rdw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ra = wm + 16 * i + c16, rb = wn + 16 * i + c16;
+    rdx[i] = ra * 64 + 8 * (g & 1) + ((ra >> 2) & 3) * 16;   // chunk index XORed in below
+    rdw[i] = rb * 64 + 8 * (g & 1) + ((rb >> 2) & 3) * 16;
+  }
+  int32x4 zero = {0, 0, 0, 0};
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto frag = [&](const uint8_t* base, int rd, int chunk) {
+    // rd holds row * 64 + 8 (g % 2) + 16 f(row); the place of chunk c is 16 (c ^ f(row))
+    const int f16x = rd & 0x30;   // 16 f(row)
+    return *(const int64_t*)(base + (rd & ~0x30) + ((chunk * 16) ^ f16x));
+  };
+  const int nc = KC;
+  for (int c = 0; c < W8_NS - 1 && c < nc; ++c) issue(c);
+  for (int c = 0; c < nc; ++c) {
+    // chunk c has landed for every wave; every wave is done with chunk c - 1's stage
+    asm volatile("" ::: "memory");
+    constexpr int VM = 5 * (W8_NS - 2);   // the DMA of the chunks after c may stay out
+    if (c + W8_NS - 2 < nc) __builtin_amdgcn_s_waitcnt((VM & 0xF) | (0x7 << 4) | (0x0 << 8) | ((VM >> 4) << 14));
+    else __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));   // vmcnt(0): the last chunks
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (c + W8_NS - 1 < nc) issue(c + W8_NS - 1);
+    const uint8_t* st = smem + (c % W8_NS) * 17408;
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      int64_t a[4], w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = frag(st, rdx[i], 2 * bb + (g >> 1));
+        w[i] = frag(st + 8192, rdw[i], 2 * bb + (g >> 1));
+      }
+      f32x4 dx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 u = *(const u32x4*)(st + 16384 + (wm + 16 * i + 4 * g) * 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dx[i][r] = f16_to_f32(bb ? u[r] >> 16 : u[r]);
+      }
+      float dw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t u = *(const uint32_t*)(st + 16896 + (wn + 16 * j + c16) * 4);
+        dw[j] = f16_to_f32(bb ? u >> 16 : u);
+      }
+      int32x4 cur[4], nxt[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cur[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[0], w[j], zero, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)   // the scale product rounded on its own, before the fused multiply-add
+        if (i + 1 < 4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) nxt[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i + 1], w[j], zero, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float sc = dx[i][r] * dw[j];
+            acc[i][j][r] = __builtin_fmaf((float)cur[j][r], sc, acc[i][j][r]);
+          }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = tm + wm + 16 * i + 4 * g + r;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t n = tn + wn + 16 * j + c16;
+        if (n >= N) continue;
+        if constexpr (F16OUT)
+          ((uint16_t*)y)[m * ldy + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
+        else
+          ((float*)y)[m * ldy + n] = acc[i][j][r];
+      }
+    }
+}
+
 hipError_t gemm_w8a8(hipStream_t s, const int8_t* xq, const uint16_t* xd, int64_t M, const int8_t* wq,
                      const uint16_t* wd, int64_t N, int64_t K, void* y, int64_t ldy, int f16out) {
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K % 32 || K <= 0 || ((uintptr_t)xq & 7) || ((uintptr_t)wq & 7) || ldy < N) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128));
-  if (f16out)
+  // the DMA path: 16-byte code chunks and 4-byte scale pairs, buffer extents within 32 bits
+  const bool dma_ok = K % 64 == 0 && ((uintptr_t)xq & 15) == 0 && ((uintptr_t)wq & 15) == 0 &&
+                      ((uintptr_t)xd & 3) == 0 && ((uintptr_t)wd & 3) == 0 && M * K < ((int64_t)1 << 31) &&
+                      N * K < ((int64_t)1 << 31);
+  if (dma_ok) {
+    const size_t shm = W8_NS * 17408;
+    static bool attr = false;
+    if (!attr) {
+      hipError_t e = hipFuncSetAttribute((const void*)k_gemm_w8a8_dma<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)shm);
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)k_gemm_w8a8_dma<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)shm);
+      if (e != hipSuccess) return e;
+      attr = true;
+    }
+    if (f16out)
+      hipLaunchKernelGGL(k_gemm_w8a8_dma<true>, grid, dim3(256), shm, s, xq, xd, wq, wd, M, N, K, y, ldy);
+    else
+      hipLaunchKernelGGL(k_gemm_w8a8_dma<false>, grid, dim3(256), shm, s, xq, xd, wq, wd, M, N, K, y, ldy);
+  } else if (f16out) {
     hipLaunchKernelGGL(k_gemm_w8a8<true>, grid, dim3(256), 0, s, xq, xd, wq, wd, M, N, K, y, ldy);
-  else
+  } else {
     hipLaunchKernelGGL(k_gemm_w8a8<false>, grid, dim3(256), 0, s, xq, xd, wq, wd, M, N, K, y, ldy);
+  }
   return hipGetLastError();
 }
 

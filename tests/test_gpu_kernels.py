@@ -554,14 +554,17 @@ def test_quant_q8_bit_exact(ctx):
             assert list(gq[7, :5]) == [1, 3, -2, 127, 127] and not gq[5, 64:96].any() and gd[5, 2] == 0
 
 
-W8A8_CASES = [(64, 256, 4096), (300, 4096, 4096), (77, 12288, 4096), (128, 4096, 12288), (40, 4096, 64)]
+# K = 96 (3 blocks) takes the product without the DMA path (K not a multiple of 64)
+W8A8_CASES = [(64, 256, 4096), (300, 4096, 4096), (77, 12288, 4096), (128, 4096, 12288), (40, 4096, 64),
+              (50, 256, 96)]
 
 
 @pytest.mark.parametrize("M,N,K", W8A8_CASES)
 def test_mm_w8a8_bit_exact(ctx, M, N, K):
     """exn_mm_w8a8 on exn_quant_q8's codes against the oracle's linear_w8a8, bit for bit (the
-    same exact integer block sums and the same float32 products and sums in the same order):
-    partial tiles in M and N, K of 2 to 384 blocks; fp16 out equal to the fp32 result rounded."""
+    same exact integer block sums, float32 scale products and single-rounding fused
+    multiply-adds in the same order): partial tiles in M and N, K of 2 to 384 blocks, through
+    the DMA path and (K = 96) the direct one; fp16 out equal to the fp32 result rounded."""
     say("mm_w8a8", M, N, K)
     rng = np.random.default_rng(M + N + K)
     x = (rng.normal(0, 1, (M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
