@@ -266,4 +266,17 @@ hipError_t vae_softmax_rows(hipStream_t s, int n, int np, float scale, const flo
 hipError_t vae_pack_conv(hipStream_t s, int64_t o, int ci, int taps, int kp, const float* src, uint16_t* dst);
 hipError_t vae_round_bf16(hipStream_t s, int64_t n, float* x);
 
+// the vision tower (vision.hip), fp32: patches/positions/rotary of a picture, LayerNorm rows,
+// Y = X W^T + bias (+ R) (act 0 none, 1 GELU tanh, 2 GELU erf), heads with the rotary, attention
+hipError_t vis_prep(hipStream_t s, const float* px, int w, int gh, int gw, const float* table, int side, int D,
+                    float* pat, float* pe, float* cs);
+hipError_t vis_ln(hipStream_t s, int64_t rows, int width, const float* x, const float* w, const float* b, float* y);
+hipError_t vis_gemm(hipStream_t s, const float* x, const float* w, const float* bias, const float* r, float* y,
+                    int64_t M, int64_t N, int64_t K, int act);
+hipError_t vis_heads(hipStream_t s, int n, int heads, const float* qkv, const float* cs, float qscale, float* q,
+                     float* k, float* vt);
+hipError_t vis_attend(hipStream_t s, int n, int heads, const float* q, const float* k, const float* vt, float* att);
+hipError_t vis_sum(hipStream_t s, int64_t n, const float* a, const float* b, float* y);
+hipError_t round_f16(hipStream_t s, int64_t n, float* x);
+
 }  // namespace exn

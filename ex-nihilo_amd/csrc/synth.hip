@@ -105,6 +105,12 @@ __global__ void k_dequant(const int8_t* __restrict__ qs, const uint16_t* __restr
   if (bf) bf[i] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
 }
 
+// each value to the nearest fp16 (even on ties, subnormals kept), back as fp32
+__global__ void k_round_f16(int64_t n, float* __restrict__ x) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = f16_to_f32(f16_rne(x[i]));
+}
+
 __global__ void k_f32_to_bf16(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -134,6 +140,12 @@ hipError_t repack_q8_blocks(hipStream_t s, const uint8_t* blocks, int64_t kb, in
 
 hipError_t dequant_q8(hipStream_t s, const int8_t* qs, const uint16_t* d, int64_t n, float* f32, uint16_t* bf16) {
   hipLaunchKernelGGL(k_dequant, dim3(grid_of(n, 256)), dim3(256), 0, s, qs, d, n, f32, bf16);
+  return hipGetLastError();
+}
+
+hipError_t round_f16(hipStream_t s, int64_t n, float* x) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_round_f16, dim3(grid_of(n, 256)), dim3(256), 0, s, n, x);
   return hipGetLastError();
 }
 

@@ -26,7 +26,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "libexn-hip.so")
 
 OK, ENODEV, EINVAL, ENOMEM, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
-Q8_0, F32, BF16 = 8, 0, 30
+Q8_0, F32, BF16, F16 = 8, 0, 30, 1
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 WIDTH, HEADS, HEAD_DIM, FFN, LATENT = 4096, 32, 128, 12288, 64
 # Qwen-Image-2.1-Turbo's schedule (src/generate.lisp:7-9)
@@ -113,6 +113,20 @@ SIGNATURES = {
                              c_int64]),
     "exn_vae_rms_silu": (c_int, [vp, c_int64, c_int, vp, vp, vp, c_int]),
     "exn_vae_dupup_add": (c_int, [vp, c_int, c_int, c_int, c_int, c_int, vp, vp]),
+    "exn_vision_create": (c_int, [vp, POINTER(vp)]),
+    "exn_vision_set": (c_int, [vp, c_char_p, c_int, vp, POINTER(c_int64), c_int]),
+    "exn_vision_synth": (c_int, [vp, c_uint64]),
+    "exn_vision_check": (c_int, [vp]),
+    "exn_vision_encode": (c_int, [vp, vp, c_int, c_int, vp, vp]),
+    "exn_vision_encode_dev": (c_int, [vp, vp, c_int, c_int, vp, vp]),
+    "exn_vision_trace": (c_int, [vp, c_int]),
+    "exn_vision_traced": (c_int, [vp, c_int, vp]),
+    "exn_vision_release": (c_int, [vp]),
+    "exn_vision_destroy": (c_int, [vp]),
+    "exn_vision_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
+    "exn_vis_gemm": (c_int, [vp, vp, vp, vp, vp, vp, c_int64, c_int64, c_int64, c_int]),
+    "exn_vis_attend": (c_int, [vp, c_int, c_int, vp, vp, vp, vp]),
+    "exn_vis_ln": (c_int, [vp, c_int64, c_int, vp, vp, vp, vp]),
 }
 
 
@@ -496,4 +510,84 @@ def vae_decode(v: Vae, latent: np.ndarray, h: int, w: int):
 
 def vae_release(v: Vae):
     """vae-release (src/cuda-vae.lisp:28-33): the scratch freed."""
+    v.release()
+
+
+# --- the vision tower: load-vision, vision-encode, vision-release (src/cuda-vision.lisp) -----
+
+VISION_WIDTH, VISION_OUT = 1152, 4096
+
+
+class Vision:
+    """Qwen3-VL's vision tower on the device: its tensors and scratch (q3vision)."""
+
+    def __init__(self, ctx: Context):
+        h = vp()
+        call("exn_vision_create", ctx.h, ctypes.byref(h))
+        self.ctx, self.h = ctx, h
+
+    def set(self, name: str, kind: int, data: np.ndarray, shape):
+        """One tensor by its GGUF name and row-major shape (F16 / BF16 bit patterns as uint16, or F32)."""
+        dims = (c_int64 * len(shape))(*shape)
+        call("exn_vision_set", self.h, name.encode(), kind, ptr(np.ascontiguousarray(data)), dims, len(shape))
+
+    def synth(self, seed: int):
+        call("exn_vision_synth", self.h, seed)
+
+    def check(self):
+        call("exn_vision_check", self.h)
+
+    def trace(self, on: bool):
+        call("exn_vision_trace", self.h, 1 if on else 0)
+
+    def traced(self, which: int, n: int):
+        """After a traced encode of N patches: the rows after the embedding (0) or block 0 (1)."""
+        out = np.empty((n, VISION_WIDTH), np.float32)
+        call("exn_vision_traced", self.h, which, ptr(out))
+        return out
+
+    def memory(self):
+        w, s = c_int64(), c_int64()
+        call("exn_vision_memory", self.h, ctypes.byref(w), ctypes.byref(s))
+        return w.value, s.value
+
+    def release(self):
+        call("exn_vision_release", self.h)
+
+    def destroy(self):
+        if self.h:
+            call("exn_vision_destroy", self.h)
+            self.h = None
+
+
+def load_vision(tensors=None, *, device: int = 0, seed: int | None = None, ctx=None) -> Vision:
+    """load-vision (src/cuda-vision.lisp:15-30): TENSORS an iterable of (name, kind,
+    data, shape) as read from the mmproj GGUF, or SEED: the synthetic tower made on
+    the device.  Checked against the tower's tensor list before return."""
+    ctx = ctx or Context(device)
+    v = Vision(ctx)
+    if seed is not None:
+        v.synth(seed)
+    for name, kind, data, shape in tensors or ():
+        v.set(name, kind, data, shape)
+    v.check()
+    return v
+
+
+def vision_encode(v: Vision, px: np.ndarray, h: int, w: int):
+    """vision-encode (src/cuda-vision.lisp:34-101): PX (H x W x 4 floats, RGBA in
+    -1..1; H, W multiples of 32) -> (merged M x 4096, deepstack 3 x M x 4096, M),
+    M = H W / 1024, rows in merge-block order."""
+    p = np.ascontiguousarray(px, dtype=np.float32).reshape(-1)
+    if p.size != h * w * 4:
+        raise ExnError(EINVAL, "picture of %d floats for %d x %d RGBA" % (p.size, h, w))
+    m = (h // 32) * (w // 32)
+    merged = np.empty((m, VISION_OUT), np.float32)
+    deep = np.empty((3, m, VISION_OUT), np.float32)
+    call("exn_vision_encode", v.h, ptr(p), h, w, ptr(merged), ptr(deep))
+    return merged, deep, m
+
+
+def vision_release(v: Vision):
+    """vision-release (src/cuda-vision.lisp:103-107): the scratch freed."""
     v.release()

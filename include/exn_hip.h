@@ -43,6 +43,7 @@ extern "C" {
 #define EXN_Q8_0 8
 #define EXN_F32 0
 #define EXN_BF16 30
+#define EXN_F16 1     /* the vision tower's tensors only (mmproj-f16.gguf) */
 
 /* activation dtypes of the op-level entry points */
 #define EXN_DT_F32 0
@@ -286,6 +287,52 @@ int exn_vae_conv(exn_ctx* ctx, int taps, int up, int outdt, const uint16_t* x, c
                  const float* res, void* y, int h, int w, int c, int cout, int kp, float* part, int64_t part_cap);
 int exn_vae_rms_silu(exn_ctx* ctx, int64_t n, int c, const float* x, const float* gamma, uint16_t* y, int silu);
 int exn_vae_dupup_add(exn_ctx* ctx, int cin, int cout, int ft, int h, int w, const float* x, float* y);
+
+/* --- the vision tower (replaces src/cuda-vision.lisp's q3vision and src/cuda/qvision.cu) -----
+ * Qwen3-VL's ViT, which lets the prompt encoder see a picture to edit: 27 blocks of 1152, 16
+ * heads of 72, FFN 4304, a learned 48 x 48 position table resampled to the picture's grid, a 2-D
+ * rotary, patches of 16 px in 2 x 2 merge blocks; the merger (four patches to one row of 4096)
+ * and three deepstack mergers after blocks 8, 16 and 24.  fp32 throughout, as the reference. */
+typedef struct exn_vision exn_vision;
+/* load-vision (src/cuda-vision.lisp:15-30) in parts: create, then one exn_vision_set a tensor */
+int exn_vision_create(exn_ctx* ctx, exn_vision** out);
+/* one tower tensor by its GGUF name (inspect/ref_vision.py's names) and row-major shape (NDIMS
+ * dims, a matrix (out, in)), KIND EXN_F32, EXN_F16 or EXN_BF16; kept as fp32 (il::load-f32).
+ * v.position_embd.weight is (S, 1152) for a square S (48 x 48 in the model); the two patch
+ * kernels (v.patch_embd.weight and .weight.1, one frame given twice) are summed, as
+ * vision-tensors does (src/host.lisp:175-190). */
+int exn_vision_set(exn_vision* v, const char* name, int kind, const void* data, const int64_t* dims, int ndims);
+/* test hook: every tower tensor from the synthetic generator (matrices fp16-valued) */
+int exn_vision_synth(exn_vision* v, uint64_t seed);
+/* EXN_OK when every tower tensor is present, else EXN_ESTATE naming the first missing one */
+int exn_vision_check(exn_vision* v);
+/* vision-encode (src/cuda-vision.lisp:34-101): PX, the picture (H x W x 4 floats, RGBA in
+ * -1 .. 1, rows of pixels; H and W multiples of 32, H W / 256 patches at most 16384) ->
+ * MERGED (M x 4096 floats, M = H W / 1024, in merge-block order: the 32-pixel grid row-major)
+ * and DEEPSTACK (3 x M x 4096: after blocks 8, 16, 24).  Host arrays; exn_vision_encode_dev
+ * takes device arrays, on the context's stream. */
+int exn_vision_encode(exn_vision* v, const float* px, int h, int w, float* merged, float* deepstack);
+int exn_vision_encode_dev(exn_vision* v, const float* px, int h, int w, float* merged, float* deepstack);
+/* test hook: with ON, each encode keeps the patch rows after the embedding (WHICH 0) and after
+ * block 0 (WHICH 1), N x 1152 floats, which exn_vision_traced copies to host memory OUT
+ * (ref_vision.py's embed.f32 and blk0.f32) */
+int exn_vision_trace(exn_vision* v, int on);
+int exn_vision_traced(exn_vision* v, int which, float* out);
+/* vision-release (src/cuda-vision.lisp:103-107): scratch freed, weights kept */
+int exn_vision_release(exn_vision* v);
+int exn_vision_destroy(exn_vision* v);
+/* bytes of device memory the tower holds: weights, scratch */
+int exn_vision_memory(exn_vision* v, int64_t* weights, int64_t* scratch);
+/* the tower's kernels one at a time (device arrays, fp32).  exn_vis_gemm: Y (M x N) = X (M x K)
+ * W^T (W: N x K) + BIAS (+ R, M x N, may be Y), then ACT (0 none, 1 GELU tanh form, 2 GELU erf
+ * form): d41_mm_f32 with v_bias and v_gelu / x_gelu_tanh; K a multiple of 4, X and W 16-byte
+ * aligned.  exn_vis_attend: softmax attention of N patches (a multiple of 4) over themselves,
+ * HEADS heads of 72: Q and K [head][N][72] (Q scaled by log2(e)/sqrt(72)), VT [head][72][N],
+ * ATT [N][HEADS x 72].  exn_vis_ln: LayerNorm of ROWS rows of WIDTH (eps 1e-6, q3v_layernorm). */
+int exn_vis_gemm(exn_ctx* ctx, const float* x, const float* w, const float* bias, const float* r, float* y, int64_t m,
+                 int64_t n, int64_t k, int act);
+int exn_vis_attend(exn_ctx* ctx, int n, int heads, const float* q, const float* k, const float* vt, float* att);
+int exn_vis_ln(exn_ctx* ctx, int64_t rows, int width, const float* x, const float* w, const float* b, float* y);
 
 #ifdef __cplusplus
 }
