@@ -36,6 +36,15 @@ final latent, 64 x 64 -> a 1024 x 1024 RGBA picture, the mean of 5 decodes.
 
 times the VAE decoder alone on a seeded 64 x 64 latent (K decodes after W) and
 prints its own JSON line.
+
+vision_encode_1024sq: the vision tower (Qwen3-VL's ViT, synthetic fp16-valued
+weights, fp32 arithmetic) on a 1024 x 1024 RGBA picture in HBM: 4096 patches
+through 27 blocks and the four mergers, the mean of 3 encodes; its rate against
+the dense fp32 MFMA peak (157.3 TFLOP/s).
+
+    python bench.py --vision-only [--steps K] [--warmup W]
+
+times the tower alone and prints its own JSON line.
 """
 import argparse
 import json
@@ -58,6 +67,7 @@ SEED = 2
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_1024sq_traffic.json")
 TRAFFIC_FILE_Q8 = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_q8_0_1024sq_traffic.json")
 PROBE_BYTES = 1 << 30         # --copy-probe 1024
+PEAK_F32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 VAE_FLOP = 17.03e12           # one decode of a 64 x 64 latent: every convolution and the attention's products
 
 
@@ -312,6 +322,59 @@ def vae_only(steps, warmup):
                       "ref_rtx3090_ms": 1500.0}), flush=True)
 
 
+def vision_flop(n, d=1152, f=4304, depth=27, out=4096):
+    """Multiply-add FLOPs of one vision encode of N patches: the patch embedding, each block's
+    four products and attention's two (n x n x d each), the four mergers' two products."""
+    m = n // 4
+    blocks = depth * (2 * n * d * (3 * d + d + 2 * f) + 4 * n * n * d)
+    return 2 * n * d * 768 + blocks + 4 * 2 * m * (4 * d * 4 * d + 4 * d * out)
+
+
+def vision_time(ctx, reps, warmup, hh=1024, ww=1024):
+    """The tower on a seeded hh x ww RGBA picture already in HBM: (ms an encode, finite, weights GB,
+    scratch GB)."""
+    import exn_hip as X
+    rng = np.random.default_rng(SEED)
+    vis = X.load_vision(seed=SEED, ctx=ctx)
+    px = X.DevBuf.of(ctx, np.clip(rng.normal(0, 0.5, (hh, ww, 4)), -1, 1).astype(np.float32))
+    m = (hh // 32) * (ww // 32)
+    out = X.DevBuf(ctx, (4, m, 4096), np.float32)
+    run = lambda: X.call("exn_vision_encode_dev", vis.h, px.h, hh, ww, out.h, out.at(m * 4096 * 4))
+    for i in range(warmup):
+        run()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(reps):
+        run()
+    ctx.sync()
+    t = (time.perf_counter() - t0) / reps
+    finite = bool(np.isfinite(out.get()).all())
+    w, sc = vis.memory()
+    vis.destroy()
+    return t, finite, w / 1e9, sc / 1e9
+
+
+def vision_record(t, finite, w_gb, s_gb, n=4096):
+    fl = vision_flop(n)
+    return {"ms": round(t * 1e3, 2), "tflop": round(fl / 1e12, 3), "tflops": round(fl / t / 1e12, 1),
+            "f32_mfma_peak_frac": round(fl / t / 1e12 / PEAK_F32_TFLOPS, 4), "patches": n, "out_rows": n // 4,
+            "outputs_finite": finite, "weights_gb": round(w_gb, 3), "scratch_gb": round(s_gb, 2)}
+
+
+def vision_only(steps, warmup):
+    """The vision tower alone: a seeded 1024 x 1024 RGBA picture in HBM -> merged + deepstack rows."""
+    import exn_hip as X
+    ctx = X.Context(0)
+    t, finite, w_gb, s_gb = vision_time(ctx, steps, warmup)
+    ctx.close()
+    rec = vision_record(t, finite, w_gb, s_gb)
+    print(json.dumps(dict({"metric": "vision encode ms @1024² (4096 patches, 27 blocks + 4 mergers), 1 GPU",
+                           "value": rec["ms"], "unit": "ms/encode", "n_gpus": 1, "steps": steps, "warmup": warmup,
+                           "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+                           "config": {"workload": "vision-encode-1024x1024", "weights": "fp16-valued synthetic, fp32",
+                                      "seed": SEED}}, **rec)), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,6 +382,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--vae-only", action="store_true", help="time the VAE decoder alone")
+    ap.add_argument("--vision-only", action="store_true", help="time the vision tower alone")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="copy MIB MiB device to device after the set-up (the traffic counters' calibration)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
@@ -346,6 +410,9 @@ def main():
         print("bench.py: the step runs on one GPU; --gpus %d is not supported (a split of the image rows "
               "across GPUs is designed, not built)" % a.gpus, file=sys.stderr)
         sys.exit(2)
+    if a.vision_only:
+        vision_only(a.steps, a.warmup)
+        return
     if a.vae_only:
         vae_only(a.steps, a.warmup)
         return
@@ -494,6 +561,9 @@ def main():
     px = pic.get()
     vae_w, vae_s = vae.memory()
     vae.destroy()
+
+    # the vision tower (editing's picture, seen by the prompt encoder) on a 1024 x 1024 picture
+    vis = vision_record(*vision_time(ctx, 3, 1))
 
     # the 1536 x 1024 and edit workloads on the same weights: cached and uncached steps
     def workload_times(hh, ww, ptext, ref, reps=3):
@@ -651,6 +721,7 @@ def main():
                               "picture_finite": bool(np.isfinite(px).all()),
                               "weights_gb": round(vae_w / 1e9, 3), "scratch_gb": round(vae_s / 1e9, 2),
                               "ref_rtx3090_ms": 1500.0},
+        "vision_encode_1024sq": vis,
         "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights (resident expansion of Q8_0)",
                      "achieved": round(achieved, 1) if achieved else None, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4) if achieved else None, "traffic": traffic,

@@ -50,8 +50,8 @@ def gelu_erf64(x):
 
 
 GEMM_CASES = [  # M, N, K, act, residual
-    (64, 1152, 1152, 0, False),        # 64 x 64 tiles
-    (2048, 4304, 1152, 1, False),      # 128 x 128 tiles, an N tail (4304 = 33 x 128 + 80), GELU tanh
+    (64, 1152, 1152, 0, False),        # one row of 64 x 64 tiles
+    (2048, 4304, 1152, 1, False),      # an N tail (4304 = 67 x 64 + 16), GELU tanh
     (256, 1152, 4304, 0, True),        # K not a multiple of 32 (the ffn_down shape), residual
     (100, 200, 68, 2, True),           # M, N, K tails everywhere, GELU erf
     (16, 4096, 4608, 0, False),        # a merger's fc2 for one merge row of a small picture

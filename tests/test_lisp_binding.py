@@ -1,8 +1,9 @@
-"""The SBCL binding (ex-nihilo_amd/lisp/hip-dit.lisp, hip-vae.lisp) against the C ABI, without
+"""The SBCL binding (ex-nihilo_amd/lisp/hip-dit.lisp, hip-vae.lisp, hip-vision.lisp) against the C ABI, without
 SBCL (neither this image nor the GPU host has it): every define-alien-routine names a function
 that include/exn_hip.h declares, with its arity and, argument by argument, a Lisp alien type
 that passes the C type (int, 64-bit integers, double, pointers, C strings); and the backend trio
-keeps the reference's lambda lists (src/cuda-dit.lisp:52,137,99; src/cuda-vae.lisp:15,94,28)."""
+keeps the reference's lambda lists (src/cuda-dit.lisp:52,137,99; src/cuda-vae.lisp:15,94,28;
+src/cuda-vision.lisp:15,34,103)."""
 import os
 import re
 
@@ -11,6 +12,7 @@ import pytest
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LISP = os.path.join(REPO, "ex-nihilo_amd", "lisp")
 HEADER = os.path.join(REPO, "include", "exn_hip.h")
+FILES = ("hip-dit.lisp", "hip-vae.lisp", "hip-vision.lisp")
 
 
 def prototypes():
@@ -52,7 +54,7 @@ def forms(name):
 
 def alien_routines():
     out = {}
-    for f in ("hip-dit.lisp", "hip-vae.lisp"):
+    for f in FILES:
         for form in forms(f):
             if isinstance(form, list) and form and form[0] == "sb-alien:define-alien-routine":
                 cname = form[1][0].strip('"')
@@ -94,7 +96,7 @@ def test_every_alien_routine_matches_the_header():
 
 def test_the_trio_keeps_the_reference_lambda_lists():
     defs = {}
-    for f in ("hip-dit.lisp", "hip-vae.lisp"):
+    for f in FILES:
         for form in forms(f):
             if isinstance(form, list) and form and form[0] == "defun":
                 defs[form[1]] = form[2]
@@ -105,6 +107,9 @@ def test_the_trio_keeps_the_reference_lambda_lists():
     assert defs["upload-vae"] == ["path", "&key", ["device", "0"]]
     assert defs["vae-decode"] == ["v", "latent", "h", "w"]
     assert defs["vae-release"] == ["v"]
+    assert defs["load-vision"] == ["path", "&key", ["device", "1"]]
+    assert defs["vision-encode"] == ["v", "px", "h", "w"]
+    assert defs["vision-release"] == ["v"]
 
 
 def test_the_header_parse_sees_the_trio():
@@ -114,7 +119,7 @@ def test_the_header_parse_sees_the_trio():
     assert p["exn_last_error"] == ("const char*", [])
 
 
-@pytest.mark.parametrize("name", ["hip-dit.lisp", "hip-vae.lisp"])
+@pytest.mark.parametrize("name", FILES)
 def test_files_parse_and_stay_in_the_package(name):
     fs = forms(name)
     assert fs[0] == ["in-package", "#:ex-nihilo"]
