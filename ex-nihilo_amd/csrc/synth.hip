@@ -76,9 +76,11 @@ __global__ void k_synth_normal(uint64_t key, int64_t n, float base, float scale,
 #pragma clang fp contract(off)
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float z = __fmul_rn((float)sum2(word(key, (uint64_t)i)), 1.3214498960651507e-05f);
-  const float v = __fmul_rn(scale, z);
-  out[i] = add_base ? __fadd_rn(base, v) : v;
+  // plain operators: under the pragma they stay a rounded product and a rounded sum (the
+  // __fmul_rn / __fadd_rn intrinsics inline without it, and were fused into one v_fma_f32)
+  const float z = (float)sum2(word(key, (uint64_t)i)) * 1.3214498960651507e-05f;
+  const float v = scale * z;
+  out[i] = add_base ? base + v : v;
 }
 
 // GGUF block_q8_0 rows (34 bytes a block) -> qs, d; row r to row_map[r]

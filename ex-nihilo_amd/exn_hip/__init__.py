@@ -127,6 +127,16 @@ SIGNATURES = {
     "exn_vis_gemm": (c_int, [vp, vp, vp, vp, vp, vp, c_int64, c_int64, c_int64, c_int]),
     "exn_vis_attend": (c_int, [vp, c_int, c_int, vp, vp, vp, vp]),
     "exn_vis_ln": (c_int, [vp, c_int64, c_int, vp, vp, vp, vp]),
+    "exn_enc_create": (c_int, [vp, c_int, c_double, POINTER(vp)]),
+    "exn_enc_set": (c_int, [vp, c_char_p, c_int, vp, c_int64, c_int64]),
+    "exn_enc_synth": (c_int, [vp, c_uint64, c_int64]),
+    "exn_enc_check": (c_int, [vp]),
+    "exn_enc_states": (c_int, [vp, vp, c_int, vp, c_int, c_int, vp, vp, vp]),
+    "exn_enc_states_dev": (c_int, [vp, vp, c_int, vp, c_int, c_int, vp, vp, vp]),
+    "exn_enc_rope_table": (c_int, [vp, c_int, c_double, vp]),
+    "exn_enc_release": (c_int, [vp]),
+    "exn_enc_destroy": (c_int, [vp]),
+    "exn_enc_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
 }
 
 
@@ -591,3 +601,82 @@ def vision_encode(v: Vision, px: np.ndarray, h: int, w: int):
 def vision_release(v: Vision):
     """vision-release (src/cuda-vision.lisp:103-107): the scratch freed."""
     v.release()
+
+
+# --- the prompt encoder: load-encoder, encoder-states (src/encoder.lisp) -------------------
+
+ENC_ROPE_BASE = 5e6
+
+
+class Encoder:
+    """Qwen3-VL-8B's text model on the device (illatio's model, for encoder-states)."""
+
+    def __init__(self, ctx: Context, layers: int = 36, rope_base: float = ENC_ROPE_BASE):
+        h = vp()
+        call("exn_enc_create", ctx.h, layers, rope_base, ctypes.byref(h))
+        self.ctx, self.h, self.layers = ctx, h, layers
+
+    def set(self, name: str, kind: int, data: np.ndarray, d0: int, d1: int):
+        """One tensor by its GGUF name and ggml dims (Q8_0 block records as uint8, or F32)."""
+        call("exn_enc_set", self.h, name.encode(), kind, ptr(np.ascontiguousarray(data)), d0, d1)
+
+    def synth(self, seed: int, vocab: int = 8192):
+        call("exn_enc_synth", self.h, seed, vocab)
+
+    def check(self):
+        call("exn_enc_check", self.h)
+
+    def memory(self):
+        w, s = c_int64(), c_int64()
+        call("exn_enc_memory", self.h, ctypes.byref(w), ctypes.byref(s))
+        return w.value, s.value
+
+    def release(self):
+        call("exn_enc_release", self.h)
+
+    def destroy(self):
+        if self.h:
+            call("exn_enc_destroy", self.h)
+            self.h = None
+
+
+def load_encoder(tensors=None, *, device: int = 0, layers: int = 36, seed: int | None = None, vocab: int = 8192,
+                 ctx=None) -> Encoder:
+    """load-encoder (src/encoder.lisp:41-48): TENSORS an iterable of (name, kind, data, d0,
+    d1) as read from te-q8_0.gguf, or SEED: the synthetic model made on the device."""
+    ctx = ctx or Context(device)
+    e = Encoder(ctx, layers)
+    if seed is not None:
+        e.synth(seed, vocab)
+    for name, kind, data, d0, d1 in tensors or ():
+        e.set(name, kind, data, d0, d1)
+    e.check()
+    return e
+
+
+def encoder_states(e: Encoder, ids, pos=None, picture=None):
+    """encoder-states (src/encoder.lisp:143-183): every token's state after the last block,
+    before the final norm, (n, 4096).  POS: (n, 3) (t, h, w) positions or None (text 0..n-1);
+    PICTURE: (a0, merged (m, 4096), deep (3, m, 4096) or None) -- the picture's rows."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    n = len(ids)
+    p = None if pos is None else np.ascontiguousarray(pos, dtype=np.int32).reshape(n, 3)
+    out = np.empty((n, WIDTH), np.float32)
+    if picture is None:
+        call("exn_enc_states", e.h, ptr(ids), n, None if p is None else ptr(p), 0, 0, None, None, ptr(out))
+    else:
+        a0, merged, deep = picture
+        mg = np.ascontiguousarray(merged, dtype=np.float32)
+        dp = None if deep is None else np.ascontiguousarray(deep, dtype=np.float32)
+        call("exn_enc_states", e.h, ptr(ids), n, None if p is None else ptr(p), a0, len(mg), ptr(mg),
+             None if dp is None else ptr(dp), ptr(out))
+    return out
+
+
+def enc_rope_table(n: int, pos=None, base: float = ENC_ROPE_BASE):
+    """mrope-table (src/encoder.lisp:26-39) as the library computes it (host only): (n, 128),
+    cos and sin of pair j at columns 2j, 2j + 1."""
+    cs = np.empty((n, 128), np.float32)
+    p = None if pos is None else np.ascontiguousarray(pos, dtype=np.int32).reshape(n, 3)
+    call("exn_enc_rope_table", None if p is None else ptr(p), n, base, ptr(cs))
+    return cs

@@ -334,6 +334,45 @@ int exn_vis_gemm(exn_ctx* ctx, const float* x, const float* w, const float* bias
 int exn_vis_attend(exn_ctx* ctx, int n, int heads, const float* q, const float* k, const float* vt, float* att);
 int exn_vis_ln(exn_ctx* ctx, int64_t rows, int width, const float* x, const float* w, const float* b, float* y);
 
+/* --- the prompt encoder (replaces illatio's qwen3 forward under src/encoder.lisp:41-67,143-183) ---
+ * Qwen3-VL-8B's text model read for every token's state after its last block, before the final
+ * norm: 36 layers of 4096, 32 query heads and 8 key/value heads of 128, FFN 12288 (SwiGLU),
+ * RMSNorm eps 1e-6 (and over each head of q and k), RoPE theta 5e6 with interleaved M-RoPE,
+ * causal.  Tokenizing stays the host's (il::tokenize). */
+typedef struct exn_enc exn_enc;
+/* load-encoder (src/encoder.lisp:41-48) in parts: an empty encoder of LAYERS blocks (36; fewer to
+ * look at part of the model) with the model's RoPE base (il::model-rope-base, 5e6) */
+int exn_enc_create(exn_ctx* ctx, int layers, double rope_base, exn_enc** out);
+/* one tensor of te-q8_0.gguf by its name (token_embd.weight, blk.N.attn_norm / attn_q / attn_k /
+ * attn_v / attn_output / attn_q_norm / attn_k_norm / ffn_norm / ffn_gate / ffn_up / ffn_down
+ * .weight) and ggml dims D0 (contiguous) x D1 (1 for a vector): matrices EXN_Q8_0 (block_q8_0
+ * records; token_embd also EXN_F32), norm weights EXN_F32.  output_norm.weight and output.weight
+ * are accepted and not kept (the states are read before them). */
+int exn_enc_set(exn_enc* e, const char* name, int kind, const void* data, int64_t d0, int64_t d1);
+/* test hook: every tensor from the synthetic generator, a token embedding of VOCAB rows */
+int exn_enc_synth(exn_enc* e, uint64_t seed, int64_t vocab);
+/* EXN_OK when every tensor is present, else EXN_ESTATE naming the first missing one */
+int exn_enc_check(exn_enc* e);
+/* encoder-states (src/encoder.lisp:143-183) with call-with-picture-rows (:69-110): IDS (N token
+ * ids), POS (N (t, h, w) triples, or NULL for text positions 0 .. N-1; mrope-table, :26-39);
+ * when M > 0 rows PIC0 .. PIC0 + M - 1 take MERGED's rows (M x 4096, the vision tower's) after
+ * the embedding and DEEP's set j (3 x M x 4096, or NULL) added after layer j; OUT: N x 4096
+ * floats.  Host arrays.  exn_enc_states_dev takes device arrays and the rotary table CS
+ * (exn_enc_rope_table's N x 128 floats) in place of POS, on the context's stream. */
+int exn_enc_states(exn_enc* e, const int32_t* ids, int n, const int32_t* pos, int pic0, int m, const float* merged,
+                   const float* deep, float* out);
+int exn_enc_states_dev(exn_enc* e, const int32_t* ids, int n, const float* cs, int pic0, int m, const float* merged,
+                       const float* deep, float* out);
+/* mrope-table (src/encoder.lisp:26-39) on the host, no GPU needed: row t's frequency j < 64 turns
+ * by its position on axis j mod 3 (t, h, w) below 60, by t above, at BASE^(-2j/128); the cos and
+ * sin of pair j at CS[128 t + 2j] and [128 t + 2j + 1] (rotate_half's dims j and j + 64). */
+int exn_enc_rope_table(const int32_t* pos, int n, double base, float* cs);
+/* scratch freed, weights kept; destroy frees both */
+int exn_enc_release(exn_enc* e);
+int exn_enc_destroy(exn_enc* e);
+/* bytes of device memory the encoder holds: weights, scratch */
+int exn_enc_memory(exn_enc* e, int64_t* weights, int64_t* scratch);
+
 #ifdef __cplusplus
 }
 #endif

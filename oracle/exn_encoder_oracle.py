@@ -81,8 +81,8 @@ class SynthEncoder:
     """wt(name) -> fp32: matrices Q8_0 from the counter generator, dequantised exactly;
     norm weights 1 + 0.05 z.  Tensor id: ENC_ID0 + its index in enc_expected for 36 layers."""
 
-    def __init__(self, seed, s: EShape = EShape()):
-        self.seed, self.s = seed, s
+    def __init__(self, seed, s: EShape = EShape(), keep=True):
+        self.seed, self.s, self.keep = seed, s, keep
         full = EShape(s.width, 36, s.heads, s.kv_heads, s.head_dim, s.ffn, s.vocab)
         self.ids = {n: ENC_ID0 + i for i, (n, _) in enumerate(enc_expected(full))}
         self.shapes = dict(enc_expected(s))
@@ -99,6 +99,8 @@ class SynthEncoder:
                 v = np.float32(1.0) + np.float32(0.05) * xo.normal(self.seed, self.ids[name], shape[0])
             else:
                 v = xo.dequant_fast(*self.q8(name))
+            if not self.keep and len(shape) > 1 and name != "token_embd.weight":
+                return v          # full depth: a layer's matrices made again when read
             self.cache[name] = v
         return self.cache[name]
 
@@ -161,26 +163,40 @@ def silu(x):
 
 # --- the forward ----------------------------------------------------------------------------
 
-def layer(wt, i, x, cos, sin, s: EShape = EShape()):
-    """Block i of the text model on rows x (n, width): causal grouped-query attention, SwiGLU."""
+def _keep(x):
+    return x
+
+
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def layer(wt, i, x, cos, sin, s: EShape = EShape(), bf16=False):
+    """Block i of the text model on rows x (n, width): causal grouped-query attention, SwiGLU.
+    BF16: round where the GPU's products and attention round (matrices and the products'
+    inputs to bf16, q, k, v to fp16) -- a model of that arithmetic, to tell its rounding from
+    a mistake; the restatement of the model is BF16 false."""
+    rb, rh = (xo.bf16_round, _f16) if bf16 else (_keep, _keep)
+    w = lambda name: rb(wt(name))
     p = "blk.%d." % i
     n = x.shape[0]
-    h = rmsnorm(x, wt(p + "attn_norm.weight"))
-    q = (h @ wt(p + "attn_q.weight").T).reshape(n, s.heads, s.head_dim)
-    k = (h @ wt(p + "attn_k.weight").T).reshape(n, s.kv_heads, s.head_dim)
-    v = (h @ wt(p + "attn_v.weight").T).reshape(n, s.kv_heads, s.head_dim)
-    q = rope_half(rmsnorm(q, wt(p + "attn_q_norm.weight")), cos, sin)
-    k = rope_half(rmsnorm(k, wt(p + "attn_k_norm.weight")), cos, sin)
+    h = rb(rmsnorm(x, wt(p + "attn_norm.weight")))
+    q = (h @ w(p + "attn_q.weight").T).reshape(n, s.heads, s.head_dim)
+    k = (h @ w(p + "attn_k.weight").T).reshape(n, s.kv_heads, s.head_dim)
+    v = (h @ w(p + "attn_v.weight").T).reshape(n, s.kv_heads, s.head_dim)
+    q = rh(rope_half(rmsnorm(q, wt(p + "attn_q_norm.weight")), cos, sin))
+    k = rh(rope_half(rmsnorm(k, wt(p + "attn_k_norm.weight")), cos, sin))
+    v = rh(v)
     g = s.heads // s.kv_heads
     k, v = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)          # query head h reads kv head h // g
-    att = xo.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), 0, n)
-    x = x + att.reshape(n, s.width) @ wt(p + "attn_output.weight").T
-    h = rmsnorm(x, wt(p + "ffn_norm.weight"))
-    ff = silu(h @ wt(p + "ffn_gate.weight").T) * (h @ wt(p + "ffn_up.weight").T)
-    return (x + ff @ wt(p + "ffn_down.weight").T).astype(np.float32)
+    att = rb(xo.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), 0, n))
+    x = x + att.reshape(n, s.width) @ w(p + "attn_output.weight").T
+    h = rb(rmsnorm(x, wt(p + "ffn_norm.weight")))
+    ff = rb(silu(h @ w(p + "ffn_gate.weight").T) * (h @ w(p + "ffn_up.weight").T))
+    return (x + ff @ w(p + "ffn_down.weight").T).astype(np.float32)
 
 
-def states(wt, ids, pos3=None, picture=None, s: EShape = EShape(), base=ROPE_BASE):
+def states(wt, ids, pos3=None, picture=None, s: EShape = EShape(), base=ROPE_BASE, bf16=False):
     """encoder-states (src/encoder.lisp:143-183): every token's state after the last block,
     before the final norm, (n, width).  POS3: (n, 3) positions, text positions 0.. when
     None.  PICTURE: (a0, merged (m, width), deep (3, m, width)) -- rows a0 .. a0 + m - 1
@@ -193,7 +209,7 @@ def states(wt, ids, pos3=None, picture=None, s: EShape = EShape(), base=ROPE_BAS
         x[a0:a0 + len(merged)] = merged
     cos, sin = mrope_tables(text_positions(n) if pos3 is None else pos3, base, s.head_dim)
     for i in range(s.layers):
-        x = layer(wt, i, x, cos, sin, s)
+        x = layer(wt, i, x, cos, sin, s, bf16)
         if picture is not None and i < len(deep):
             x[a0:a0 + len(merged)] += deep[i]
     return x

@@ -1,0 +1,142 @@
+"""The prompt encoder (Qwen3-VL-8B's text model) on the GPU through the C ABI, against the
+oracle (oracle/exn_encoder_oracle.py; parity unpinned against illatio, whose arithmetic the
+reference does not vendor).  The products take bf16 activations and the Q8_0 weights
+dequantised to bf16, attention fp16 operands, as the DiT's blocks do.  Through the text
+model's attention (no gates: every block's output is the residual's bulk) that rounding
+leaves the states about 1% from the fp32 oracle after 2 blocks and 2.3% after 36, and an
+oracle that rounds at the same points lands as far: the bar is relative L2 1.5e-2 for 2
+blocks, 3e-2 for all 36, with the rounding model checked beside it.  Needs an MI355X."""
+import sys
+
+import numpy as np
+import pytest
+
+import exn_hip as X
+from oracle import exn_encoder_oracle as eo
+from oracle import exn_oracle as xo
+
+pytestmark = pytest.mark.gpu
+SEED = 31
+VOCAB = 8192
+
+
+def say(*a):
+    print("[gpu]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = X.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def enc2(ctx):
+    say("encoder synth, 2 layers")
+    e = X.load_encoder(seed=SEED, layers=2, vocab=VOCAB, ctx=ctx)
+    yield e
+    e.destroy()
+
+
+@pytest.fixture(scope="module")
+def owt2():
+    return eo.SynthEncoder(SEED, eo.EShape(layers=2))
+
+
+@pytest.mark.parametrize("n", [1, 37, 300])
+def test_states_two_layers_against_oracle(enc2, owt2, n):
+    say("encoder states, 2 layers, n", n)
+    ids = eo.synth_ids(SEED + n, n, VOCAB)
+    got = X.encoder_states(enc2, ids)
+    want = eo.states(owt2, ids, s=eo.EShape(layers=2))
+    err = xo.rel_l2(got, want)
+    say("rel l2", err)
+    assert err < 1.5e-2
+    assert np.isfinite(got).all()
+
+
+def test_states_of_an_edit_prompt(enc2, owt2):
+    """5 text tokens, a 4 x 6 picture's rows (merged, and deepstack added after layers 0 and
+    1), 9 more: positions and picture rows as encode-edit-prompt gives them."""
+    a0, gh, gw, after = 5, 4, 6, 9
+    pos = eo.edit_positions(a0, gh, gw, after)
+    n = len(pos)
+    ids = eo.synth_ids(SEED + 1, n, VOCAB)
+    merged, deep = eo.synth_picture_rows(SEED + 2, gh * gw)
+    got = X.encoder_states(enc2, ids, pos, (a0, merged, deep))
+    want = eo.states(owt2, ids, pos, (a0, merged, deep), s=eo.EShape(layers=2))
+    err = xo.rel_l2(got, want)
+    say("edit rel l2", err)
+    assert err < 1.5e-2
+    plain = X.encoder_states(enc2, ids)
+    assert xo.rel_l2(plain[a0 + gh * gw:], got[a0 + gh * gw:]) > 1e-2     # the picture is seen after it
+
+
+def test_set_from_gguf_records_equals_synth(ctx, enc2, owt2):
+    """exn_enc_set with block_q8_0 records and F32 norms (the file's kinds) gives the synthetic
+    model's states bit for bit."""
+    e = X.Encoder(ctx, 2)
+    try:
+        qs, d = owt2.q8("token_embd.weight")
+        e.set("token_embd.weight", X.Q8_0, xo.q8_0_to_blocks(qs, d), 4096, VOCAB)
+        for name, shape in eo.enc_expected(eo.EShape(layers=2))[1:]:
+            if len(shape) == 1:
+                e.set(name, X.F32, owt2(name), shape[0], 1)
+            else:
+                e.set(name, X.Q8_0, xo.q8_0_to_blocks(*owt2.q8(name)), shape[1], shape[0])
+        e.set("output_norm.weight", X.F32, np.ones(4096, np.float32), 4096, 1)
+        e.check()
+        ids = eo.synth_ids(SEED + 3, 50, VOCAB)
+        assert np.array_equal(X.encoder_states(e, ids), X.encoder_states(enc2, ids))
+    finally:
+        e.destroy()
+
+
+def test_states_full_depth(ctx):
+    """All 36 blocks on 48 tokens against the oracle (its layers made as read)."""
+    say("encoder synth, 36 layers")
+    e = X.load_encoder(seed=SEED, layers=36, vocab=VOCAB, ctx=ctx)
+    try:
+        ids = eo.synth_ids(SEED + 4, 48, VOCAB)
+        got = X.encoder_states(e, ids)
+        w, s = e.memory()
+        assert w > 8e9
+    finally:
+        e.destroy()
+    want = eo.states(eo.SynthEncoder(SEED, eo.EShape(), keep=False), ids)
+    err = xo.rel_l2(got, want)
+    say("36 layers rel l2", err)
+    assert err < 3e-2 and np.isfinite(got).all()
+
+
+def test_the_distance_is_the_rounding(enc2, owt2):
+    """The oracle with bf16 matrices and product inputs and fp16 q, k, v (the GPU's rounding
+    points) is as far from the fp32 oracle as the GPU is, and nearer the GPU than that."""
+    ids = eo.synth_ids(SEED + 5, 64, VOCAB)
+    got = X.encoder_states(enc2, ids)
+    exact = eo.states(owt2, ids, s=eo.EShape(layers=2))
+    model = eo.states(owt2, ids, s=eo.EShape(layers=2), bf16=True)
+    g, m, gm = xo.rel_l2(got, exact), xo.rel_l2(model, exact), xo.rel_l2(got, model)
+    say("gpu-fp32", g, "model-fp32", m, "gpu-model", gm)
+    assert abs(g - m) < 0.25 * g and gm < g
+
+
+def test_encoder_errors(ctx, enc2):
+    e = X.Encoder(ctx, 2)
+    try:
+        with pytest.raises(X.ExnError) as ex:
+            e.check()
+        assert ex.value.code == X.ESTATE
+        with pytest.raises(X.ExnError) as ex:
+            e.set("blk.2.attn_norm.weight", X.F32, np.ones(4096, np.float32), 4096, 1)
+        assert ex.value.code == X.EINVAL                      # past the layers
+        with pytest.raises(X.ExnError) as ex:
+            e.set("blk.0.attn_k.weight", X.Q8_0, np.zeros(4096 * 34 * 32, np.uint8), 4096, 4096)
+        assert ex.value.code == X.EINVAL                      # k has 1024 rows
+    finally:
+        e.destroy()
+    with pytest.raises(X.ExnError) as ex:
+        X.encoder_states(enc2, np.array([0, VOCAB], np.int32))
+    assert ex.value.code == X.EINVAL

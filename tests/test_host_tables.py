@@ -58,3 +58,17 @@ def test_rope_table_refuses_bad_layouts():
         X.call("exn_dit_rope_table", 4, 2, 2, 0, 0, 0, 0, 7, None, None)     # 8 rows, room for 7
     assert e.value.code == X.EINVAL
     X.call("exn_dit_rope_table", 4, 2, 2, 0, 0, 0, 0, 8, None, None)
+
+
+# --- the prompt encoder's M-RoPE table (mrope-table, src/encoder.lisp:26-39) ----------------
+
+@pytest.mark.parametrize("case", ["text", "edit"])
+def test_encoder_rope_table_matches_the_oracle(case):
+    """exn_enc_rope_table against the oracle's mrope_tables: text positions 0 .. 299, and an edit
+    prompt's positions (5 text tokens, a 7 x 11 picture, 9 more), within one float32 ulp
+    (angles above 2^12 radians are not reached here)."""
+    from oracle import exn_encoder_oracle as eo
+    pos = eo.text_positions(300) if case == "text" else eo.edit_positions(5, 7, 11, 9)
+    cs = X.enc_rope_table(len(pos), None if case == "text" else pos)
+    cos, sin = eo.mrope_tables(pos)
+    assert ulps(cs[:, 0::2], cos).max() <= 1 and ulps(cs[:, 1::2], sin).max() <= 1
