@@ -1,9 +1,10 @@
-"""The SBCL binding (ex-nihilo_amd/lisp/hip-dit.lisp, hip-vae.lisp, hip-vision.lisp) against the C ABI, without
+"""The SBCL binding (ex-nihilo_amd/lisp/hip-dit.lisp, hip-vae.lisp, hip-vision.lisp, hip-encoder.lisp)
+against the C ABI, without
 SBCL (neither this image nor the GPU host has it): every define-alien-routine names a function
 that include/exn_hip.h declares, with its arity and, argument by argument, a Lisp alien type
 that passes the C type (int, 64-bit integers, double, pointers, C strings); and the backend trio
 keeps the reference's lambda lists (src/cuda-dit.lisp:52,137,99; src/cuda-vae.lisp:15,94,28;
-src/cuda-vision.lisp:15,34,103)."""
+src/cuda-vision.lisp:15,34,103; src/encoder.lisp:41,55)."""
 import os
 import re
 
@@ -12,7 +13,7 @@ import pytest
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LISP = os.path.join(REPO, "ex-nihilo_amd", "lisp")
 HEADER = os.path.join(REPO, "include", "exn_hip.h")
-FILES = ("hip-dit.lisp", "hip-vae.lisp", "hip-vision.lisp")
+FILES = ("hip-dit.lisp", "hip-vae.lisp", "hip-vision.lisp", "hip-encoder.lisp")
 
 
 def prototypes():
@@ -110,6 +111,8 @@ def test_the_trio_keeps_the_reference_lambda_lists():
     assert defs["load-vision"] == ["path", "&key", ["device", "1"]]
     assert defs["vision-encode"] == ["v", "px", "h", "w"]
     assert defs["vision-release"] == ["v"]
+    assert defs["load-encoder"] == ["path", "&key", "device", ["threads", ["il::default-thread-count"]]]
+    assert defs["encode-prompt"] == ["model", "prompt", "&key", "vision", "picture"]
 
 
 def test_the_header_parse_sees_the_trio():
