@@ -37,6 +37,14 @@ final latent, 64 x 64 -> a 1024 x 1024 RGBA picture, the mean of 5 decodes.
 times the VAE decoder alone on a seeded 64 x 64 latent (K decodes after W) and
 prints its own JSON line.
 
+prompt_encoder: the prompt encoder (Qwen3-VL-8B's text model, 36 blocks, synthetic Q8_0
+weights) over a 256-token prompt, and over an edit prompt of 1100 tokens of which 1024 are a
+1024 x 1024 picture's rows (merged and deepstack), each the mean of 3 calls with the inputs in
+HBM; FLOPs counted with the model's 8 key/value heads (the products write them out per query
+head).
+
+    python bench.py --encoder-only [--steps K] [--warmup W]
+
 vision_encode_1024sq: the vision tower (Qwen3-VL's ViT, synthetic fp16-valued
 weights, fp32 arithmetic) on a 1024 x 1024 RGBA picture in HBM: 4096 patches
 through 27 blocks and the four mergers, the mean of 3 encodes; its rate against
@@ -361,6 +369,51 @@ def vision_record(t, finite, w_gb, s_gb, n=4096):
             "outputs_finite": finite, "weights_gb": round(w_gb, 3), "scratch_gb": round(s_gb, 2)}
 
 
+def encoder_flop(n, layers=36):
+    """Multiply-add FLOPs of encoder-states over N tokens: per token and layer the products (q, k,
+    v: 4096 -> 6144; out; gate and up; down) and causal attention's two (each token over itself
+    and the tokens before it)."""
+    return layers * (n * 2 * 4096 * (6144 + 4096 + 2 * 12288 + 12288) + 4 * 4096 * n * (n + 1) // 2)
+
+
+def encoder_time(ctx, n, reps, warmup, picture_rows=0):
+    """The prompt encoder (36 blocks, synthetic Q8_0 weights) over N tokens already in HBM, the
+    last PICTURE_ROWS .. of them a picture's (merged rows and three deepstack sets, the vision
+    tower's shapes, after 40 text tokens): ms per call."""
+    import exn_hip as X
+    rng = np.random.default_rng(SEED + n)
+    enc = X.load_encoder(seed=SEED, layers=36, vocab=8192, ctx=ctx)
+    ids = X.DevBuf.of(ctx, rng.integers(0, 8192, n).astype(np.int32))
+    if picture_rows:
+        a0, g = 40, int(round(picture_rows ** 0.5))
+        r, c = np.divmod(np.arange(picture_rows), g)
+        pos = np.concatenate([np.repeat(np.arange(a0)[:, None], 3, 1),
+                              np.stack([np.full(picture_rows, a0), a0 + r, a0 + c], 1),
+                              np.repeat(a0 + g + np.arange(n - a0 - picture_rows)[:, None], 3, 1)])
+    else:
+        a0, pos = 0, None
+    cs = X.DevBuf.of(ctx, X.enc_rope_table(n, pos))
+    pic = X.DevBuf.of(ctx, rng.normal(0, 1, (4, max(picture_rows, 1), 4096)).astype(np.float32))
+    out = X.DevBuf(ctx, (n, 4096), np.float32)
+    run = lambda: X.call("exn_enc_states_dev", enc.h, ids.h, n, cs.h, a0, picture_rows, pic.h,
+                         pic.at(picture_rows * 4096 * 4), out.h)
+    for i in range(warmup):
+        run()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(reps):
+        run()
+    ctx.sync()
+    t = (time.perf_counter() - t0) / reps
+    finite = bool(np.isfinite(out.get()).all())
+    w, _ = enc.memory()
+    enc.destroy()
+    fl = encoder_flop(n)
+    return {"tokens": n, "picture_rows": picture_rows, "ms": round(t * 1e3, 2), "tflop": round(fl / 1e12, 3),
+            "tflops": round(fl / t / 1e12, 1), "mfma_peak_frac": round(fl / t / 1e12 / PEAK_TFLOPS, 4),
+            "states_finite": finite, "weights_gb": round(w / 1e9, 2)}
+
+
 def vision_only(steps, warmup):
     """The vision tower alone: a seeded 1024 x 1024 RGBA picture in HBM -> merged + deepstack rows."""
     import exn_hip as X
@@ -383,6 +436,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--vae-only", action="store_true", help="time the VAE decoder alone")
     ap.add_argument("--vision-only", action="store_true", help="time the vision tower alone")
+    ap.add_argument("--encoder-only", action="store_true", help="time the prompt encoder alone")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="copy MIB MiB device to device after the set-up (the traffic counters' calibration)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
@@ -412,6 +466,18 @@ def main():
         sys.exit(2)
     if a.vision_only:
         vision_only(a.steps, a.warmup)
+        return
+    if a.encoder_only:
+        import exn_hip as X
+        ctx = X.Context(0)
+        rec = {"prompt_256": encoder_time(ctx, 256, a.steps, a.warmup),
+               "edit_1024sq": encoder_time(ctx, 1100, a.steps, a.warmup, 1024)}
+        ctx.close()
+        print(json.dumps({"metric": "prompt encoder ms (36 blocks of Qwen3-VL-8B's text model), 1 GPU",
+                          "value": rec["prompt_256"]["ms"], "unit": "ms/prompt", "n_gpus": 1, "steps": a.steps,
+                          "warmup": a.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+                          "config": {"workload": "encoder-states-256-tokens", "weights": "Q8_0 synthetic",
+                                     "seed": SEED}, "records": rec}), flush=True)
         return
     if a.vae_only:
         vae_only(a.steps, a.warmup)
@@ -562,8 +628,10 @@ def main():
     vae_w, vae_s = vae.memory()
     vae.destroy()
 
-    # the vision tower (editing's picture, seen by the prompt encoder) on a 1024 x 1024 picture
+    # the vision tower (editing's picture, seen by the prompt encoder) on a 1024 x 1024 picture,
+    # and the prompt encoder on a 256-token prompt and on an edit prompt holding that picture's rows
     vis = vision_record(*vision_time(ctx, 3, 1))
+    enc = {"prompt_256": encoder_time(ctx, 256, 3, 1), "edit_1024sq": encoder_time(ctx, 1100, 3, 1, 1024)}
 
     # the 1536 x 1024 and edit workloads on the same weights: cached and uncached steps
     def workload_times(hh, ww, ptext, ref, reps=3):
@@ -722,6 +790,7 @@ def main():
                               "weights_gb": round(vae_w / 1e9, 3), "scratch_gb": round(vae_s / 1e9, 2),
                               "ref_rtx3090_ms": 1500.0},
         "vision_encode_1024sq": vis,
+        "prompt_encoder": enc,
         "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights (resident expansion of Q8_0)",
                      "achieved": round(achieved, 1) if achieved else None, "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4) if achieved else None, "traffic": traffic,

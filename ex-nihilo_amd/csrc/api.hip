@@ -3036,6 +3036,18 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
   TRY(enc_buf(e, "q", (size_t)n * EXN_W * 2, (void**)&q));
   TRY(enc_buf(e, "kc", (size_t)lcap * EXN_W * 2, (void**)&kc, true));
   TRY(enc_buf(e, "vt", (size_t)lcap * EXN_W * 2, (void**)&vt, true));
+  // a prompt of at most 1024 tokens is about one row of 256-row tiles: its products split K
+  // over the chip (the DiT's prompt-row path), the partial sums then added in order
+  float* part = nullptr;
+  const bool split = n <= 1024;
+  if (split) TRY(enc_buf(e, "part", (size_t)kSplitCap * 4, (void**)&part));
+  auto mm = [&](const exn_w* w, const uint16_t* xin, int64_t lda, Epi epi, const EpiArgs& a) -> hipError_t {
+    if (split) {
+      const hipError_t r = gemm_split_rows(s, xin, lda, wop(w), n, w->rows, w->cols, epi, a, part, kSplitCap);
+      if (r != hipErrorNotSupported) return r;
+    }
+    return gemm_any(s, w, xin, lda, n, epi, a);
+  };
   HIPCHK(enc_embed(s, ids, n, e->eqs, e->ed, e->ef, EXN_W, x));
   if (m > 0)
     HIPCHK(hipMemcpyAsync(x + (int64_t)pic0 * EXN_W, merged, (size_t)m * EXN_W * 4, hipMemcpyDeviceToDevice, s));
@@ -3054,13 +3066,13 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
     ea.kc = kc;
     ea.vt = vt;
     ea.lcap = lcap;
-    const hipError_t r = gemm_qkv(s, y, EXN_W, wop(L.qkv), n, EXN_W, ea);
+    const hipError_t r = split ? hipErrorNotSupported : gemm_qkv(s, y, EXN_W, wop(L.qkv), n, EXN_W, ea);
     if (r == hipErrorNotSupported) {
       TRY(enc_buf(e, "qkv", (size_t)n * 3 * EXN_W * 2, (void**)&qkv));
       ea = EpiArgs{};
       ea.y = qkv;
       ea.ldy = 3 * EXN_W;
-      HIPCHK(gemm_any(s, L.qkv, y, EXN_W, n, EPI_F16, ea));
+      HIPCHK(mm(L.qkv, y, EXN_W, EPI_F16, ea));
       HIPCHK(qkv_prep(s, qkv, n, L.vec[E_QNORM], L.vec[E_KNORM], cs, q, kc, vt, 0, lcap, n));
     } else {
       HIPCHK(r);
@@ -3070,17 +3082,17 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
     ea.resid = x;
     ea.ldy = EXN_W;
     ea.gate = e->one_gate;
-    HIPCHK(gemm_any(s, L.out, att, EXN_W, n, EPI_GATE_ADD, ea));
+    HIPCHK(mm(L.out, att, EXN_W, EPI_GATE_ADD, ea));
     HIPCHK(rms_norm(s, n, EXN_W, 1e-6f, x, L.vec[E_FFN_NORM], y, 1));
     ea = EpiArgs{};
     ea.y = ff;
     ea.ldy = EXN_F;
-    HIPCHK(gemm_any(s, L.gate_up, y, EXN_W, n, EPI_SWIGLU, ea));
+    HIPCHK(mm(L.gate_up, y, EXN_W, EPI_SWIGLU, ea));
     ea = EpiArgs{};
     ea.resid = x;
     ea.ldy = EXN_W;
     ea.gate = e->one_gate;
-    HIPCHK(gemm_any(s, L.down, ff, EXN_F, n, EPI_GATE_ADD, ea));
+    HIPCHK(mm(L.down, ff, EXN_F, EPI_GATE_ADD, ea));
     if (m > 0 && il < 3 && deep)
       HIPCHK(gate_add(s, (int64_t)m * EXN_W, EXN_W, 0, 0, 0, x + (int64_t)pic0 * EXN_W, deep + (int64_t)il * m * EXN_W,
                       e->one_gate));
