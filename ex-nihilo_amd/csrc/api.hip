@@ -3048,7 +3048,7 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
     }
     return gemm_any(s, w, xin, lda, n, epi, a);
   };
-  HIPCHK(enc_embed(s, ids, n, e->eqs, e->ed, e->ef, EXN_W, x));
+  HIPCHK(enc_embed(s, ids, n, e->vocab, e->eqs, e->ed, e->ef, EXN_W, x));
   if (m > 0)
     HIPCHK(hipMemcpyAsync(x + (int64_t)pic0 * EXN_W, merged, (size_t)m * EXN_W * 4, hipMemcpyDeviceToDevice, s));
   EpiArgs ea;

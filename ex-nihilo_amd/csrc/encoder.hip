@@ -7,15 +7,19 @@
 namespace exn {
 
 // one workgroup a token: row ids[t] of the token embedding, from Q8_0 codes and scales
-// (fp32(d) x q, exact) or from fp32 rows
+// (fp32(d) x q, exact) or from fp32 rows; an id outside 0 .. vocab-1 gives a row of zeros (the
+// host entry point rejects such ids before they get here)
 __global__ void __launch_bounds__(256)
-k_enc_embed(const int32_t* __restrict__ ids, const int8_t* __restrict__ qs, const uint16_t* __restrict__ d,
-            const float* __restrict__ f32, int width, float* __restrict__ out) {
+k_enc_embed(const int32_t* __restrict__ ids, int64_t vocab, const int8_t* __restrict__ qs,
+            const uint16_t* __restrict__ d, const float* __restrict__ f32, int width, float* __restrict__ out) {
   const int t = blockIdx.x;
   const int64_t id = ids[t];
   float* o = out + (int64_t)t * width;
+  const bool live = id >= 0 && id < vocab;
   for (int c = 4 * threadIdx.x; c < width; c += 1024) {
-    if (f32) {
+    if (!live) {
+      *(f32x4*)(o + c) = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else if (f32) {
       *(f32x4*)(o + c) = *(const f32x4*)(f32 + id * width + c);
     } else {
       const float sc = f16_to_f32(d[(id * width + c) / 32]);
@@ -28,11 +32,11 @@ k_enc_embed(const int32_t* __restrict__ ids, const int8_t* __restrict__ qs, cons
   }
 }
 
-hipError_t enc_embed(hipStream_t s, const int32_t* ids, int n, const int8_t* qs, const uint16_t* d, const float* f32,
-                     int width, float* out) {
+hipError_t enc_embed(hipStream_t s, const int32_t* ids, int n, int64_t vocab, const int8_t* qs, const uint16_t* d,
+                     const float* f32, int width, float* out) {
   if (n <= 0) return hipSuccess;
   if (width % 32) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_enc_embed, dim3(n), dim3(256), 0, s, ids, qs, d, f32, width, out);
+  hipLaunchKernelGGL(k_enc_embed, dim3(n), dim3(256), 0, s, ids, vocab, qs, d, f32, width, out);
   return hipGetLastError();
 }
 

@@ -280,7 +280,7 @@ hipError_t vis_sum(hipStream_t s, int64_t n, const float* a, const float* b, flo
 hipError_t round_f16(hipStream_t s, int64_t n, float* x);
 
 // the prompt encoder (encoder.hip): the token embedding's rows, Q8_0 (qs, d) or fp32 (f32)
-hipError_t enc_embed(hipStream_t s, const int32_t* ids, int n, const int8_t* qs, const uint16_t* d, const float* f32,
-                     int width, float* out);
+hipError_t enc_embed(hipStream_t s, const int32_t* ids, int n, int64_t vocab, const int8_t* qs, const uint16_t* d,
+                     const float* f32, int width, float* out);
 
 }  // namespace exn

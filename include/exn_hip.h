@@ -357,8 +357,9 @@ int exn_enc_check(exn_enc* e);
  * ids), POS (N (t, h, w) triples, or NULL for text positions 0 .. N-1; mrope-table, :26-39);
  * when M > 0 rows PIC0 .. PIC0 + M - 1 take MERGED's rows (M x 4096, the vision tower's) after
  * the embedding and DEEP's set j (3 x M x 4096, or NULL) added after layer j; OUT: N x 4096
- * floats.  Host arrays.  exn_enc_states_dev takes device arrays and the rotary table CS
- * (exn_enc_rope_table's N x 128 floats) in place of POS, on the context's stream. */
+ * floats.  Host arrays; an id outside the vocabulary is EXN_EINVAL.  exn_enc_states_dev takes
+ * device arrays and the rotary table CS (exn_enc_rope_table's N x 128 floats) in place of POS,
+ * on the context's stream; there an id outside the vocabulary embeds as a row of zeros. */
 int exn_enc_states(exn_enc* e, const int32_t* ids, int n, const int32_t* pos, int pic0, int m, const float* merged,
                    const float* deep, float* out);
 int exn_enc_states_dev(exn_enc* e, const int32_t* ids, int n, const float* cs, int pic0, int m, const float* merged,
