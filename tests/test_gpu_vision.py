@@ -134,11 +134,12 @@ def owt():
     return vo.SynthVision(SEED)
 
 
-@pytest.mark.parametrize("hw", [(128, 128), (96, 224), (512, 512)])
+@pytest.mark.parametrize("hw", [(128, 128), (96, 224), (512, 512), (1024, 1024)])
 def test_encode_against_oracle(tower, owt, hw):
     """The whole tower (27 blocks, the three deepstack mergers, the merger) on
     synthetic fp16-valued weights: a 4 x 4 grid of merge blocks, a 3 x 7 one (the
-    table resampled to a wide grid) and the 1024 patches of a 512 x 512 picture."""
+    table resampled to a wide grid), the 1024 patches of a 512 x 512 picture and the
+    4096 of the timed 1024 x 1024 one."""
     h, w = hw
     say("vision encode", h, w)
     px = vo.synth_picture(SEED + h + w, h, w)
