@@ -187,7 +187,7 @@ hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint1
 // over S workgroups a tile into PART (S x M x N floats, at most PART_CAP), then the sums in
 // order through the epilogue: EPI_GATE_ADD, EPI_SWIGLU, EPI_F32, EPI_BF16 or EPI_F16; bf16 weights
 hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
-                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap);
+                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap, int smax = 8);
 // the QKV product with the q/k norm, RoPE and the K/V^T stores fused (EPI_QKV), bf16 or Q8_0
 // weights; hipErrorNotSupported when the shapes or alignments do not fit the fused path
 hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t K,

@@ -879,16 +879,18 @@ k_split_sum(int S, int64_t M, int64_t N, const float* __restrict__ part, EpiArgs
 }
 
 hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
-                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap) {
+                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap, int smax) {
   if (M == 0) return hipSuccess;
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  // S workgroups a tile, about one wave in all, at least 4 k-steps each, at most 8 (past 8 the
-  // partial sums' traffic, S x M x N fp32 written and read back, outweighs the wider spread:
-  // 256 prompt rows through to_out and down, 0.2 ms less a pass than at 16, 0.9 ms less than at 4)
+  // S workgroups a tile, about one wave in all, at least 4 k-steps each, at most SMAX (in a DiT
+  // pass, past 8 the partial sums' traffic, S x M x N fp32 written and read back, outweighs the
+  // wider spread: 256 prompt rows through to_out and down, 0.2 ms less a pass than at 16, 0.9 ms
+  // less than at 4), and no more than PART_CAP holds
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
   int64_t S = 256 / tiles;
   if (S > K / 64 / 4) S = K / 64 / 4;
-  if (S > 8) S = 8;
+  if (S > smax) S = smax;
+  if (S > part_cap / (M * N)) S = part_cap / (M * N);
   if (S < 1) S = 1;
   EpiArgs pa{};
   pa.y = part;
