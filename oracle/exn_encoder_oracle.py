@@ -24,11 +24,14 @@ and i + 64 turn together), causal attention; and the reference's own parts aroun
     p0 = a0 + max(gh, gw);
   - src/encoder.lisp:143-183 (encoder-states): the states after the last block, before
     the final norm.
-Against illatio's arithmetic this is parity unpinned.  tests/test_encoder_oracle.py
-pins it by the mathematics: the M-RoPE table on text positions against 1-D RoPE,
-causality (a prefix's states do not change when tokens follow), grouped heads against
-the same model with every key/value head repeated, rotate_half as a rotation, RMSNorm's
-closed form.  The synthetic weights (Q8_0 matrices, fp32 norms) come from the counter
+Against illatio's own arithmetic (its quantisation and order of operations) this is
+parity unpinned.  tests/test_encoder_oracle.py pins the model it computes: against
+transformers' Qwen3VLTextModel (transformers 5.15.0, installed here; the published
+implementation this restates) with the same weights, on an edit prompt's (t, h, w)
+positions with picture rows and deepstack sets, within float32 rounding; and by the
+mathematics: the M-RoPE table on text positions against 1-D RoPE, causality (a prefix's
+states do not change when tokens follow), grouped heads against the same model with every
+key/value head repeated, rotate_half as a rotation, RMSNorm's closed form.  The synthetic weights (Q8_0 matrices, fp32 norms) come from the counter
 generator of oracle/exn_oracle.py, tensor ids from ENC_ID0 on.
 """
 from __future__ import annotations

@@ -1,6 +1,7 @@
 """Pins oracle/exn_encoder_oracle.py (the prompt encoder's text model).  Its arithmetic
 lives in illatio, which the reference does not vendor, so no vector of the reference's
-covers it (parity unpinned against illatio); these checks hold it to what the
+covers it (parity unpinned against illatio's own arithmetic).  These checks hold it to the
+published model -- transformers' Qwen3VLTextModel with the same weights -- and to what the
 mathematics and the reference's own text fix: M-RoPE on text positions is 1-D RoPE with
 theta 5e6 (docs/design.md:46-48), the sections are 24/20/20, attention is causal,
 grouped key/value heads equal repeated ones, rotate_half is a rotation, and the
@@ -103,3 +104,56 @@ def test_picture_rows_enter_as_call_with_picture_rows(wt):
     got = eo.states(wt, ids, picture=(6, emb, delta), s=one)
     assert np.array_equal(got[:6], base[:6]) and np.array_equal(got[10:], base[10:])
     assert np.allclose(got[6:10], base[6:10] + delta[0], atol=1e-6)
+
+
+def test_states_match_transformers_qwen3vl_text_model(wt):
+    """The published model itself: transformers' Qwen3VLTextModel (the implementation the oracle
+    restates; an installed library, not the reference) with the oracle's weights copied in and
+    its final norm taken out, on an edit prompt's positions (t, h, w) with picture rows and two
+    deepstack sets: the same states within float32 rounding."""
+    torch = pytest.importorskip("torch")
+    pytest.importorskip("transformers")
+    from transformers import Qwen3VLTextConfig
+    from transformers.models.qwen3_vl.modeling_qwen3_vl import Qwen3VLTextModel
+
+    s = SMALL
+    cfg = Qwen3VLTextConfig(vocab_size=s.vocab, hidden_size=s.width, intermediate_size=s.ffn,
+                            num_hidden_layers=s.layers, num_attention_heads=s.heads, num_key_value_heads=s.kv_heads,
+                            head_dim=s.head_dim, rms_norm_eps=1e-6, max_position_embeddings=4096,
+                            rope_parameters={"rope_type": "default", "rope_theta": eo.ROPE_BASE,
+                                             "mrope_section": [24, 20, 20], "mrope_interleaved": True})
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    model = Qwen3VLTextModel(cfg).eval()
+    model.norm = torch.nn.Identity()                      # the states before the final norm
+    names = {"self_attn.q_proj": "attn_q", "self_attn.k_proj": "attn_k", "self_attn.v_proj": "attn_v",
+             "self_attn.o_proj": "attn_output", "self_attn.q_norm": "attn_q_norm", "self_attn.k_norm": "attn_k_norm",
+             "input_layernorm": "attn_norm", "post_attention_layernorm": "ffn_norm", "mlp.gate_proj": "ffn_gate",
+             "mlp.up_proj": "ffn_up", "mlp.down_proj": "ffn_down"}
+    sd = {"embed_tokens.weight": torch.from_numpy(wt("token_embd.weight").copy())}
+    for i in range(s.layers):
+        for theirs, ours in names.items():
+            sd["layers.%d.%s.weight" % (i, theirs)] = torch.from_numpy(wt("blk.%d.%s.weight" % (i, ours)).copy())
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k or k.startswith("norm") for k in missing), (missing, unexpected)
+
+    a0, gh, gw, after = 3, 2, 3, 4
+    pos = eo.edit_positions(a0, gh, gw, after)
+    n = len(pos)
+    ids = eo.synth_ids(8, n, s.vocab)
+    merged, deep = eo.synth_picture_rows(9, gh * gw, s.width)
+    deep = deep[:2]                                        # two sets: after layers 0 and 1
+    want = eo.states(wt, ids, pos, (a0, merged, deep), s=s)
+
+    emb = torch.from_numpy(wt("token_embd.weight")[ids].copy())[None]
+    emb[0, a0:a0 + gh * gw] = torch.from_numpy(merged)
+    mask = torch.zeros(1, n, dtype=torch.bool)
+    mask[0, a0:a0 + gh * gw] = True
+    with torch.no_grad():
+        out = model(inputs_embeds=emb, position_ids=torch.from_numpy(pos.T.copy())[:, None, :],
+                    visual_pos_masks=mask, deepstack_visual_embeds=[torch.from_numpy(d) for d in deep],
+                    use_cache=False).last_hidden_state[0].numpy()
+    assert xo.rel_l2(want, out) < 2e-6
+    # and a mistake the oracle could make shows: the h and w axes swapped in the table
+    swapped = pos[:, [0, 2, 1]]
+    assert xo.rel_l2(eo.states(wt, ids, swapped, (a0, merged, deep), s=s), out) > 1e-4

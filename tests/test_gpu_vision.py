@@ -159,9 +159,10 @@ def test_encode_against_oracle(tower, owt, hw):
 
 
 def test_encode_reads_a_table_of_another_side_and_f16_tensors(ctx, owt):
-    """exn_vision_set: the position table of a 36 x 36 grid (F32), every other tensor
-    as the fp16 bit patterns an mmproj-f16 file holds (1-D ones as F32): the encode
-    matches the oracle run on the same tensors."""
+    """exn_vision_set: the position table of a 36 x 36 grid (F32), the matrices as the fp16
+    bit patterns an mmproj-f16 file holds, except the blocks' attn_out matrices as bf16 bit
+    patterns (their values rounded to bf16 on both sides), 1-D tensors as F32: the encode
+    matches the oracle run on the same values."""
     s36 = vo.VShape(side=36)
     wt = vo.SynthVision(SEED, s36)
     wt.cache = {k: a for k, a in owt.cache.items() if k != "v.position_embd.weight"}   # the same tensors
@@ -169,7 +170,11 @@ def test_encode_reads_a_table_of_another_side_and_f16_tensors(ctx, owt):
     try:
         for name, shape in vo.vision_expected(s36):
             a = wt(name)
-            if a.ndim > 1 and name != "v.position_embd.weight":
+            if name.endswith("attn_out.weight"):
+                b = xo.bf16_bits(a)
+                wt.cache[name] = xo.bf16_to_f32(b).reshape(a.shape)     # the oracle reads the same values
+                v.set(name, X.BF16, b, shape)
+            elif a.ndim > 1 and name != "v.position_embd.weight":
                 v.set(name, X.F16, a.astype(np.float16).view(np.uint16), shape)
             else:
                 v.set(name, X.F32, a, shape)
