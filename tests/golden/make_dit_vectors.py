@@ -1,5 +1,5 @@
 """Writes the oracle's results for the full-depth GPU parity tests, which the
-GPU box cannot afford to recompute inside a test (a 32-block numpy step is
+GPU tests cannot afford to recompute (a 32-block numpy step is
 minutes of CPU).  These are the oracle's outputs (oracle/exn_oracle.py,
 itself pinned against the reference's ref_dit.py vectors), cached:
 

@@ -3,7 +3,7 @@ reference's own numpy DiT (inspect/ref_dit.py `forward`, :108-153) at tiny
 shapes, so that the oracle's forward composition is pinned against the
 reference's and not against a retyping of it.
 
-Run in the build container only (the reference tree is not on the GPU box):
+Run where the reference tree is (it does not travel with the tests):
 
     python tests/golden/make_ref_dit_vectors.py [/root/reference]
 

@@ -2,7 +2,7 @@
 vision tower (inspect/ref_vision.py `main`, :72-148) on synthetic weights at a
 narrow width, the vectors that pin oracle/exn_vision_oracle.py's encode.
 
-Run in the build container only (the reference tree is not on the GPU box):
+Run where the reference tree is (it does not travel with the tests):
 
     python tests/golden/make_ref_vision_vectors.py [/root/reference]
 
