@@ -53,6 +53,14 @@ the dense fp32 MFMA peak (157.3 TFLOP/s).
     python bench.py --vision-only [--steps K] [--warmup W]
 
 times the tower alone and prints its own JSON line.
+
+pictures: whole pictures as the reference's README times them (1024 x 1024,
+1536 x 1024 and an edit at 1024 x 1024 on an RTX 3090: about 11, 22 and 20 s):
+the prompt encoder's states, the 8-step loop from fresh noise (its first step
+uncached) and the VAE decode, plus for the edit the vision tower on the picture
+to edit and its rows in the prompt; each part timed between synchronisations,
+the mean of 2 pictures after one.  The edit's picture latent is synthetic (the
+VAE encoder is not built).
 """
 import argparse
 import json
@@ -414,6 +422,84 @@ def encoder_time(ctx, n, reps, warmup, picture_rows=0):
             "states_finite": finite, "weights_gb": round(w / 1e9, 2)}
 
 
+def pictures(ctx, d, reps=2):
+    """Whole pictures on the device, as the reference's README times them (1024 x 1024, 1536 x
+    1024, an edit at 1024 x 1024): the prompt's states from the encoder (synthetic ids), the
+    8-step loop from fresh noise (a fresh prefix key: the first step uncached), the VAE decode to
+    RGBA; an edit adds the vision tower on the picture to edit, whose merged and deepstack rows
+    the encoder takes in the prompt, and gives the DiT the picture's latent (synthetic here: the
+    VAE encoder is not built) beside the text's 512 states.  Each part is timed between
+    synchronisations; ms a picture, the mean of REPS after one untimed picture."""
+    import exn_hip as X
+    rng = np.random.default_rng(SEED + 77)
+    enc = X.load_encoder(seed=SEED, layers=36, vocab=8192, ctx=ctx)
+    vis = X.load_vision(seed=SEED, ctx=ctx)
+    vae = X.upload_vae(seed=SEED, ctx=ctx)
+    sg = np.array(X.TURBO_SIGMAS, np.float64)
+    recs = {}
+    for name, (hh, ww, edit, ref_s) in {"1024sq": (64, 64, False, 11.0), "1536x1024": (96, 64, False, 22.0),
+                                        "edit_1024sq": (64, 64, True, 20.0)}.items():
+        ptext, a0, m = 512 if edit else P, 40, 1024 if edit else 0
+        n = ptext + m
+        ids = X.DevBuf.of(ctx, rng.integers(0, 8192, n).astype(np.int32))
+        if edit:
+            r, c = np.divmod(np.arange(m), 32)
+            pos = np.concatenate([np.repeat(np.arange(a0)[:, None], 3, 1),
+                                  np.stack([np.full(m, a0), a0 + r, a0 + c], 1),
+                                  np.repeat(a0 + 32 + np.arange(n - a0 - m)[:, None], 3, 1)])
+            px = X.DevBuf.of(ctx, np.clip(rng.normal(0, 0.5, (16 * hh, 16 * ww, 4)), -1, 1).astype(np.float32))
+            vrows = X.DevBuf(ctx, (4, m, 4096), np.float32)
+            rl = X.DevBuf.of(ctx, rng.normal(0, 1, (64, hh, ww)).astype(np.float32))
+        else:
+            pos = None
+        cs = X.DevBuf.of(ctx, X.enc_rope_table(n, pos))
+        states = X.DevBuf(ctx, (n, 4096), np.float32)
+        context = X.DevBuf(ctx, (ptext, 4096), np.float32) if edit else states
+        noise = rng.normal(0, 1, (64, hh, ww)).astype(np.float32)
+        z = X.DevBuf(ctx, (64, hh, ww), np.float32)
+        pic = X.DevBuf(ctx, (16 * hh, 16 * ww, 4), np.float32)
+
+        def picture():
+            z.upload(noise)
+            ctx.sync()
+            t = [time.perf_counter()]
+            if edit:
+                X.call("exn_vision_encode_dev", vis.h, px.h, 16 * hh, 16 * ww, vrows.h, vrows.at(m * 4096 * 4))
+                ctx.sync()
+                t.append(time.perf_counter())
+                X.call("exn_enc_states_dev", enc.h, ids.h, n, cs.h, a0, m, vrows.h, vrows.at(m * 4096 * 4), states.h)
+                # the text's states: the picture's rows left out
+                X.call("exn_copy", ctx.h, context.h, states.h, a0 * 4096 * 4)
+                X.call("exn_copy", ctx.h, context.at(a0 * 4096 * 4), states.at((a0 + m) * 4096 * 4),
+                       (n - a0 - m) * 4096 * 4)
+                refargs = (a0, rl.h, hh, ww)
+            else:
+                X.call("exn_enc_states_dev", enc.h, ids.h, n, cs.h, 0, 0, None, None, states.h)
+                refargs = (0, None, 0, 0)
+            ctx.sync()
+            t.append(time.perf_counter())
+            X.call("exn_dit_generate_dev", d.h, context.h, ptext, z.h, hh, ww, X.ptr(sg), len(sg), *refargs)
+            ctx.sync()
+            t.append(time.perf_counter())
+            X.call("exn_vae_decode_dev", vae.h, z.h, hh, ww, pic.h)
+            ctx.sync()
+            t.append(time.perf_counter())
+            return np.diff(t)
+
+        picture()
+        parts = np.mean([picture() for _ in range(reps)], axis=0) * 1e3
+        names = (["vision_ms"] if edit else []) + ["encoder_ms", "dit_8_steps_ms", "vae_ms"]
+        recs[name] = {"ms": round(float(parts.sum()), 1), **{k: round(float(v), 1) for k, v in zip(names, parts)},
+                      "picture_h_x_w": "%d x %d" % (16 * hh, 16 * ww), "prompt_tokens": n, "text_rows": ptext,
+                      "picture_finite": bool(np.isfinite(pic.get()).all()), "ref_rtx3090_s": ref_s}
+        for b in [ids, cs, states, z, pic] + ([context, px, vrows, rl] if edit else []):
+            b.free()
+    enc.destroy()
+    vis.destroy()
+    vae.destroy()
+    return recs
+
+
 def vision_only(steps, warmup):
     """The vision tower alone: a seeded 1024 x 1024 RGBA picture in HBM -> merged + deepstack rows."""
     import exn_hip as X
@@ -677,6 +763,9 @@ def main():
     workloads = {"cfg3_1536x1024": workload_times(96, 64, 256, None),
                  "cfg4_edit_1024sq": workload_times(64, 64, 512, (8, 64, 64))}
 
+    # whole pictures: prompt encoder, the 8-step loop and the VAE decode (an edit: the vision tower too)
+    pics = pictures(ctx, d)
+
     # the same cached 1024^2 step with the block matrices multiplied from Q8_0: the codes
     # dequantised inside the products' pipeline, the resident bf16 copies dropped (the change of
     # product path drops the kept K/V too, so the first step recomputes them)
@@ -783,6 +872,7 @@ def main():
         "q8_0": q8,
         "w8a8": w8a8,
         "workloads": workloads,
+        "pictures": pics,
         "vae_decode_1024sq": {"ms": round(t_vae * 1e3, 2), "tflop": round(VAE_FLOP / 1e12, 2),
                               "tflops": round(VAE_FLOP / t_vae / 1e12, 1),
                               "mfma_peak_frac": round(VAE_FLOP / t_vae / 1e12 / PEAK_TFLOPS, 4),
