@@ -381,9 +381,9 @@ def test_cfg2_eight_steps_full_depth(ctx):
     d.destroy()
 
 
-WORKLOADS = {  # name: (seed, text rows, image h, w, reference picture (a, rh, rw) or None)
-    "cfg3_1536x1024": (6, 256, 96, 64, None),
-    "cfg4_edit_1024sq": (7, 512, 64, 64, (8, 64, 64)),
+WORKLOADS = {  # name: (seed, text rows, image h, w, reference picture (a, rh, rw) or None, the oracle's run)
+    "cfg3_1536x1024": (6, 256, 96, 64, None, "dit_cfg3_8step.npz"),
+    "cfg4_edit_1024sq": (7, 512, 64, 64, (8, 64, 64), "dit_cfg4_edit_8step.npz"),
 }
 
 
@@ -391,11 +391,14 @@ WORKLOADS = {  # name: (seed, text rows, image h, w, reference picture (a, rh, r
 def test_workloads_eight_steps_full_depth(ctx, case):
     """The 1536 x 1024 workload (6144 image rows over 256 text rows) and the edit workload
     (512 text rows with a 64 x 64 reference picture after the first 8, then a 64 x 64 image:
-    8704 keys) end to end, 32 blocks: the first step uncached and again on the kept prefix K/V
-    (one velocity, <= 1e-5); the 8 Turbo steps of the host loop (exn_dit_velocity and the
-    Euler update in numpy) and of the device loop (exn_dit_generate_dev) give one latent
-    (<= 1e-5), every value finite."""
-    seed, p, h, w, ref = WORKLOADS[case]
+    8704 keys) end to end, 32 blocks: the first step's velocity (uncached, <= 1e-2) and the
+    final latent after the 8 Turbo steps (<= 2e-2) against the oracle's run cached as float16
+    in tests/golden (hours of numpy each); the first step again on the kept prefix K/V (one
+    velocity, <= 1e-5); the host loop (exn_dit_velocity and the Euler update in numpy) and the
+    device loop (exn_dit_generate_dev) give one latent (<= 1e-5), every value finite."""
+    seed, p, h, w, ref, fixture = WORKLOADS[case]
+    g = np.load(os.path.join(GOLDEN, fixture))
+    assert [int(v) for v in g["meta"]] == [seed, p, h, w]
     say(case, "32 blocks, p", p, "image", h, "x", w, "ref", ref, "8 steps")
     d = model(ctx, 32, seed)
     if ref is None:
@@ -409,8 +412,9 @@ def test_workloads_eight_steps_full_depth(ctx, case):
     v0 = X.dit_velocity(d, ctxa, p, lat, h, w, sig[0], prefix_key="k", ref=refarg)
     v0c = X.dit_velocity(d, ctxa, p, lat, h, w, sig[0], prefix_key="k", ref=refarg)
     e01 = xo.rel_l2(v0c, v0)
-    say("%s: step 0 cached vs uncached rel-L2 %.2e" % (case, e01))
-    assert np.isfinite(v0).all() and e01 < 1e-5
+    e0 = xo.rel_l2(v0, g["v_step0"].astype(np.float32))
+    say("%s: step 0 against the oracle rel-L2 %.2e, cached vs uncached %.2e" % (case, e0, e01))
+    assert np.isfinite(v0).all() and e01 < 1e-5 and e0 < 1e-2
     z = lat.copy()
     for i, (s, s2) in enumerate(zip(sig[:-1], sig[1:])):
         v = v0c if i == 0 else X.dit_velocity(d, ctxa, p, z, h, w, s, prefix_key="k", ref=refarg)
@@ -425,8 +429,9 @@ def test_workloads_eight_steps_full_depth(ctx, case):
         X.call("exn_dit_generate_dev", d.h, cd.h, p, zd.h, h, w, X.ptr(sg), len(sg), ref[0], rd.h, ref[1], ref[2])
     zg = zd.get()
     ez = xo.rel_l2(zg, z)
-    say("%s: final latent, device loop vs host loop rel-L2 %.2e, |z| %.4f" % (case, ez, float(np.sqrt((z * z).mean()))))
-    assert np.isfinite(zg).all() and ez < 1e-5
+    eo = xo.rel_l2(zg, g["z_final"].astype(np.float32))
+    say("%s: final latent against the oracle rel-L2 %.2e, device loop vs host loop %.2e" % (case, eo, ez))
+    assert np.isfinite(zg).all() and ez < 1e-5 and eo < 2e-2
     d.destroy()
 
 
