@@ -58,9 +58,16 @@ pictures: whole pictures as the reference's README times them (1024 x 1024,
 1536 x 1024 and an edit at 1024 x 1024 on an RTX 3090: about 11, 22 and 20 s):
 the prompt encoder's states, the 8-step loop from fresh noise (its first step
 uncached) and the VAE decode, plus for the edit the vision tower on the picture
-to edit and its rows in the prompt; each part timed between synchronisations,
-the mean of 2 pictures after one.  The edit's picture latent is synthetic (the
-VAE encoder is not built).
+to edit and its rows in the prompt, and the VAE encoder's latent of that
+picture; each part timed between synchronisations, the mean of 2 pictures after
+one.
+
+vae_encode_1024sq: the VAE encoder (an edit's picture to its 64 x 64 latent) on
+the decoded 1024 x 1024 picture, the mean of 5 encodes (--vae-only too).
+
+    python bench.py --vae-encode-only [--steps K] [--warmup W]
+
+times the encoder alone on a seeded picture and prints its own JSON line.
 """
 import argparse
 import json
@@ -85,6 +92,7 @@ TRAFFIC_FILE_Q8 = os.path.join(REPO, "profiles", "gemm_gate_up_swiglu_q8_0_1024s
 PROBE_BYTES = 1 << 30         # --copy-probe 1024
 PEAK_F32_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 VAE_FLOP = 17.03e12           # one decode of a 64 x 64 latent: every convolution and the attention's products
+VAE_ENC_FLOP = 3.1585e12      # one encode of a 1024 x 1024 picture, likewise (the first convolution at 4 channels)
 
 
 def gemm_flops_per_row():
@@ -324,6 +332,7 @@ def vae_only(steps, warmup):
     ctx.sync()
     t = (time.perf_counter() - t0) / steps
     px = pic.get()
+    t_enc, zf = vae_encode_time(ctx, vae, pic, steps, warmup)
     vae_w, vae_s = vae.memory()
     vae.destroy()
     ctx.close()
@@ -335,7 +344,51 @@ def vae_only(steps, warmup):
                       "mfma_peak_frac": round(VAE_FLOP / t / 1e12 / PEAK_TFLOPS, 4),
                       "picture_finite": bool(np.isfinite(px).all()),
                       "weights_gb": round(vae_w / 1e9, 3), "scratch_gb": round(vae_s / 1e9, 2),
-                      "ref_rtx3090_ms": 1500.0}), flush=True)
+                      "ref_rtx3090_ms": 1500.0, "vae_encode_1024sq": vae_encode_record(t_enc, zf)}), flush=True)
+
+
+def vae_encode_time(ctx, vae, pic, reps, warmup):
+    """The VAE encoder on the 1024 x 1024 picture PIC (in HBM) -> its 64 x 64 latent: (s an
+    encode, whether every value is finite)."""
+    import exn_hip as X
+    z = X.DevBuf(ctx, (64, H, W), np.float32)
+    for i in range(warmup):
+        X.call("exn_vae_encode_dev", vae.h, pic.h, 16 * H, 16 * W, z.h)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(reps):
+        X.call("exn_vae_encode_dev", vae.h, pic.h, 16 * H, 16 * W, z.h)
+    ctx.sync()
+    t = (time.perf_counter() - t0) / reps
+    finite = bool(np.isfinite(z.get()).all())
+    z.free()
+    return t, finite
+
+
+def vae_encode_only(steps, warmup):
+    """The VAE encoder alone: a seeded 1024 x 1024 RGBA picture in HBM -> its 64 x 64 latent."""
+    import exn_hip as X
+    rng = np.random.default_rng(SEED)
+    ctx = X.Context(0)
+    vae = X.upload_vae(seed=SEED, ctx=ctx)
+    pic = X.DevBuf.of(ctx, np.clip(rng.normal(0, 0.5, (16 * H, 16 * W, 4)), -1, 1).astype(np.float32))
+    t, finite = vae_encode_time(ctx, vae, pic, steps, warmup)
+    vae_w, vae_s = vae.memory()
+    vae.destroy()
+    ctx.close()
+    rec = vae_encode_record(t, finite)
+    print(json.dumps(dict({"metric": "VAE encode ms @1024² (1024x1024 RGBA -> 64x64x64 latent), 1 GPU",
+                           "value": rec["ms"], "unit": "ms/encode", "n_gpus": 1, "steps": steps, "warmup": warmup,
+                           "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+                           "config": {"workload": "vae-encode-1024x1024", "weights": "bf16 synthetic", "seed": SEED},
+                           "weights_gb": round(vae_w / 1e9, 3), "scratch_gb": round(vae_s / 1e9, 2)}, **rec)),
+          flush=True)
+
+
+def vae_encode_record(t, finite):
+    return {"ms": round(t * 1e3, 2), "tflop": round(VAE_ENC_FLOP / 1e12, 3),
+            "tflops": round(VAE_ENC_FLOP / t / 1e12, 1),
+            "mfma_peak_frac": round(VAE_ENC_FLOP / t / 1e12 / PEAK_TFLOPS, 4), "latent_finite": finite}
 
 
 def vision_flop(n, d=1152, f=4304, depth=27, out=4096):
@@ -427,9 +480,10 @@ def pictures(ctx, d, reps=2):
     1024, an edit at 1024 x 1024): the prompt's states from the encoder (synthetic ids), the
     8-step loop from fresh noise (a fresh prefix key: the first step uncached), the VAE decode to
     RGBA; an edit adds the vision tower on the picture to edit, whose merged and deepstack rows
-    the encoder takes in the prompt, and gives the DiT the picture's latent (synthetic here: the
-    VAE encoder is not built) beside the text's 512 states.  Each part is timed between
-    synchronisations; ms a picture, the mean of REPS after one untimed picture."""
+    the encoder takes in the prompt, and the VAE encoder's latent of the picture, which the DiT
+    takes beside the text's 512 states (the Lisp host's per-channel normalisation of that latent
+    left out).  Each part is timed between synchronisations; ms a picture, the mean of REPS after
+    one untimed picture."""
     import exn_hip as X
     rng = np.random.default_rng(SEED + 77)
     enc = X.load_encoder(seed=SEED, layers=36, vocab=8192, ctx=ctx)
@@ -449,7 +503,7 @@ def pictures(ctx, d, reps=2):
                                   np.repeat(a0 + 32 + np.arange(n - a0 - m)[:, None], 3, 1)])
             px = X.DevBuf.of(ctx, np.clip(rng.normal(0, 0.5, (16 * hh, 16 * ww, 4)), -1, 1).astype(np.float32))
             vrows = X.DevBuf(ctx, (4, m, 4096), np.float32)
-            rl = X.DevBuf.of(ctx, rng.normal(0, 1, (64, hh, ww)).astype(np.float32))
+            rl = X.DevBuf(ctx, (64, hh, ww), np.float32)
         else:
             pos = None
         cs = X.DevBuf.of(ctx, X.enc_rope_table(n, pos))
@@ -465,6 +519,9 @@ def pictures(ctx, d, reps=2):
             t = [time.perf_counter()]
             if edit:
                 X.call("exn_vision_encode_dev", vis.h, px.h, 16 * hh, 16 * ww, vrows.h, vrows.at(m * 4096 * 4))
+                ctx.sync()
+                t.append(time.perf_counter())
+                X.call("exn_vae_encode_dev", vae.h, px.h, 16 * hh, 16 * ww, rl.h)
                 ctx.sync()
                 t.append(time.perf_counter())
                 X.call("exn_enc_states_dev", enc.h, ids.h, n, cs.h, a0, m, vrows.h, vrows.at(m * 4096 * 4), states.h)
@@ -488,7 +545,7 @@ def pictures(ctx, d, reps=2):
 
         picture()
         parts = np.mean([picture() for _ in range(reps)], axis=0) * 1e3
-        names = (["vision_ms"] if edit else []) + ["encoder_ms", "dit_8_steps_ms", "vae_ms"]
+        names = (["vision_ms", "vae_encode_ms"] if edit else []) + ["encoder_ms", "dit_8_steps_ms", "vae_ms"]
         recs[name] = {"ms": round(float(parts.sum()), 1), **{k: round(float(v), 1) for k, v in zip(names, parts)},
                       "picture_h_x_w": "%d x %d" % (16 * hh, 16 * ww), "prompt_tokens": n, "text_rows": ptext,
                       "picture_finite": bool(np.isfinite(pic.get()).all()), "ref_rtx3090_s": ref_s}
@@ -521,6 +578,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--vae-only", action="store_true", help="time the VAE decoder alone")
+    ap.add_argument("--vae-encode-only", action="store_true", help="time the VAE encoder alone")
     ap.add_argument("--vision-only", action="store_true", help="time the vision tower alone")
     ap.add_argument("--encoder-only", action="store_true", help="time the prompt encoder alone")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -564,6 +622,9 @@ def main():
                           "warmup": a.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
                           "config": {"workload": "encoder-states-256-tokens", "weights": "Q8_0 synthetic",
                                      "seed": SEED}, "records": rec}), flush=True)
+        return
+    if a.vae_encode_only:
+        vae_encode_only(a.steps, a.warmup)
         return
     if a.vae_only:
         vae_only(a.steps, a.warmup)
@@ -711,6 +772,8 @@ def main():
     ctx.sync()
     t_vae = (time.perf_counter() - t0) / VAE_REPS
     px = pic.get()
+    # the encoder (an edit's picture to its latent) on that picture
+    t_venc, venc_ok = vae_encode_time(ctx, vae, pic, VAE_REPS, 1)
     vae_w, vae_s = vae.memory()
     vae.destroy()
 
@@ -879,6 +942,7 @@ def main():
                               "picture_finite": bool(np.isfinite(px).all()),
                               "weights_gb": round(vae_w / 1e9, 3), "scratch_gb": round(vae_s / 1e9, 2),
                               "ref_rtx3090_ms": 1500.0},
+        "vae_encode_1024sq": vae_encode_record(t_venc, venc_ok),
         "vision_encode_1024sq": vis,
         "prompt_encoder": enc,
         "roofline": {"bound": "mfma", "kernel": "gemm gate_up + SwiGLU, 4096 x 24576 x 4096, bf16 weights (resident expansion of Q8_0)",

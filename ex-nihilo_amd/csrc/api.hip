@@ -1831,6 +1831,53 @@ std::vector<VExpect> vae_expected() {
   return r;
 }
 
+// the encoder (a picture to a latent): (in, out, spatial down, temporal down), the picture's
+// end first: src/weights.lisp:100-102
+const VStage kVaeEncStages[5] = {{96, 96, true, false}, {96, 192, true, true}, {192, 384, true, true},
+                                 {384, 768, true, true}, {768, 768, false, false}};
+const int kVaeIn = 4;
+
+// src/weights.lisp:104-134 (vae-encoder-expected), the video-only time_conv tensors left out
+std::vector<VExpect> vae_encoder_expected() {
+  std::vector<VExpect> r;
+  const int top = kVaeEncStages[4].out;
+  auto add = [&](const std::string& n, std::vector<int64_t> s) { r.push_back(VExpect{n, s}); };
+  auto conv = [&](const std::string& n, int64_t o, int64_t i, int64_t k, bool frames) {
+    if (frames) add(n + ".weight", {o, i, 1, k, k});
+    else add(n + ".weight", {o, i, k, k});
+    add(n + ".bias", {o});
+  };
+  auto res = [&](const std::string& p, int i, int o) {
+    add(p + ".residual.0.gamma", {i, 1, 1, 1});
+    conv(p + ".residual.2", o, i, 3, true);
+    add(p + ".residual.3.gamma", {o, 1, 1, 1});
+    conv(p + ".residual.6", o, o, 3, true);
+    if (i != o) conv(p + ".shortcut", o, i, 1, true);
+  };
+  conv("encoder.conv1", kVaeEncStages[0].in, kVaeIn, 3, true);
+  char p[96];
+  for (int s = 0; s < 5; ++s) {
+    const VStage& st = kVaeEncStages[s];
+    for (int j = 0; j < 2; ++j) {
+      snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.%d", s, j);
+      res(p, j == 0 ? st.in : st.out, st.out);
+    }
+    if (st.up) {
+      snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.2.resample.1", s);
+      conv(p, st.out, st.out, 3, false);
+    }
+  }
+  res("encoder.middle.0", top, top);
+  add("encoder.middle.1.norm.gamma", {top, 1, 1});
+  conv("encoder.middle.1.to_qkv", 3 * top, top, 1, false);
+  conv("encoder.middle.1.proj", top, top, 1, false);
+  res("encoder.middle.2", top, top);
+  add("encoder.head.0.gamma", {top, 1, 1, 1});
+  conv("encoder.head.2", 2 * kVaeZ, top, 3, true);
+  conv("conv1", 2 * kVaeZ, 2 * kVaeZ, 1, true);
+  return r;
+}
+
 // a decoder tensor on the device: a convolution's weights as bf16 rows of (tap, channel), K
 // padded with zeros to kp (a multiple of 64); anything else as fp32
 struct VT {
@@ -1848,7 +1895,8 @@ bool is_conv_weight(const VExpect& e) {
 
 struct exn_vae {
   exn_ctx* ctx = nullptr;
-  std::vector<VExpect> expect;
+  std::vector<VExpect> expect;   // the decoder's tensors, then (from n_dec on) the encoder's
+  size_t n_dec = 0;
   std::map<std::string, VT> t;
   std::map<std::string, Buf> bufs;
   float* part = nullptr;   // split-K partial sums of the small convolutions (a decode's scratch)
@@ -1921,6 +1969,8 @@ int exn_vae_create(exn_ctx* ctx, exn_vae** out) {
   exn_vae* v = new exn_vae();
   v->ctx = ctx;
   v->expect = vae_expected();
+  v->n_dec = v->expect.size();
+  for (auto& e : vae_encoder_expected()) v->expect.push_back(e);
   *out = v;
   return EXN_OK;
 }
@@ -1948,7 +1998,7 @@ int exn_vae_set(exn_vae* v, const char* name, int kind, const void* data, const 
   if (!v || !name || !data || !dims) FAIL(EXN_EINVAL, "vae set: null argument");
   TRY(use(v->ctx));
   const VExpect* e = vae_find(v, name, nullptr);
-  if (!e) FAIL(EXN_EINVAL, "vae set: no decoder tensor %s", name);
+  if (!e) FAIL(EXN_EINVAL, "vae set: no decoder or encoder tensor %s", name);
   if (kind != EXN_F32 && kind != EXN_BF16) FAIL(EXN_EINVAL, "vae set %s: kind %d (F32 or BF16 only)", name, kind);
   bool same = ndims == (int)e->shape.size();
   for (int i = 0; same && i < ndims; ++i) same = dims[i] == e->shape[i];
@@ -1977,8 +2027,9 @@ int exn_vae_set(exn_vae* v, const char* name, int kind, const void* data, const 
   return EXN_OK;
 }
 
-// every decoder tensor from the counter generator (the oracle's SynthVae): value =
-// bf16(base + scale * normal), normal i of key(seed, 4000 + the tensor's index)
+// every decoder and encoder tensor from the counter generator (the oracle's SynthVae): value =
+// bf16(base + scale * normal), normal i of key(seed, 4000 + the tensor's index), the encoder's
+// after the decoder's
 int exn_vae_synth(exn_vae* v, uint64_t seed) {
   if (!v) FAIL(EXN_EINVAL, "null decoder");
   TRY(use(v->ctx));
@@ -1998,7 +2049,9 @@ int exn_vae_synth(exn_vae* v, uint64_t seed) {
       int64_t fan = 1;
       for (size_t k = 1; k < e.shape.size(); ++k) fan *= e.shape[k];
       double g = 1.0;
-      if (nm.find(".residual.6.") != std::string::npos || nm.rfind("decoder.middle.1.proj", 0) == 0) g = 0.5;
+      if (nm.find(".residual.6.") != std::string::npos || nm.rfind("decoder.middle.1.proj", 0) == 0 ||
+          nm.rfind("encoder.middle.1.proj", 0) == 0)
+        g = 0.5;
       if (nm.rfind("decoder.head.2", 0) == 0) g = 1.2;
       scale = g / sqrt((double)fan);
     }
@@ -2014,8 +2067,15 @@ int exn_vae_synth(exn_vae* v, uint64_t seed) {
 
 int exn_vae_check(exn_vae* v) {
   if (!v) FAIL(EXN_EINVAL, "null decoder");
-  for (auto& e : v->expect)
-    if (!vae_t(v, e.name)) FAIL(EXN_ESTATE, "decoder: missing %s", e.name.c_str());
+  for (size_t i = 0; i < v->n_dec; ++i)
+    if (!vae_t(v, v->expect[i].name)) FAIL(EXN_ESTATE, "decoder: missing %s", v->expect[i].name.c_str());
+  return EXN_OK;
+}
+
+int exn_vae_check_encoder(exn_vae* v) {
+  if (!v) FAIL(EXN_EINVAL, "null decoder");
+  for (size_t i = v->n_dec; i < v->expect.size(); ++i)
+    if (!vae_t(v, v->expect[i].name)) FAIL(EXN_ESTATE, "encoder: missing %s", v->expect[i].name.c_str());
   return EXN_OK;
 }
 
@@ -2225,7 +2285,108 @@ static int vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba
   return vae_conv_named(v, "decoder.head.2", 0, VAE_CLAMP, a_rs, nullptr, rgba, hh, ww);
 }
 
+// the encoder (src/cuda-vae.lisp:138-190): RGBA (h x w x 4 fp32, -1 .. 1) -> the latent's mean
+// (64 x h/16 x w/16 fp32, channel-major, as the decoder takes it).  The first convolution runs
+// as a 1 x 1 product over each pixel's 3 x 3 RGBA neighbourhood (36 values, padded to 64); a
+// stage is two residual blocks, then a stride-2 convolution plus AvgDown3D of the stage's input
+// (or, without the spatial step, the input added); the middle; the head's norm, SiLU, 3 x 3 to
+// the mean and log-variance and conv1 (1 x 1), of which the mean is kept.
+static int vae_encode(exn_vae* v, const float* rgba, int h, int w, float* latent) {
+  hipStream_t s = v->ctx->stream;
+  const int top = kVaeEncStages[4].out;
+  int64_t most = (int64_t)h * w * kVaeEncStages[0].in;
+  {
+    int64_t hh = h, ww = w;
+    for (auto& st : kVaeEncStages) {
+      most = std::max(most, hh * ww * std::max(st.in, st.out));
+      if (st.up) {
+        hh /= 2;
+        ww /= 2;
+      }
+    }
+  }
+  float *A, *B, *C, *t2;
+  uint16_t *t1, *u, *t3;
+  TRY(vae_buf(v, "A", (size_t)most * 4, (void**)&A));
+  TRY(vae_buf(v, "B", (size_t)most * 4, (void**)&B));
+  TRY(vae_buf(v, "C", (size_t)most * 4, (void**)&C));
+  TRY(vae_buf(v, "t2", (size_t)most * 4, (void**)&t2));
+  TRY(vae_buf(v, "t1", (size_t)most * 2, (void**)&t1));
+  TRY(vae_buf(v, "u", (size_t)most * 2, (void**)&u));
+  TRY(vae_buf(v, "t3", (size_t)most * 2, (void**)&t3));
+  TRY(vae_buf(v, "part", (size_t)kVaePartCap * 4, (void**)&v->part));
+  v->part_cap = kVaePartCap;
+  int hh = h, ww = w;
+  // encoder.conv1: RGBA neighbourhoods (t1, 64 bf16 a pixel) x the weights' (tap, channel) rows
+  {
+    const VT* wt = vae_t(v, "encoder.conv1.weight");
+    const VT* b = vae_t(v, "encoder.conv1.bias");
+    if (!wt || !b || wt->kp != 64) FAIL(EXN_ESTATE, "encoder: encoder.conv1 not loaded");
+    HIPCHK(vae_rgba_taps(s, h, w, rgba, t1));
+    const VaeEpi ep{nullptr, nullptr, 0, 0, nullptr, v->part, v->part_cap, nullptr, nullptr};
+    HIPCHK(vae_conv(s, 1, 0, VAE_F32, t1, (const uint16_t*)wt->p, (const float*)b->p, ep, A, h, w, 64, (int)wt->o, 64));
+  }
+  char p[96];
+  for (int si = 0; si < 5; ++si) {
+    const VStage& st = kVaeEncStages[si];
+    // A: the stage's input, kept for AvgDown3D (or the add) at the stage's end
+    snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.0", si);
+    TRY(vae_resblock(v, p, A, nullptr, nullptr, B, false, st.in, st.out, hh, ww, t1, t2, u, t3));
+    snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.1", si);
+    if (st.up) {
+      // the second block in bf16 for the stride-2 convolution, into B at half size, then
+      // AvgDown3D of A added
+      TRY(vae_resblock(v, p, B, nullptr, nullptr, u, true, st.out, st.out, hh, ww, t1, t2, u, t3));
+      snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.2.resample.1", si);
+      TRY(vae_conv_named(v, p, 2, VAE_F32, u, nullptr, C, hh / 2, ww / 2));
+      HIPCHK(vae_avgdown_add(s, st.in, st.out, st.tup ? 2 : 1, hh, ww, A, C));
+      hh /= 2;
+      ww /= 2;
+    } else {
+      TRY(vae_resblock(v, p, B, nullptr, nullptr, C, false, st.out, st.out, hh, ww, t1, t2, u, t3));
+      HIPCHK(vae_add(s, (int64_t)hh * ww * st.out, A, C));
+    }
+    std::swap(A, C);
+  }
+  TRY(vae_resblock(v, "encoder.middle.0", A, nullptr, nullptr, B, false, top, top, hh, ww, t1, t2, u, t3));
+  TRY(vae_attention(v, "encoder.middle.1", B, C, hh, ww, top, t1));
+  TRY(vae_resblock(v, "encoder.middle.2", C, nullptr, nullptr, A, false, top, top, hh, ww, t1, t2, u, t3));
+  const float* ghead = vae_vec(v, "encoder.head.0.gamma");
+  if (!ghead) FAIL(EXN_ESTATE, "encoder: missing encoder.head.0.gamma");
+  const int64_t n = (int64_t)hh * ww;
+  HIPCHK(vae_rms_silu(s, n, top, A, ghead, t1, 1));
+  TRY(vae_conv_named(v, "encoder.head.2", 0, VAE_BF16, t1, nullptr, u, hh, ww));
+  TRY(vae_conv_named(v, "conv1", 0, VAE_F32, u, nullptr, t2, hh, ww));
+  HIPCHK(vae_pixels_latent(s, n, kVaeZ, 2 * kVaeZ, t2, latent));
+  return EXN_OK;
+}
+
 extern "C" {
+
+int exn_vae_encode_dev(exn_vae* v, const float* rgba, int h, int w, float* latent) {
+  if (!v) FAIL(EXN_EINVAL, "null decoder");
+  TRY(use(v->ctx));
+  if (!rgba || !latent || h <= 0 || w <= 0 || h % 16 || w % 16 || (int64_t)h * w > ((int64_t)1 << 24))
+    FAIL(EXN_EINVAL, "vae encode: picture %d x %d (multiples of 16, at most 2^24 pixels)", h, w);
+  TRY(exn_vae_check_encoder(v));
+  return vae_encode(v, rgba, h, w, latent);
+}
+
+int exn_vae_encode(exn_vae* v, const float* rgba, int h, int w, float* latent) {
+  if (!v) FAIL(EXN_EINVAL, "null decoder");
+  TRY(use(v->ctx));
+  if (!rgba || !latent || h <= 0 || w <= 0 || h % 16 || w % 16 || (int64_t)h * w > ((int64_t)1 << 24))
+    FAIL(EXN_EINVAL, "vae encode: picture %d x %d (multiples of 16, at most 2^24 pixels)", h, w);
+  const int64_t npx = (int64_t)h * w * kVaeIn, nz = (int64_t)kVaeZ * (h / 16) * (w / 16);
+  float *dp, *dz;
+  TRY(vae_buf(v, "h_px", (size_t)npx * 4, (void**)&dp));
+  TRY(vae_buf(v, "h_z", (size_t)nz * 4, (void**)&dz));
+  HIPCHK(hipMemcpyAsync(dp, rgba, (size_t)npx * 4, hipMemcpyHostToDevice, v->ctx->stream));
+  TRY(exn_vae_encode_dev(v, dp, h, w, dz));
+  HIPCHK(hipMemcpyAsync(latent, dz, (size_t)nz * 4, hipMemcpyDeviceToHost, v->ctx->stream));
+  HIPCHK(hipStreamSynchronize(v->ctx->stream));
+  return EXN_OK;
+}
 
 int exn_vae_decode_dev(exn_vae* v, const float* latent, int h, int w, float* rgba) {
   if (!v) FAIL(EXN_EINVAL, "null decoder");
@@ -2277,6 +2438,15 @@ int exn_vae_dupup_add(exn_ctx* ctx, int cin, int cout, int ft, int h, int w, con
   TRY(use(ctx));
   if (!x || !y || cin <= 0 || cout <= 0 || ft < 1 || (int64_t)cout * ft * 4 % cin) FAIL(EXN_EINVAL, "dupup arguments");
   HIPCHK(vae_dupup_add(ctx->stream, cin, cout, ft, h, w, x, y));
+  return EXN_OK;
+}
+
+int exn_vae_avgdown_add(exn_ctx* ctx, int cin, int cout, int ft, int h, int w, const float* x, float* y) {
+  TRY(use(ctx));
+  if (!x || !y || cin <= 0 || cout <= 0 || ft < 1 || (int64_t)cin * ft * 4 % cout || h <= 0 || w <= 0 || h % 2 ||
+      w % 2)
+    FAIL(EXN_EINVAL, "avgdown arguments");
+  HIPCHK(vae_avgdown_add(ctx->stream, cin, cout, ft, h, w, x, y));
   return EXN_OK;
 }
 

@@ -237,7 +237,8 @@ hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uin
 
 // the VAE decoder (vae.hip).  vae_conv's outputs: fp32 (+ bias, + res when given), bf16 (+ bias,
 // + res when given), fp32 (+ bias) clamped to -1 .. 1, fp32 (+ bias, + DupUp3D of keep: kcin
-// channels at half size, frame ft - 1 of ft); taps 9 or 1; up: the input is the half-size picture
+// channels at half size, frame ft - 1 of ft); taps 9 or 1; up 1: the input is the half-size
+// picture; up 2: stride 2 over the double-size input (zero padding below and to the right)
 enum VaeOut { VAE_F32 = 0, VAE_BF16 = 1, VAE_CLAMP = 2, VAE_DUPUP = 3, VAE_PART = 4, VAE_RMS = 5 };
 struct VaeEpi {
   const float* res;    // VAE_F32 / VAE_BF16: added when not null (the output's layout)
@@ -260,6 +261,12 @@ hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x,
 hipError_t vae_rms_silu(hipStream_t s, int64_t P, int C, const float* x, const float* gamma, uint16_t* y, int silu);
 hipError_t vae_dupup_add(hipStream_t s, int cin, int cout, int ft, int h, int w, const float* x, float* y);
 hipError_t vae_latent_pixels(hipStream_t s, int64_t P, int C, const float* z, uint16_t* y);
+// the encoder's: AvgDown3D's shortcut (y, h/2 x w/2, += that of x, h x w), y += x, the first
+// convolution's RGBA neighbourhoods as rows of 64 bf16, the mean's channels out of pixel rows
+hipError_t vae_avgdown_add(hipStream_t s, int cin, int cout, int ft, int h, int w, const float* x, float* y);
+hipError_t vae_add(hipStream_t s, int64_t n, const float* x, float* y);
+hipError_t vae_rgba_taps(hipStream_t s, int h, int w, const float* x, uint16_t* y);
+hipError_t vae_pixels_latent(hipStream_t s, int64_t P, int C, int ld, const float* x, float* z);
 hipError_t vae_split_qkv(hipStream_t s, int64_t n, int64_t np, int c, const float* qkv, uint16_t* q, uint16_t* k,
                          uint16_t* vt);
 hipError_t vae_softmax_rows(hipStream_t s, int n, int np, float scale, const float* S, uint16_t* P);

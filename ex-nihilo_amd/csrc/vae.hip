@@ -40,22 +40,27 @@ __device__ __forceinline__ void conv_dma(const void* base, uint32_t extent, lds_
 #define VEPI_LDS (8 * 32 * 148 * 4)   // the epilogue's staging: 8 waves x 32 pixels x 148 floats
 
 // Tiles of 256 pixels x BN output channels, BN = 144 (3 LDS stages), 288 (2 stages; the
-// widths that 288 divides) or 16 (3 stages; the head's 4 channels): 8 waves of WM pixels x WNC
-// channels (WNC = 144, or 16 at BN 16), each a (WM/16) x (WNC/16) grid of
-// v_mfma_f32_16x16x32_bf16 -- 0.61 fragment reads an MFMA at BN 144, 0.36 at BN 288.
+// widths that 288 divides), 96 (3 stages) and 192 (2 stages; the encoder's 96 .. 768) or 16
+// (3 stages; the head's 4 channels): 8 waves of WM pixels x WNC channels (WNC = 144 where 144
+// divides BN, 96 where 96 does, else BN), each a (WM/16) x (WNC/16) grid of
+// v_mfma_f32_16x16x32_bf16 -- 0.61 fragment reads an MFMA at BN 144, 0.36 at BN 288, 0.42 at
+// BN 192.
 template <int BN>
 struct ConvTile {
-  static constexpr int WNC = BN >= 144 ? 144 : BN, NJ = WNC / 16;   // a wave's channels, its 16-column blocks
+  static constexpr int WNC = BN % 144 == 0 ? 144 : BN % 96 == 0 ? 96 : BN, NJ = WNC / 16;
   static constexpr int NWN = BN / WNC, NWM = 8 / NWN, WM = VBM / NWM, MI = WM / 16;
   static constexpr int LS = WNC + 4, RC = WNC / 4, NCH = 32 * RC / 64;   // staging: row floats, chunks a row, a lane
   static constexpr int STAGE = VBM * 128 + BN * 128;   // A rows | B rows, 64 bf16 of K each
   static constexpr int NST = BN <= 144 ? 3 : 2;
   static constexpr int BFULL = BN * 8 / 512;           // full B DMA rounds a step
   static constexpr int BREM = (BN * 8 - 512 * BFULL) / 8;   // lanes a wave in the partial round
-  static constexpr int NDMA = 4 + BFULL + 1;           // DMA instructions a wave a step
+  static constexpr int NDMA = 4 + BFULL + (BREM > 0);  // DMA instructions a wave a step
   static constexpr int LDS = NST * STAGE > VEPI_LDS ? NST * STAGE : VEPI_LDS;
 };
 
+// UP: 0 a 'same' convolution of an H x W picture; 1 the same of the picture nearest-upsampled
+// from H/2 x W/2 (the input); 2 stride 2 over a 2H x 2W input, padded with zeros below and to
+// the right (src/cuda/vae.cu's x_conv3s2: output pixel (y, x) takes input rows 2y .. 2y + 2).
 // OUT: VAE_F32 fp32 (+ bias, + res when given), VAE_BF16 bf16 (+ bias, + res when given),
 // VAE_CLAMP fp32 (+ bias) clamped to -1 .. 1, VAE_DUPUP fp32 (+ bias, + DupUp3D of keep),
 // VAE_PART the fp32 sums of k-steps kt0 .. kt1-1 only (workgroup z of a split K) into z's slice,
@@ -75,7 +80,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   // split K (VAE_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1
   const int KTT = Kp / 64, S = gridDim.z, z = blockIdx.z;
   const int kt0 = (int)((int64_t)KTT * z / S), kt1 = (int)((int64_t)KTT * (z + 1) / S);
-  const int Hs = UP ? H >> 1 : H, Ws = UP ? W >> 1 : W;
+  const int Hs = UP == 1 ? H >> 1 : UP == 2 ? 2 * H : H, Ws = UP == 1 ? W >> 1 : UP == 2 ? 2 * W : W;
   const uint32_t xext = (uint32_t)((int64_t)Hs * Ws * C * 2);
   const uint16_t* wbase = Wt + (int64_t)n0 * Kp;
   const uint32_t wext = (uint32_t)((int64_t)max(0, cout - n0) * Kp * 2);
@@ -100,8 +105,9 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   uint32_t boff[T::BFULL + 1];
 #pragma unroll
   for (int rd = 0; rd <= T::BFULL; ++rd) {
-    const int row = rd < T::BFULL ? 64 * rd + 8 * wave + (lane >> 3)
-                                  : 64 * T::BFULL + (T::BREM / 8) * wave + ((lane >> 3) % (T::BREM / 8));
+    int row = 64 * rd + 8 * wave + (lane >> 3);
+    if constexpr (T::BREM > 0)
+      if (rd == T::BFULL) row = 64 * T::BFULL + (T::BREM / 8) * wave + ((lane >> 3) % (T::BREM / 8));
     boff[rd] = (uint32_t)((row * Kp + 8 * ((lane & 7) ^ ((row >> 1) & 7))) * 2);
   }
   // issue the next k-step's tiles into stage s (the A chunks' positions then move on)
@@ -113,12 +119,13 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
       int dy = 0, dx = 0;
       if constexpr (TAPS == 9) {
         const int q = (tap * 11) >> 5;   // tap / 3 for tap < 9
-        dy = q - 1;
-        dx = tap - 3 * q - 1;
+        dy = UP == 2 ? q : q - 1;
+        dx = UP == 2 ? tap - 3 * q : tap - 3 * q - 1;
       }
-      int sy = py[i] + dy, sx = px[i] + dx;
-      const bool ok = tap < TAPS && sy >= 0 && sy < H && sx >= 0 && sx < W;
-      if constexpr (UP) {
+      // UP 2: a row past the picture has py -2^30, so sy stays negative (-2^31 + dy at least)
+      int sy = (UP == 2 ? 2 * py[i] : py[i]) + dy, sx = (UP == 2 ? 2 * px[i] : px[i]) + dx;
+      const bool ok = tap < TAPS && sy >= 0 && sy < (UP == 2 ? Hs : H) && sx >= 0 && sx < (UP == 2 ? Ws : W);
+      if constexpr (UP == 1) {
         sy >>= 1;
         sx >>= 1;
       }
@@ -133,8 +140,9 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
 #pragma unroll
     for (int rd = 0; rd < T::BFULL; ++rd)
       conv_dma(wbase, wext, (lds_void*)(st + 32768 + rd * 8192 + wave * 1024), boff[rd], t * 128);
-    if (lane < T::BREM)
-      conv_dma(wbase, wext, (lds_void*)(st + 32768 + T::BFULL * 8192 + wave * T::BREM * 16), boff[T::BFULL], t * 128);
+    if constexpr (T::BREM > 0)
+      if (lane < T::BREM)
+        conv_dma(wbase, wext, (lds_void*)(st + 32768 + T::BFULL * 8192 + wave * T::BREM * 16), boff[T::BFULL], t * 128);
   };
 
   // fragments: lane holds row lo of a 16-row block, K 8 q4 .. of a slice of 32
@@ -367,17 +375,22 @@ static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* 
   return hipGetLastError();
 }
 
+// the decoder's tiles (BN 144, 288: waves of 144 channels) take the norm in the store, the
+// clamp and the upsampling convolutions; the encoder's (BN 96, 192) the stride-2 ones
 template <int BN>
 static hipError_t conv_bn(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
                           const float* bias, const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp) {
+  constexpr bool DEC = ConvTile<BN>::WNC == 144;
   // a 3 x 3 convolution of fewer tiles than the chip's CUs (the decoder's 64 x 64 stages: 64
   // tiles) splits its K over up to 4 workgroups a tile, each at least 16 k-steps, into fp32
   // partials; k_part_sum adds them in order with bias and res
   if (ep.gamma) {   // the output's norm too: one channel tile (cout == BN), never split
-    if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
-    if (taps == 9 && !up && out == VAE_RMS) return launch_conv<BN, 9, 0, VAE_RMS, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
-    if (taps == 9 && up && out == VAE_DUPUP)
-      return launch_conv<BN, 9, 1, VAE_DUPUP, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    if constexpr (DEC) {
+      if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+      if (taps == 9 && !up && out == VAE_RMS) return launch_conv<BN, 9, 0, VAE_RMS, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+      if (taps == 9 && up == 1 && out == VAE_DUPUP)
+        return launch_conv<BN, 9, 1, VAE_DUPUP, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    }
     return hipErrorInvalidValue;
   }
   const int64_t P = (int64_t)h * w, tiles = grid_of(P, VBM) * (int64_t)grid_of(cout, BN);
@@ -391,9 +404,14 @@ static hipError_t conv_bn(hipStream_t s, int taps, int up, int out, const uint16
   }
   if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
   if (taps == 9 && !up && out == VAE_BF16) return launch_conv<BN, 9, 0, VAE_BF16>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
-  if (taps == 9 && !up && out == VAE_CLAMP) return launch_conv<BN, 9, 0, VAE_CLAMP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
-  if (taps == 9 && up && out == VAE_F32) return launch_conv<BN, 9, 1, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
-  if (taps == 9 && up && out == VAE_DUPUP) return launch_conv<BN, 9, 1, VAE_DUPUP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if constexpr (DEC) {
+    if (taps == 9 && !up && out == VAE_CLAMP) return launch_conv<BN, 9, 0, VAE_CLAMP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    if (taps == 9 && up == 1 && out == VAE_F32) return launch_conv<BN, 9, 1, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    if (taps == 9 && up == 1 && out == VAE_DUPUP)
+      return launch_conv<BN, 9, 1, VAE_DUPUP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  } else {
+    if (taps == 9 && up == 2 && out == VAE_F32) return launch_conv<BN, 9, 2, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  }
   if (taps == 1 && !up && out == VAE_F32) return launch_conv<BN, 1, 0, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
   if (taps == 1 && !up && out == VAE_BF16) return launch_conv<BN, 1, 0, VAE_BF16>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
   return hipErrorInvalidValue;
@@ -403,20 +421,25 @@ hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x,
                     const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp) {
   // the loads move 8 channels at once and each k-step moves a chunk's tap at most once; the
   // epilogue moves 4 channels at once; every offset and extent fits 31 bits
-  if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || cout % 4 || h <= 0 || w <= 0 ||
-      (up && (h % 2 || w % 2)) || ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || ((uintptr_t)y & 15) ||
+  // (up 2: the input is 2h x 2w)
+  const int64_t in_px = (int64_t)h * w * (up == 2 ? 4 : 1);
+  if (c < 64 || c % 8 || kp % 64 || kp < taps * c || cout <= 0 || cout % 4 || h <= 0 || w <= 0 || up < 0 || up > 2 ||
+      (up == 1 && (h % 2 || w % 2)) || (up == 2 && taps != 9) || ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || ((uintptr_t)y & 15) ||
       (!y && !(out == VAE_DUPUP && (ep.y2 || ep.yr)) && out != VAE_RMS) ||
       ((uintptr_t)bias & 15) || ((uintptr_t)ep.res & 15) || ((uintptr_t)ep.y2 & 7) || ((uintptr_t)ep.part & 15) ||
       (ep.gamma && (!ep.yr || ((uintptr_t)ep.yr & 7) || ((uintptr_t)ep.gamma & 15) || (cout != 144 && cout != 288))) ||
       (!ep.gamma && out == VAE_RMS) ||
-      (int64_t)h * w * c * 2 >= ((int64_t)1 << 31) || (int64_t)cout * kp * 2 >= ((int64_t)1 << 31) ||
+      in_px * c * 2 >= ((int64_t)1 << 31) || (int64_t)cout * kp * 2 >= ((int64_t)1 << 31) ||
       (int64_t)h * w * cout >= ((int64_t)1 << 31) ||
       (out == VAE_DUPUP && (!ep.keep || ep.ft < 1 || ep.kcin <= 0 || (int64_t)cout * ep.ft * 4 % ep.kcin || h % 2 ||
                             w % 2 || ((cout * ep.ft * 4 / ep.kcin) & (cout * ep.ft * 4 / ep.kcin - 1)))))
     return hipErrorInvalidValue;
-  // the wide tile where 288 divides the width (1152, 576, 288 and the 3456 of q|k|v); a narrow
-  // one for a few channels (the head's 4): 16 columns of MFMA work instead of 144
+  // the wide tile where 288 divides the width (1152, 576, 288 and the 3456 of q|k|v); 144 for
+  // the decoder's 144; 192 and 96 for the encoder's widths (96, 192, 384, 768); a narrow one
+  // for a few channels (the head's 4): 16 columns of MFMA work instead of 144
   if (cout % 288 == 0) return conv_bn<288>(s, taps, up, out, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (cout % 144 != 0 && cout % 192 == 0) return conv_bn<192>(s, taps, up, out, x, wt, bias, ep, y, h, w, c, cout, kp);
+  if (cout % 144 != 0 && cout % 96 == 0) return conv_bn<96>(s, taps, up, out, x, wt, bias, ep, y, h, w, c, cout, kp);
   if (cout <= 16 && !ep.gamma) {
     if (taps == 9 && !up && out == VAE_CLAMP) return launch_conv<16, 9, 0, VAE_CLAMP>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
     if (taps == 9 && !up && out == VAE_F32) return launch_conv<16, 9, 0, VAE_F32>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
@@ -554,6 +577,95 @@ hipError_t vae_dupup_add(hipStream_t s, int cin, int cout, int ft, int h, int w,
   const int64_t n = 4LL * h * w * cout;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(k_dupup_add, dim3(grid_of(n, 256)), dim3(256), 0, s, cin, cout, ft, h, w, x, y);
+  return hipGetLastError();
+}
+
+// y (H/2 x W/2 x cout, fp32) += AvgDown3D(x) (H x W x cin) on one frame, padded in front to ft
+// frames with zeros (src/cuda/vae.cu's x_avgdown_add): output channel o of pixel (Y, X) is the
+// mean of the g = cin ft 4 / cout values j = o g .. o g + g - 1 of the view (cin, ft, 2, 2) of
+// the 2 x 2 block at (2Y, 2X): channel j / (4 ft), frame (j / 4) % ft (zero but the last), row
+// 2Y + (j / 2) % 2, column 2X + j % 2.  One thread an output value.
+__global__ void k_avgdown_add(int cin, int cout, int ft, int H, int W, const float* __restrict__ x,
+                              float* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int ow = W / 2;
+  if (i >= (int64_t)(H / 2) * ow * cout) return;
+  const int o = (int)(i % cout);
+  const int64_t p = i / cout;
+  const int yy = (int)(p / ow), xx = (int)(p % ow);
+  const int g = cin * ft * 4 / cout;
+  float acc = 0.f;
+  for (int k = 0; k < g; ++k) {
+    const int j = o * g + k;
+    if ((j >> 2) % ft != ft - 1) continue;   // a padding frame: zero
+    acc += x[((int64_t)(2 * yy + ((j >> 1) & 1)) * W + 2 * xx + (j & 1)) * cin + j / (4 * ft)];
+  }
+  y[i] += acc / (float)g;
+}
+
+hipError_t vae_avgdown_add(hipStream_t s, int cin, int cout, int ft, int h, int w, const float* x, float* y) {
+  if (cin <= 0 || cout <= 0 || ft < 1 || (int64_t)cin * ft * 4 % cout || h % 2 || w % 2) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)(h / 2) * (w / 2) * cout;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_avgdown_add, dim3(grid_of(n, 256)), dim3(256), 0, s, cin, cout, ft, h, w, x, y);
+  return hipGetLastError();
+}
+
+// y += x over n floats (4 a thread; n a multiple of 4)
+__global__ void k_add4(int64_t n4, const float* __restrict__ x, float* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n4) ((f32x4*)y)[i] += ((const f32x4*)x)[i];
+}
+
+hipError_t vae_add(hipStream_t s, int64_t n, const float* x, float* y) {
+  if (n % 4) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_add4, dim3(grid_of(n / 4, 256)), dim3(256), 0, s, n / 4, x, y);
+  return hipGetLastError();
+}
+
+// the encoder's first convolution's input: each pixel's 3 x 3 neighbourhood of RGBA (x: H x W
+// x 4 fp32) as one row of 64 bf16, k = tap 4 + channel for k < 36 (tap = 3 (dy + 1) + dx + 1,
+// off the picture zero), zeros after -- a 1 x 1 product with the weights packed as (tap,
+// channel) rows then is the 3 x 3 'same' convolution.  One thread 8 values of a row.
+__global__ void k_rgba_taps(int H, int W, const float* __restrict__ x, uint16_t* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)H * W * 8) return;
+  const int64_t p = i >> 3;
+  const int k0 = 8 * (int)(i & 7);
+  const int py = (int)(p / W), px = (int)(p % W);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int k = k0 + e, tap = k >> 2, c = k & 3;
+    const int sy = py + tap / 3 - 1, sx = px + tap % 3 - 1;
+    v[e] = k < 36 && sy >= 0 && sy < H && sx >= 0 && sx < W ? x[((int64_t)sy * W + sx) * 4 + c] : 0.f;
+  }
+  *(u32x4*)(y + p * 64 + k0) =
+      u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+}
+
+hipError_t vae_rgba_taps(hipStream_t s, int h, int w, const float* x, uint16_t* y) {
+  const int64_t n = (int64_t)h * w * 8;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rgba_taps, dim3(grid_of(n, 256)), dim3(256), 0, s, h, w, x, y);
+  return hipGetLastError();
+}
+
+// the first C of each pixel row's LD fp32 values, channel-major: z[c][p] = x[p][c] (the
+// encoder's mean, out of its 2 z channels)
+__global__ void k_pixels_latent(int64_t P, int C, int ld, const float* __restrict__ x, float* __restrict__ z) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= P * C) return;
+  const int c = (int)(i / P);
+  const int64_t p = i % P;
+  z[i] = x[p * ld + c];
+}
+
+hipError_t vae_pixels_latent(hipStream_t s, int64_t P, int C, int ld, const float* x, float* z) {
+  if (C > ld) return hipErrorInvalidValue;
+  if (P * C == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_pixels_latent, dim3(grid_of(P * C, 256)), dim3(256), 0, s, P, C, ld, x, z);
   return hipGetLastError();
 }
 

@@ -104,6 +104,9 @@ SIGNATURES = {
     "exn_vae_set": (c_int, [vp, c_char_p, c_int, vp, POINTER(c_int64), c_int]),
     "exn_vae_synth": (c_int, [vp, c_uint64]),
     "exn_vae_check": (c_int, [vp]),
+    "exn_vae_check_encoder": (c_int, [vp]),
+    "exn_vae_encode": (c_int, [vp, vp, c_int, c_int, vp]),
+    "exn_vae_encode_dev": (c_int, [vp, vp, c_int, c_int, vp]),
     "exn_vae_decode": (c_int, [vp, vp, c_int, c_int, vp]),
     "exn_vae_decode_dev": (c_int, [vp, vp, c_int, c_int, vp]),
     "exn_vae_release": (c_int, [vp]),
@@ -113,6 +116,7 @@ SIGNATURES = {
                              c_int64]),
     "exn_vae_rms_silu": (c_int, [vp, c_int64, c_int, vp, vp, vp, c_int]),
     "exn_vae_dupup_add": (c_int, [vp, c_int, c_int, c_int, c_int, c_int, vp, vp]),
+    "exn_vae_avgdown_add": (c_int, [vp, c_int, c_int, c_int, c_int, c_int, vp, vp]),
     "exn_vision_create": (c_int, [vp, POINTER(vp)]),
     "exn_vision_set": (c_int, [vp, c_char_p, c_int, vp, POINTER(c_int64), c_int]),
     "exn_vision_synth": (c_int, [vp, c_uint64]),
@@ -457,10 +461,10 @@ def generate_latent(d: Dit, context: np.ndarray, p: int, z: np.ndarray, h: int, 
     return z
 
 
-# --- the VAE decoder: upload-vae, vae-decode, vae-release (src/cuda-vae.lisp) -------------
+# --- the VAE: upload-vae, vae-decode, vae-encode, vae-release (src/cuda-vae.lisp) ----------
 
 class Vae:
-    """The decoder on the device: its tensors and scratch (gvae)."""
+    """The decoder and encoder on the device: their tensors and scratch (gvae)."""
 
     def __init__(self, ctx: Context):
         h = vp()
@@ -477,6 +481,9 @@ class Vae:
 
     def check(self):
         call("exn_vae_check", self.h)
+
+    def check_encoder(self):
+        call("exn_vae_check_encoder", self.h)
 
     def memory(self):
         w, s = c_int64(), c_int64()
@@ -516,6 +523,18 @@ def vae_decode(v: Vae, latent: np.ndarray, h: int, w: int):
     px = np.empty((16 * h, 16 * w, 4), np.float32)
     call("exn_vae_decode", v.h, ptr(lat), h, w, ptr(px))
     return px, 16 * h, 16 * w
+
+
+def vae_encode(v: Vae, px: np.ndarray, h: int, w: int) -> np.ndarray:
+    """vae-encode (src/cuda-vae.lisp:138-190): PX (H x W x 4 floats, RGBA in -1..1, rows of
+    W pixels; H and W multiples of 16) -> the latent's mean, 64 x H/16 x W/16 floats
+    channel-major, as vae_decode takes it (denormalized)."""
+    x = np.ascontiguousarray(px, dtype=np.float32).reshape(-1)
+    if x.size != h * w * 4:
+        raise ExnError(EINVAL, "picture of %d floats for %d x %d RGBA" % (x.size, h, w))
+    z = np.empty((64, h // 16, w // 16), np.float32)
+    call("exn_vae_encode", v.h, ptr(x), h, w, ptr(z))
+    return z
 
 
 def vae_release(v: Vae):

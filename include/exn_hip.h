@@ -252,33 +252,45 @@ int exn_dit_destroy(exn_dit* d);
 /* bytes of device memory the model holds: weights, scratch, kept K/V */
 int exn_dit_memory(exn_dit* d, int64_t* weights, int64_t* scratch);
 
-/* --- the VAE decoder (replaces src/cuda-vae.lisp's gvae and src/cuda/vae.cu) ---------- */
+/* --- the VAE decoder and encoder (replace src/cuda-vae.lisp's gvae and src/cuda/vae.cu) --- */
 typedef struct exn_vae exn_vae;
 /* upload-vae (src/cuda-vae.lisp:15-26) in parts: create, then one exn_vae_set a tensor */
 int exn_vae_create(exn_ctx* ctx, exn_vae** out);
-/* one decoder tensor by its safetensors name and shape (NDIMS dims, row-major), KIND
+/* one decoder or encoder tensor by its safetensors name and shape (NDIMS dims, row-major), KIND
  * EXN_BF16 (the file's bit patterns) or EXN_F32; names and shapes held against vae-expected
- * (src/weights.lisp:69-98).  A convolution's (o, i, [1,] k, k) weights are kept as bf16 rows
+ * and vae-encoder-expected (src/weights.lisp:69-134; the video-only time_conv tensors are not
+ * taken).  A convolution's (o, i, [1,] k, k) weights are kept as bf16 rows
  * of (ky, kx, ci), as src/host.lisp:73-90 lays them out for the GPU. */
 int exn_vae_set(exn_vae* v, const char* name, int kind, const void* data, const int64_t* dims, int ndims);
-/* test hook: every decoder tensor made on the device by the synthetic generator (bf16 values) */
+/* test hook: every decoder and encoder tensor made on the device by the synthetic generator
+ * (bf16 values) */
 int exn_vae_synth(exn_vae* v, uint64_t seed);
 /* EXN_OK when every decoder tensor is present, else EXN_ESTATE naming the first missing one
  * (open-vae's check, src/weights.lisp:136-147) */
 int exn_vae_check(exn_vae* v);
+/* the same for the encoder's tensors (open-vae checks both, src/weights.lisp:136-147; here a
+ * decoder may be loaded alone, and exn_vae_encode makes this check) */
+int exn_vae_check_encoder(exn_vae* v);
 /* vae-decode (src/cuda-vae.lisp:94-136): LATENT (64 x H x W floats, channel-major,
  * denormalized) -> RGBA (16H x 16W x 4 floats in -1..1, rows of pixels, channels last).
  * Host arrays; exn_vae_decode_dev takes device arrays, on the context's stream. */
 int exn_vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba);
 int exn_vae_decode_dev(exn_vae* v, const float* latent, int h, int w, float* rgba);
+/* vae-encode (src/cuda-vae.lisp:138-190): RGBA (H x W x 4 floats in -1..1, rows of pixels; H
+ * and W multiples of 16) -> the latent's mean (64 x H/16 x W/16 floats, channel-major, as
+ * exn_vae_decode takes it: denormalized).  Host arrays; exn_vae_encode_dev takes device
+ * arrays, on the context's stream. */
+int exn_vae_encode(exn_vae* v, const float* rgba, int h, int w, float* latent);
+int exn_vae_encode_dev(exn_vae* v, const float* rgba, int h, int w, float* latent);
 /* vae-release (src/cuda-vae.lisp:28-33): the scratch freed, the weights kept */
 int exn_vae_release(exn_vae* v);
 int exn_vae_destroy(exn_vae* v);
 /* bytes of device memory the decoder holds: weights, scratch */
 int exn_vae_memory(exn_vae* v, int64_t* weights, int64_t* scratch);
-/* the decoder's kernels one at a time (src/cuda/vae.cu's x_conv3 with the 1 x 1 products,
- * x_up2 folded in (UP), bias and residual fused; v_rms with x_silu; x_dupup_add).  X: bf16 pixel
- * rows (H x W x C, or H/2 x W/2 x C with UP); WT: bf16 rows of (tap, channel), KP long (a
+/* the decoder's and encoder's kernels one at a time (src/cuda/vae.cu's x_conv3 with the 1 x 1
+ * products, x_up2 folded in (UP 1), x_conv3s2 (UP 2), bias and residual fused; v_rms with
+ * x_silu; x_dupup_add; x_avgdown_add).  X: bf16 pixel rows (H x W x C; H/2 x W/2 x C with UP 1;
+ * 2H x 2W x C with UP 2, the output H x W); WT: bf16 rows of (tap, channel), KP long (a
  * multiple of 64, zero past TAPS * C); OUTDT 0 fp32 (+ RES when not null), 1 bf16, 2 fp32
  * clamped to -1..1.  C a multiple of 8, at least 64.  PART (PART_CAP floats, or null): scratch
  * with which a 3 x 3 convolution of fewer 256 x 288 tiles than the chip has CUs splits its K
@@ -287,6 +299,8 @@ int exn_vae_conv(exn_ctx* ctx, int taps, int up, int outdt, const uint16_t* x, c
                  const float* res, void* y, int h, int w, int c, int cout, int kp, float* part, int64_t part_cap);
 int exn_vae_rms_silu(exn_ctx* ctx, int64_t n, int c, const float* x, const float* gamma, uint16_t* y, int silu);
 int exn_vae_dupup_add(exn_ctx* ctx, int cin, int cout, int ft, int h, int w, const float* x, float* y);
+/* Y (H/2 x W/2 x COUT) += AvgDown3D(X) (H x W x CIN), frame FT - 1 of FT */
+int exn_vae_avgdown_add(exn_ctx* ctx, int cin, int cout, int ft, int h, int w, const float* x, float* y);
 
 /* --- the vision tower (replaces src/cuda-vision.lisp's q3vision and src/cuda/qvision.cu) -----
  * Qwen3-VL's ViT, which lets the prompt encoder see a picture to edit: 27 blocks of 1152, 16

@@ -1,4 +1,4 @@
-"""exn_vae_oracle -- the CPU restatement of ex-nihilo's VAE decoder, float32 numpy.
+"""exn_vae_oracle -- the CPU restatement of ex-nihilo's VAE decoder and encoder, float32 numpy.
 
 TEST INFRASTRUCTURE ONLY.  Tests and the benchmark's checks use this module as
 the checker; the product path (libexn-hip.so and the exn_hip host package)
@@ -13,7 +13,14 @@ It restates:
   - src/weights.lisp:65-98: the stages and the decoder's tensor names and
     shapes (vae-expected);
   - src/cuda-vae.lisp:94-136: the output as 16H x 16W rows of RGBA (channels
-    last), the reference script writing it channel-major.
+    last), the reference script writing it channel-major;
+  - the encoder, src/cuda-vae.lisp:138-190 with src/weights.lisp:100-134 (its
+    stages, names and shapes) and src/cuda/vae.cu's x_conv3s2 and
+    x_avgdown_add (the stride-2 convolution, zero-padded below and to the
+    right; AvgDown3D on one frame, padded in front with zero frames): conv1 on
+    RGBA, per stage two residual blocks then the stride-2 convolution plus
+    AvgDown3D of the stage's input (or the input added), the middle, the head
+    (norm, SiLU, 3 x 3 to the mean and log-variance, conv1), the mean kept.
 Activations here are channels last (H, W, C), the layout the GPU decoder uses;
 inspect/ref_vae.py keeps them channel-major, which changes no arithmetic.
 
@@ -24,7 +31,15 @@ VAE_ID0 on.
 How it is pinned (tests/test_vae_oracle.py): decode against vectors that the
 reference's own inspect/ref_vae.py wrote from the same synthetic weights
 (tests/golden/ref_vae_tiny.npz, made by tests/golden/make_ref_vae_vectors.py);
-the pieces against float64 brute force and closed forms.
+the pieces against float64 brute force and closed forms.  The encoder shares
+conv, rms, silu, resblock and attention with the decoder (pinned there); its own
+pieces are pinned by brute force (the stride-2 convolution) and by the index
+formula of x_avgdown_add against the view-and-mean form here; its stage wiring
+by a closed form on weights that make every block an identity.  Parity
+unpinned: the encoder's composition as a whole has no reference vectors (the
+reference's inspect/ref_vae.py holds the decoder only, and diffusers is not
+installed), so beyond those checks it rests on reading src/cuda-vae.lisp and
+src/metal-vae.lisp.
 """
 from __future__ import annotations
 
@@ -77,8 +92,53 @@ def vae_expected(stages=STAGES, z=Z, out=OUT):
     return r
 
 
-def vae_tensor_id(name, stages=STAGES):
-    return VAE_ID0 + [n for n, _ in vae_expected(stages)].index(name)
+# the encoder: (in, out, spatial down, temporal down), the picture's end first
+# (src/weights.lisp:100-102)
+ENC_STAGES = ((96, 96, True, False), (96, 192, True, True), (192, 384, True, True),
+              (384, 768, True, True), (768, 768, False, False))
+IN = 4          # RGBA
+
+
+def vae_encoder_expected(enc_stages=ENC_STAGES, z=Z, inp=IN):
+    """(name, shape) of every tensor the encoder reads, in src/weights.lisp:104-134's
+    order (the video-only time_conv tensors left out)."""
+    top = enc_stages[-1][1]
+    r = []
+
+    def conv(name, o, i, k, frames=True):
+        r.append((name + ".weight", (o, i, 1, k, k) if frames else (o, i, k, k)))
+        r.append((name + ".bias", (o,)))
+
+    def res(p, i, o):
+        r.append((p + ".residual.0.gamma", (i, 1, 1, 1)))
+        conv(p + ".residual.2", o, i, 3)
+        r.append((p + ".residual.3.gamma", (o, 1, 1, 1)))
+        conv(p + ".residual.6", o, o, 3)
+        if i != o:
+            conv(p + ".shortcut", o, i, 1)
+
+    conv("encoder.conv1", enc_stages[0][0], inp, 3)
+    for s, (i, o, down, _td) in enumerate(enc_stages):
+        for j in range(2):
+            res("encoder.downsamples.%d.downsamples.%d" % (s, j), i if j == 0 else o, o)
+        if down:
+            conv("encoder.downsamples.%d.downsamples.2.resample.1" % s, o, o, 3, frames=False)
+    res("encoder.middle.0", top, top)
+    r.append(("encoder.middle.1.norm.gamma", (top, 1, 1)))
+    conv("encoder.middle.1.to_qkv", 3 * top, top, 1, frames=False)
+    conv("encoder.middle.1.proj", top, top, 1, frames=False)
+    res("encoder.middle.2", top, top)
+    r.append(("encoder.head.0.gamma", (top, 1, 1, 1)))
+    conv("encoder.head.2", 2 * z, top, 3)
+    conv("conv1", 2 * z, 2 * z, 1)
+    return r
+
+
+def vae_tensor_id(name, stages=STAGES, enc_stages=ENC_STAGES):
+    """The generator's id of a tensor: VAE_ID0 + its index in the decoder's list, then the
+    encoder's."""
+    names = [n for n, _ in vae_expected(stages)] + [n for n, _ in vae_encoder_expected(enc_stages)]
+    return VAE_ID0 + names.index(name)
 
 
 def synth_scale(name, shape):
@@ -92,7 +152,8 @@ def synth_scale(name, shape):
     if name.endswith(".bias"):
         return 0.0, 0.02
     fan = int(np.prod(shape[1:]))
-    g = 0.5 if (".residual.6." in name or name.startswith("decoder.middle.1.proj")) else 1.0
+    g = 0.5 if (".residual.6." in name or name.startswith("decoder.middle.1.proj")
+                or name.startswith("encoder.middle.1.proj")) else 1.0
     if name.startswith("decoder.head.2"):
         g = 1.2
     return 0.0, g / np.sqrt(fan)
@@ -111,16 +172,16 @@ def normal_fast(seed, tensor, n):
 class SynthVae:
     """wt(name) -> the tensor as float32 in the file's shape, each value a bf16."""
 
-    def __init__(self, seed, stages=STAGES):
-        self.seed, self.stages = seed, stages
-        self.shapes = dict(vae_expected(stages))
+    def __init__(self, seed, stages=STAGES, enc_stages=ENC_STAGES):
+        self.seed, self.stages, self.enc_stages = seed, stages, enc_stages
+        self.shapes = dict(vae_expected(stages) + vae_encoder_expected(enc_stages))
         self.cache = {}
 
     def __call__(self, name):
         if name not in self.cache:
             shape = self.shapes[name]
             base, scale = synth_scale(name, shape)
-            z = normal_fast(self.seed, vae_tensor_id(name, self.stages), int(np.prod(shape)))
+            z = normal_fast(self.seed, vae_tensor_id(name, self.stages, self.enc_stages), int(np.prod(shape)))
             self.cache[name] = xo.bf16_round(np.float32(base) + np.float32(scale) * z).reshape(shape)
         return self.cache[name]
 
@@ -219,6 +280,69 @@ def decode(wt, z, stages=STAGES, on_stage=None):
     return np.clip(x, -1, 1).astype(np.float32)
 
 
+# --- the encoder (src/cuda-vae.lisp:138-190), channels last --------------------------
+
+def conv3s2(x, w, b):
+    """x: (2H, 2W, C) -> (H, W, O): the 3 x 3 convolution at stride 2, the input padded with one
+    row of zeros below and one column to the right (src/cuda/vae.cu's x_conv3s2: output pixel
+    (y, x) takes input rows 2y .. 2y + 2 and columns 2x .. 2x + 2); + b."""
+    o, c = w.shape[0], w.shape[1]
+    w = w.reshape(o, c, 3, 3)
+    h2, w2, _ = x.shape
+    h, wd = h2 // 2, w2 // 2
+    xp = np.pad(x, ((0, 1), (0, 1), (0, 0)))
+    out = np.zeros((h * wd, o), dtype=np.float32)
+    for dy in range(3):
+        for dx in range(3):
+            out += xp[dy:dy + 2 * h:2, dx:dx + 2 * wd:2].reshape(-1, c) @ w[:, :, dy, dx].T
+    return out.reshape(h, wd, o) + b
+
+
+def avgdown(x, out_c, ft, fs=2):
+    """AvgDown3D on one frame, padded in front to FT frames with zeros: the (C, FT, fs, fs) view
+    of each fs x fs block (channel, frame, row, column: frames 0 .. ft-2 zero, the last the
+    block) flattened, cut into OUT_C groups of g = C ft fs^2 / OUT_C, each group's mean -- the
+    view-and-mean form of AvgDown3D."""
+    h, w, c = x.shape
+    g = c * ft * fs * fs // out_c
+    blocks = x.reshape(h // fs, fs, w // fs, fs, c).transpose(0, 2, 4, 1, 3)   # H', W', C, fs, fs
+    full = np.zeros((h // fs, w // fs, c, ft, fs, fs), np.float32)
+    full[:, :, :, ft - 1] = blocks
+    return full.reshape(h // fs, w // fs, out_c, g).mean(-1, dtype=np.float64).astype(np.float32)
+
+
+def encode(wt, px, enc_stages=ENC_STAGES, z=Z, on_stage=None):
+    """px: (H, W, 4) RGBA in -1..1 (H, W multiples of 16) -> the latent's mean, (64, H/16, W/16)
+    float32 channel-major, denormalized (src/cuda-vae.lisp:138-190)."""
+    x = conv(np.asarray(px, np.float32), wt("encoder.conv1.weight"), wt("encoder.conv1.bias"), 3)
+    for s, (i, o, down, tdown) in enumerate(enc_stages):
+        keep = x
+        for j in range(2):
+            x = resblock(wt, "encoder.downsamples.%d.downsamples.%d" % (s, j), x)
+        if down:
+            p = "encoder.downsamples.%d.downsamples.2.resample.1" % s
+            x = conv3s2(x, wt(p + ".weight"), wt(p + ".bias")) + avgdown(keep, o, 2 if tdown else 1)
+        else:
+            x = x + keep
+        if on_stage:
+            on_stage(s, x)
+    x = resblock(wt, "encoder.middle.0", x)
+    x = attention(wt, "encoder.middle.1", x)
+    x = resblock(wt, "encoder.middle.2", x)
+    x = silu(rms(x, wt("encoder.head.0.gamma")))
+    x = conv(x, wt("encoder.head.2.weight"), wt("encoder.head.2.bias"), 3)
+    x = conv(x, wt("conv1.weight"), wt("conv1.bias"), 1)
+    return np.ascontiguousarray(x[..., :z].transpose(2, 0, 1)).astype(np.float32)
+
+
+INPUT_VAE_PICTURE = 4998
+
+
+def synth_picture(seed, h, w):
+    """An encoder input: h x w RGBA, each value 0.5 z clipped to -1 .. 1."""
+    return np.clip(np.float32(0.5) * xo.normal(seed, INPUT_VAE_PICTURE, h * w * 4), -1, 1).reshape(h, w, 4)
+
+
 # --- work counts -----------------------------------------------------------------
 
 def decode_flops(h, w, stages=STAGES, z=Z, out=OUT):
@@ -242,4 +366,26 @@ def decode_flops(h, w, stages=STAGES, z=Z, out=OUT):
             hh, ww = 2 * hh, 2 * ww
             f += 2 * hh * ww * o * o * 9
     f += 2 * hh * ww * stages[-1][1] * out * 9
+    return f
+
+
+def encode_flops(h, w, enc_stages=ENC_STAGES, z=Z, inp=IN):
+    """Algorithmic FLOPs of one encode of an h x w picture: every convolution's
+    2 * pixels * cin * cout * taps (the first at its 4 input channels), the attention's two
+    products."""
+    def res(n, i, o):
+        return 2 * n * (i * o * 9 + o * o * 9 + (i * o if i != o else 0))
+
+    f = 2 * h * w * inp * enc_stages[0][0] * 9
+    hh, ww = h, w
+    for i, o, down, _ in enc_stages:
+        n = hh * ww
+        f += res(n, i, o) + res(n, o, o)
+        if down:
+            hh, ww = hh // 2, ww // 2
+            f += 2 * hh * ww * o * o * 9
+    n, top = hh * ww, enc_stages[-1][1]
+    f += 2 * res(n, top, top)
+    f += 2 * n * top * 3 * top + 2 * 2 * n * n * top + 2 * n * top * top
+    f += 2 * n * top * 2 * z * 9 + 2 * n * 2 * z * 2 * z
     return f

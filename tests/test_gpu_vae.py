@@ -1,4 +1,4 @@
-"""The VAE decoder on the GPU through the C ABI, against the oracle
+"""The VAE decoder and encoder on the GPU through the C ABI, against the oracle
 (oracle/exn_vae_oracle.py) and the reference script's own pictures
 (tests/golden/ref_vae_tiny.npz).  The picture's bar is the reference's for its
 half-precision decoder against the decoder in floats: within 3 of 255
@@ -64,6 +64,15 @@ CONV_CASES = [  # (h, w, c, cout, taps, up, out, with res)
     (11, 5, 288, 144, 1, 0, 0, True),
     (4, 4, 64, 64, 1, 0, 1, False),
     (10, 7, 64, 12, 9, 0, 0, True),      # the narrow tile (16 columns) with a residual
+    # the encoder's: stride 2 (the input 2h x 2w), the 96- and 192-wide tiles
+    (12, 20, 96, 96, 9, 2, 0, False),
+    (40, 36, 192, 384, 9, 2, 0, True),
+    (7, 5, 768, 768, 9, 2, 0, False),
+    (17, 15, 96, 192, 9, 0, 0, True),
+    (9, 11, 384, 768, 9, 0, 1, False),
+    (13, 7, 96, 192, 1, 0, 0, True),
+    (21, 19, 64, 96, 1, 0, 0, False),   # encoder.conv1: a 1 x 1 product over RGBA neighbourhoods
+    (6, 6, 768, 128, 9, 0, 1, False),   # the encoder's head: 128 of a 144-wide tile
 ]
 
 
@@ -72,26 +81,30 @@ SPLIT_CASES = [  # split K: fewer tiles than CUs, 3 x 3, no upsampling, fp32 or 
     (9, 7, 576, 288, 9, 0, 1, True),
     (16, 20, 288, 144, 9, 0, 0, False),
     (4, 4, 1152, 576, 9, 0, 0, True),
+    (8, 8, 768, 768, 9, 0, 0, True),     # the 192-wide tile split
 ]
 
 
 @pytest.mark.parametrize("case,split", [(c, False) for c in CONV_CASES] + [(c, True) for c in SPLIT_CASES])
 def test_conv_against_float64(ctx, case, split):
     """The implicit-GEMM convolution: partial pixel and channel tiles, K not a
-    multiple of 64 (144, 288 wide), the upsampling fold, the three outputs; with a
+    multiple of 64 (144, 288 wide), the upsampling fold, stride 2, the three outputs; with a
     partials buffer, K split over up to 4 workgroups a tile (their sum in order)."""
     h, w, c, cout, taps, up, out, with_res = case
     say("conv", case, "split" if split else "")
     rng = np.random.default_rng(h * 1000 + c + cout)
-    hs, ws = (h // 2, w // 2) if up else (h, w)
+    hs, ws = (h // 2, w // 2) if up == 1 else (2 * h, 2 * w) if up == 2 else (h, w)
     x = xo.bf16_round(rng.standard_normal((hs, ws, c)).astype(np.float32))
     k = 3 if taps == 9 else 1
     wt = xo.bf16_round((rng.standard_normal((cout, c, 1, k, k)) / np.sqrt(c * taps)).astype(np.float32))
     b = rng.standard_normal(cout).astype(np.float32) * 0.1
     kp = (taps * c + 63) // 64 * 64
     res = rng.standard_normal((h * w, cout)).astype(np.float32) if with_res else None
-    xin = np.repeat(np.repeat(x, 2, 0), 2, 1) if up else x
-    want = vo.conv(xin.astype(np.float64), wt.astype(np.float64), b.astype(np.float64), k).reshape(h * w, cout)
+    xin = np.repeat(np.repeat(x, 2, 0), 2, 1) if up == 1 else x
+    if up == 2:
+        want = vo.conv3s2(x.astype(np.float64), wt.astype(np.float64), b.astype(np.float64)).reshape(h * w, cout)
+    else:
+        want = vo.conv(xin.astype(np.float64), wt.astype(np.float64), b.astype(np.float64), k).reshape(h * w, cout)
     if with_res:
         want = want + res
     if out == 2:
@@ -199,3 +212,106 @@ def test_vae_set_and_check_errors(ctx):
     assert e.value.code == X.EINVAL
     v.set("decoder.head.2.bias", X.BF16, xo.bf16_bits(np.array([0.5, -0.25, 0, 1], np.float32)), (4,))
     v.destroy()
+
+
+# --- the encoder ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("cin,cout,ft,h,w", [(96, 96, 1, 8, 12), (96, 192, 2, 6, 4), (384, 768, 2, 4, 6),
+                                             (192, 384, 2, 10, 2)])
+def test_avgdown_add(ctx, cin, cout, ft, h, w):
+    """AvgDown3D's shortcut, added: against the oracle's view-and-mean form (fp32 sums of at
+    most 8 values in another order: 1e-6)."""
+    rng = np.random.default_rng(cin + cout + h)
+    x = rng.standard_normal((h, w, cin)).astype(np.float32)
+    y0 = rng.standard_normal((h // 2, w // 2, cout)).astype(np.float32)
+    yb = X.DevBuf.of(ctx, y0)
+    X.call("exn_vae_avgdown_add", ctx.h, cin, cout, ft, h, w, dev(ctx, x).h, yb.h)
+    want = y0 + vo.avgdown(x, cout, ft)
+    assert np.abs(yb.get() - want).max() <= 1e-6 * max(1.0, np.abs(want).max())
+
+
+ENC_SEED = 23
+
+
+@pytest.fixture(scope="module")
+def enc_vae(ctx):
+    v = X.upload_vae(seed=ENC_SEED, ctx=ctx)
+    v.check_encoder()
+    yield v
+    v.destroy()
+
+
+# the latent's distance to the oracle: bf16 operands (8 significant bits) in every convolution
+# and the attention, through 14 residual blocks; measured 5.4e-3 .. 5.7e-3 (2.7e-3 with the
+# blocks identities), bar 1e-2
+ENC_REL = 1e-2
+
+
+@pytest.mark.parametrize("h,w", [(64, 64), (96, 128), (160, 48)])
+def test_encode_against_oracle(enc_vae, h, w):
+    """vae-encode on synthetic weights: the latent's mean against the oracle's encode of the
+    same picture (one and several pixel tiles a stage; a picture taller than wide)."""
+    px = vo.synth_picture(ENC_SEED + h, h, w)
+    say("encode", h, "x", w)
+    got = X.vae_encode(enc_vae, px, h, w)
+    want = vo.encode(vo.SynthVae(ENC_SEED), px)
+    e = xo.rel_l2(got, want)
+    say("encode %d x %d: latent rel-L2 %.2e, |z| %.3f" % (h, w, e, float(np.sqrt((want * want).mean()))))
+    assert got.shape == (64, h // 16, w // 16) and np.isfinite(got).all() and e < ENC_REL
+
+
+def test_encode_device_entry_matches_host(ctx, enc_vae):
+    """exn_vae_encode_dev on device arrays gives the host entry point's latent bit for bit."""
+    h, w = 64, 96
+    px = vo.synth_picture(5, h, w)
+    want = X.vae_encode(enc_vae, px, h, w)
+    pd = X.DevBuf.of(ctx, px)
+    zd = X.DevBuf(ctx, (64, h // 16, w // 16), np.float32)
+    X.call("exn_vae_encode_dev", enc_vae.h, pd.h, h, w, zd.h)
+    assert np.array_equal(zd.get(), want)
+
+
+def skeleton_names():
+    """The tensors zeroed to make the encoder's blocks identities: every residual block's
+    second convolution, every stride-2 convolution and the attention's projection."""
+    return [n for n, _ in vo.vae_encoder_expected()
+            if ".residual.6." in n or ".resample.1." in n or n.startswith("encoder.middle.1.proj.")]
+
+
+def test_encode_skeleton_wiring(ctx):
+    """With every block an identity (residual blocks their shortcut or nothing, the stride-2
+    convolutions zero, the attention's projection zero) the latent is the first convolution,
+    the AvgDown3D chain over the stages' inputs, the last stage's input doubled and the head:
+    the GPU against the oracle on the same weights, tighter than the full encode."""
+    h, w = 64, 48
+    v = X.upload_vae(seed=ENC_SEED, ctx=ctx)
+    try:
+        wt = vo.SynthVae(ENC_SEED)
+        shapes = dict(vo.vae_encoder_expected())
+        for n in skeleton_names():
+            z = np.zeros(shapes[n], np.float32)
+            wt.cache[n] = z
+            v.set(n, X.F32, z, shapes[n])
+        px = vo.synth_picture(41, h, w)
+        got = X.vae_encode(v, px, h, w)
+        want = vo.encode(wt, px)
+        e = xo.rel_l2(got, want)
+        say("skeleton encode rel-L2 %.2e" % e)
+        assert e < 5e-3
+    finally:
+        v.destroy()
+
+
+def test_encode_rejects(ctx, enc_vae):
+    """A picture whose sides are not multiples of 16; a decoder loaded without the encoder's
+    tensors (EXN_ESTATE naming the first missing one)."""
+    with pytest.raises(X.ExnError) as e:
+        X.vae_encode(enc_vae, np.zeros((40, 64, 4), np.float32), 40, 64)
+    assert e.value.code == X.EINVAL
+    v = X.Vae(ctx)
+    try:
+        with pytest.raises(X.ExnError) as e:
+            X.vae_encode(v, np.zeros((32, 32, 4), np.float32), 32, 32)
+        assert e.value.code == X.ESTATE and "encoder.conv1.weight" in str(e.value)
+    finally:
+        v.destroy()

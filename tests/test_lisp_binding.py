@@ -3,7 +3,7 @@ against the C ABI, without
 SBCL (neither this image nor the GPU host has it): every define-alien-routine names a function
 that include/exn_hip.h declares, with its arity and, argument by argument, a Lisp alien type
 that passes the C type (int, 64-bit integers, double, pointers, C strings); and the backend trio
-keeps the reference's lambda lists (src/cuda-dit.lisp:52,137,99; src/cuda-vae.lisp:15,94,28;
+keeps the reference's lambda lists (src/cuda-dit.lisp:52,137,99; src/cuda-vae.lisp:15,94,138,28;
 src/cuda-vision.lisp:15,34,103; src/encoder.lisp:41,55)."""
 import os
 import re
@@ -107,6 +107,7 @@ def test_the_trio_keeps_the_reference_lambda_lists():
     assert defs["dit-release"] == ["d"]
     assert defs["upload-vae"] == ["path", "&key", ["device", "0"]]
     assert defs["vae-decode"] == ["v", "latent", "h", "w"]
+    assert defs["vae-encode"] == ["v", "px", "h", "w"]   # src/cuda-vae.lisp:138
     assert defs["vae-release"] == ["v"]
     assert defs["load-vision"] == ["path", "&key", ["device", "1"]]
     assert defs["vision-encode"] == ["v", "px", "h", "w"]

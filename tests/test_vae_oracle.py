@@ -1,8 +1,10 @@
-"""Pins oracle/exn_vae_oracle.py (the VAE decoder's CPU restatement): decode
-against the reference's own inspect/ref_vae.py (vectors in
+"""Pins oracle/exn_vae_oracle.py (the VAE decoder's and encoder's CPU restatement):
+decode against the reference's own inspect/ref_vae.py (vectors in
 tests/golden/ref_vae_tiny.npz, written by make_ref_vae_vectors.py from the same
 synthetic weights), and the pieces against float64 brute force, closed forms and
-src/cuda/vae.cu's index formulas."""
+src/cuda/vae.cu's index formulas; the encoder's stride-2 convolution by brute
+force, its AvgDown3D against x_avgdown_add's index formula, its stage wiring by a
+closed form on identity blocks."""
 import os
 
 import numpy as np
@@ -143,3 +145,147 @@ def test_decode_flops_counts_every_product(monkeypatch, golden, wt):
     n = h * w
     assert count["f"] + 2 * 2 * n * n * 1152 == vo.decode_flops(h, w)
     assert vo.decode_flops(64, 64) == pytest.approx(17.03e12, rel=1e-3)
+
+
+
+# --- the encoder ----------------------------------------------------------------------
+
+def test_encoder_schema_follows_the_stages():
+    """src/weights.lisp:100-134: conv1 on RGBA, two residual blocks a stage with a shortcut
+    where the width changes, a stride-2 convolution (no frame axis) on the four downsampling
+    stages, the middle, the head to 2 x 64 channels and conv1 (1 x 1)."""
+    names = dict(vo.vae_encoder_expected())
+    assert len(names) == 98
+    assert names["encoder.conv1.weight"] == (96, 4, 1, 3, 3)
+    shortcuts = sorted(n for n in names if n.endswith("shortcut.weight"))
+    assert shortcuts == ["encoder.downsamples.%d.downsamples.0.shortcut.weight" % s for s in (1, 2, 3)]
+    assert [s for s in range(5) if "encoder.downsamples.%d.downsamples.2.resample.1.weight" % s in names] == [0, 1, 2, 3]
+    assert names["encoder.downsamples.3.downsamples.2.resample.1.weight"] == (768, 768, 3, 3)
+    assert names["encoder.middle.1.to_qkv.weight"] == (2304, 768, 1, 1)
+    assert names["encoder.head.2.weight"] == (128, 768, 1, 3, 3)
+    assert names["conv1.weight"] == (128, 128, 1, 1, 1)
+    assert not set(names) & set(dict(vo.vae_expected()))   # no name shared with the decoder
+
+
+def test_conv3s2_against_direct_sum():
+    """The stride-2 convolution against a float64 sum over every output pixel and tap, the
+    input padded with zeros below and to the right only (x_conv3s2's bounds: rows 2y .. 2y + 2
+    and columns 2x .. 2x + 2 of the input, off it zero)."""
+    rng = np.random.default_rng(7)
+    h2, w2, c, o = 6, 10, 5, 3
+    x = rng.standard_normal((h2, w2, c))
+    w = rng.standard_normal((o, c, 3, 3))
+    b = rng.standard_normal(o)
+    got = vo.conv3s2(x, w, b)
+    want = np.zeros((h2 // 2, w2 // 2, o))
+    for y in range(h2 // 2):
+        for xx in range(w2 // 2):
+            for ky in range(3):
+                for kx in range(3):
+                    sy, sx = 2 * y + ky, 2 * xx + kx
+                    if sy < h2 and sx < w2:
+                        want[y, xx] += w[:, :, ky, kx] @ x[sy, sx]
+            want[y, xx] += b
+    assert np.abs(got - want).max() < 1e-4
+    # a symmetric padding (rows 2y - 1 .. 2y + 1) gives another answer
+    xs = np.pad(x, ((1, 1), (1, 1), (0, 0)))
+    sym = sum(xs[ky:ky + h2:2, kx:kx + w2:2] @ w[:, :, ky, kx].T for ky in range(3) for kx in range(3)) + b
+    assert np.abs(sym - want).max() > 0.1
+
+
+def avgdown_index_formula(x, cout, ft, swap_rc=False, pad_last=False, chan_mod=False):
+    """src/cuda/vae.cu's x_avgdown_add as a loop: output channel o of pixel (Y, X) sums x at
+    channel j / (4 ft), row 2Y + (j / 2) % 2, column 2X + j % 2 for the j = o g .. o g + g - 1
+    whose frame (j / 4) % ft is the last, over g = cin ft 4 / cout.  The flags plant mistakes:
+    the block's row and column bits exchanged, the real frame first, the channel as j % cin."""
+    h, w, cin = x.shape
+    g = cin * ft * 4 // cout
+    out = np.zeros((h // 2, w // 2, cout))
+    for yy in range(h // 2):
+        for xx in range(w // 2):
+            for o in range(cout):
+                s = 0.0
+                for k in range(g):
+                    j = o * g + k
+                    if (j >> 2) % ft != (0 if pad_last else ft - 1):
+                        continue
+                    r, c = (j >> 1) & 1, j & 1
+                    if swap_rc:
+                        r, c = c, r
+                    s += x[2 * yy + r, 2 * xx + c, j % cin if chan_mod else j // (4 * ft)]
+                out[yy, xx, o] = s / g
+    return out
+
+
+# (cin, cout, ft, the planted mistakes the case tells apart)
+AVGDOWN_CASES = [(8, 8, 1, ("chan_mod",)), (6, 12, 2, ("pad_last",)), (4, 8, 1, ("swap_rc", "chan_mod")),
+                 (4, 16, 2, ("swap_rc", "pad_last")), (12, 12, 2, ("chan_mod",)), (8, 4, 1, ("chan_mod",))]
+
+
+@pytest.mark.parametrize("cin,cout,ft,mistakes", AVGDOWN_CASES)
+def test_avgdown_view_against_index_formula(cin, cout, ft, mistakes):
+    """The view-and-mean form of AvgDown3D (the oracle) against x_avgdown_add's index formula,
+    and the formula with each planted mistake the case's geometry can show failing it."""
+    rng = np.random.default_rng(cin * 10 + cout + ft)
+    x = rng.standard_normal((6, 4, cin)).astype(np.float32)
+    got = vo.avgdown(x, cout, ft)
+    want = avgdown_index_formula(x.astype(np.float64), cout, ft)
+    assert np.abs(got - want).max() < 1e-6
+    for m in mistakes:
+        assert np.abs(avgdown_index_formula(x.astype(np.float64), cout, ft, **{m: True}) - got).max() > 1e-3, m
+
+
+def test_encode_identity_blocks_closed_form():
+    """The stage wiring: with every residual block's second convolution, every stride-2
+    convolution and the attention's projection zero, a block returns its input (or its
+    shortcut) and the encoder is the first convolution, then per downsampling stage the mean
+    of each 2 x 2 block of the stage's input (with temporal downsampling only the odd output
+    channels, o // 2's mean: the padding frame comes first), the last stage's input doubled,
+    and the head -- computed here by hand from those rules."""
+    wt = vo.SynthVae(3)
+    for n, shape in vo.vae_encoder_expected():
+        if ".residual.6." in n or ".resample.1." in n or n.startswith("encoder.middle.1.proj."):
+            wt.cache[n] = np.zeros(shape, np.float32)
+    px = vo.synth_picture(9, 32, 48)
+    got = vo.encode(wt, px)
+    x = vo.conv(px, wt("encoder.conv1.weight"), wt("encoder.conv1.bias"), 3).astype(np.float64)
+    for s, (i, o, down, tdown) in enumerate(vo.ENC_STAGES):
+        if not down:
+            x = 2 * x
+            continue
+        h, w = x.shape[0] // 2, x.shape[1] // 2
+        m = x.reshape(h, 2, w, 2, i).mean(axis=(1, 3))
+        if tdown:
+            y = np.zeros((h, w, o))
+            y[..., 1::2] = m   # odd channel o: channel o // 2 of the stage's input
+            x = y
+        else:
+            x = m
+    x = x.astype(np.float32)
+    x = vo.silu(vo.rms(x, wt("encoder.head.0.gamma")))
+    x = vo.conv(x, wt("encoder.head.2.weight"), wt("encoder.head.2.bias"), 3)
+    x = vo.conv(x, wt("conv1.weight"), wt("conv1.bias"), 1)
+    want = x[..., :64].transpose(2, 0, 1)
+    assert got.shape == (64, 2, 3)
+    assert np.abs(got - want).max() < 1e-4 * max(1.0, np.abs(want).max())
+
+
+def test_encode_flops_counts_every_product(monkeypatch):
+    """encode_flops against the products encode takes (every convolution as it runs, the
+    stride-2 ones at their output size, the attention's two added)."""
+    count = {"f": 0}
+    real_conv, real_s2 = vo.conv, vo.conv3s2
+
+    def counting(x, w, b, k):
+        count["f"] += 2 * x.shape[0] * x.shape[1] * w.shape[0] * w.shape[1] * k * k
+        return real_conv(x, w, b, k)
+
+    def counting_s2(x, w, b):
+        count["f"] += 2 * (x.shape[0] // 2) * (x.shape[1] // 2) * w.shape[0] * w.shape[1] * 9
+        return real_s2(x, w, b)
+
+    monkeypatch.setattr(vo, "conv", counting)
+    monkeypatch.setattr(vo, "conv3s2", counting_s2)
+    vo.encode(vo.SynthVae(4), vo.synth_picture(2, 32, 32))
+    n = 2 * 2
+    assert count["f"] + 2 * 2 * n * n * 768 == vo.encode_flops(32, 32)
