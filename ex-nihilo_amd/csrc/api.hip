@@ -2111,7 +2111,7 @@ static const float* vae_vec(const exn_vae* v, const std::string& name) {
 }
 
 // a width whose output channels one convolution tile holds: the norm can ride in its store
-static bool vae_one_tile(int c) { return c == 144 || c == 288; }
+static bool vae_one_tile(int c) { return c == 96 || c == 144 || c == 192 || c == 288; }
 
 // OUT = conv(silu(norm(conv(silu(norm(X)))))) + (X, or its 1 x 1 shortcut): src/cuda-vae.lisp's
 // resblock, inspect/ref_vae.py:59-65.  OUT fp32, or bf16 when OUT_BF16 (a product's input next);
@@ -2317,33 +2317,49 @@ static int vae_encode(exn_vae* v, const float* rgba, int h, int w, float* latent
   TRY(vae_buf(v, "part", (size_t)kVaePartCap * 4, (void**)&v->part));
   v->part_cap = kVaePartCap;
   int hh = h, ww = w;
-  // encoder.conv1: RGBA neighbourhoods (t1, 64 bf16 a pixel) x the weights' (tap, channel) rows
+  // the residual.0 gamma of block j of stage si (the norm its input takes)
+  auto g0_of = [&](int si, int j) {
+    char q[96];
+    snprintf(q, sizeof q, "encoder.downsamples.%d.downsamples.%d.residual.0.gamma", si, j);
+    return vae_vec(v, q);
+  };
+  // encoder.conv1: RGBA neighbourhoods (u, 64 bf16 a pixel) x the weights' (tap, channel) rows;
+  // at a one-tile width it leaves the first block's normed input in t1 too
+  const uint16_t* a_rs = nullptr;
   {
     const VT* wt = vae_t(v, "encoder.conv1.weight");
     const VT* b = vae_t(v, "encoder.conv1.bias");
     if (!wt || !b || wt->kp != 64) FAIL(EXN_ESTATE, "encoder: encoder.conv1 not loaded");
-    HIPCHK(vae_rgba_taps(s, h, w, rgba, t1));
-    const VaeEpi ep{nullptr, nullptr, 0, 0, nullptr, v->part, v->part_cap, nullptr, nullptr};
-    HIPCHK(vae_conv(s, 1, 0, VAE_F32, t1, (const uint16_t*)wt->p, (const float*)b->p, ep, A, h, w, 64, (int)wt->o, 64));
+    HIPCHK(vae_rgba_taps(s, h, w, rgba, u));
+    const bool one = vae_one_tile((int)wt->o) && g0_of(0, 0);
+    const VaeEpi ep{nullptr, nullptr, 0, 0, nullptr, v->part, v->part_cap, one ? g0_of(0, 0) : nullptr,
+                    one ? t1 : nullptr};
+    HIPCHK(vae_conv(s, 1, 0, VAE_F32, u, (const uint16_t*)wt->p, (const float*)b->p, ep, A, h, w, 64, (int)wt->o, 64));
+    a_rs = one ? t1 : nullptr;
   }
   char p[96];
   for (int si = 0; si < 5; ++si) {
     const VStage& st = kVaeEncStages[si];
-    // A: the stage's input, kept for AvgDown3D (or the add) at the stage's end
+    // A: the stage's input, kept for AvgDown3D (or the add) at the stage's end.  At one-tile
+    // widths the first block's second convolution leaves the second block's normed input in t1.
     snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.0", si);
-    TRY(vae_resblock(v, p, A, nullptr, nullptr, B, false, st.in, st.out, hh, ww, t1, t2, u, t3));
+    bool made = false;
+    TRY(vae_resblock(v, p, A, nullptr, a_rs, B, false, st.in, st.out, hh, ww, t1, t2, u, t3, g0_of(si, 1), t1,
+                     &made));
+    const uint16_t* b_rs = made ? t1 : nullptr;
+    a_rs = nullptr;
     snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.1", si);
     if (st.up) {
-      // the second block in bf16 for the stride-2 convolution, into B at half size, then
+      // the second block in bf16 for the stride-2 convolution, into C at half size, then
       // AvgDown3D of A added
-      TRY(vae_resblock(v, p, B, nullptr, nullptr, u, true, st.out, st.out, hh, ww, t1, t2, u, t3));
+      TRY(vae_resblock(v, p, B, nullptr, b_rs, u, true, st.out, st.out, hh, ww, t1, t2, u, t3));
       snprintf(p, sizeof p, "encoder.downsamples.%d.downsamples.2.resample.1", si);
       TRY(vae_conv_named(v, p, 2, VAE_F32, u, nullptr, C, hh / 2, ww / 2));
       HIPCHK(vae_avgdown_add(s, st.in, st.out, st.tup ? 2 : 1, hh, ww, A, C));
       hh /= 2;
       ww /= 2;
     } else {
-      TRY(vae_resblock(v, p, B, nullptr, nullptr, C, false, st.out, st.out, hh, ww, t1, t2, u, t3));
+      TRY(vae_resblock(v, p, B, nullptr, b_rs, C, false, st.out, st.out, hh, ww, t1, t2, u, t3));
       HIPCHK(vae_add(s, (int64_t)hh * ww * st.out, A, C));
     }
     std::swap(A, C);

@@ -12,6 +12,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t int32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -251,8 +252,8 @@ struct VaeEpi {
   float* part;
   int64_t part_cap;
   // when gamma is given (a convolution whose one channel tile holds every output channel: cout
-  // 144 or 288): yr = silu(rms(output) x gamma) in bf16 too, the next block's or the head's
-  // normed input; VAE_RMS writes yr only
+  // 96, 144, 192 or 288): yr = silu(rms(output) x gamma) in bf16 too, the next block's or the
+  // head's normed input; VAE_RMS writes yr only
   const float* gamma;
   uint16_t* yr;
 };

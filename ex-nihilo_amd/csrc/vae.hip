@@ -295,33 +295,34 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
       }
     }
     if constexpr (GAM) {
-      static_assert(T::WNC == 144, "the norm's layout: rows of 144 a wave");
-      // each staged row's sum of squares: lanes 2r and 2r + 1 take its two halves of 72, then
-      // swap; at BN 288 the row's other 144 channels are the partner wave's (same pixels)
+      static_assert(T::WNC == 144 || T::WNC == 96, "the norm's layout: rows of 144 or 96 a wave");
+      // each staged row's sum of squares: lanes 2r and 2r + 1 take its two halves, then swap; at
+      // BN 288 and 192 the row's other channels are the partner wave's (same pixels)
+      constexpr int HALF4 = T::WNC / 8;   // 4-channel chunks in half a row
       const int rr = lane >> 1, hh = lane & 1;
       float ss = 0.f;
 #pragma unroll 3
-      for (int c = 0; c < 18; ++c) {
-        const f32x4 t = *(const f32x4*)(stg + rr * 148 + 72 * hh + 4 * c);
+      for (int c = 0; c < HALF4; ++c) {
+        const f32x4 t = *(const f32x4*)(stg + rr * T::LS + (T::WNC / 2) * hh + 4 * c);
         ss += (t[0] * t[0] + t[1] * t[1]) + (t[2] * t[2] + t[3] * t[3]);
       }
       ss += dpp_f<0xB1>(ss);   // quad_perm [1, 0, 3, 2]: lane ^ 1
       if constexpr (T::NWN == 2) {
-        if (hh == 0) stg[rr * 148 + 144] = ss;
+        if (hh == 0) stg[rr * T::LS + T::WNC] = ss;
         __syncthreads();
         const int partner = wn ? wave - T::NWM : wave + T::NWM;
-        ss += ((const float*)smem + partner * (32 * 148))[rr * 148 + 144];
+        ss += ((const float*)smem + partner * (32 * T::LS))[rr * T::LS + T::WNC];
       }
       const float inv = sqrtf((float)cout) / fmaxf(sqrtf(ss), 1e-12f);
-      if (hh == 0) stg[rr * 148 + 145] = inv;
+      if (hh == 0) stg[rr * T::LS + T::WNC + 1] = inv;
       asm volatile("" ::: "memory");
 #pragma unroll 2
-      for (int q = 0; q < 18; ++q) {
-        const int k = q * 64 + lane, row = k / 36, c4 = k - row * 36;
-        const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + 144 * wn + 4 * c4;
+      for (int q = 0; q < T::NCH; ++q) {
+        const int k = q * 64 + lane, row = k / T::RC, c4 = k - row * T::RC;
+        const int m = m0 + T::WM * wm + 32 * half + row, n = n0 + T::WNC * wn + 4 * c4;
         if (m >= P) continue;
-        const f32x4 o = *(const f32x4*)(stg + row * 148 + 4 * c4), g = *(const f32x4*)(ep.gamma + n);
-        const float iv = stg[row * 148 + 145];
+        const f32x4 o = *(const f32x4*)(stg + row * T::LS + 4 * c4), g = *(const f32x4*)(ep.gamma + n);
+        const float iv = stg[row * T::LS + T::WNC + 1];
         float e[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) e[j] = silu_bf16out(o[j] * iv * g[j]);
@@ -385,11 +386,15 @@ static hipError_t conv_bn(hipStream_t s, int taps, int up, int out, const uint16
   // tiles) splits its K over up to 4 workgroups a tile, each at least 16 k-steps, into fp32
   // partials; k_part_sum adds them in order with bias and res
   if (ep.gamma) {   // the output's norm too: one channel tile (cout == BN), never split
+    if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    if (taps == 9 && !up && out == VAE_RMS) return launch_conv<BN, 9, 0, VAE_RMS, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
     if constexpr (DEC) {
-      if (taps == 9 && !up && out == VAE_F32) return launch_conv<BN, 9, 0, VAE_F32, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
-      if (taps == 9 && !up && out == VAE_RMS) return launch_conv<BN, 9, 0, VAE_RMS, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
       if (taps == 9 && up == 1 && out == VAE_DUPUP)
         return launch_conv<BN, 9, 1, VAE_DUPUP, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
+    } else {
+      // the encoder's first convolution (a 1 x 1 product over RGBA neighbourhoods) with the
+      // first block's normed input
+      if (taps == 1 && !up && out == VAE_F32) return launch_conv<BN, 1, 0, VAE_F32, 1>(s, x, wt, bias, ep, y, h, w, c, cout, kp);
     }
     return hipErrorInvalidValue;
   }
@@ -427,7 +432,8 @@ hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x,
       (up == 1 && (h % 2 || w % 2)) || (up == 2 && taps != 9) || ((uintptr_t)x & 15) || ((uintptr_t)wt & 15) || ((uintptr_t)y & 15) ||
       (!y && !(out == VAE_DUPUP && (ep.y2 || ep.yr)) && out != VAE_RMS) ||
       ((uintptr_t)bias & 15) || ((uintptr_t)ep.res & 15) || ((uintptr_t)ep.y2 & 7) || ((uintptr_t)ep.part & 15) ||
-      (ep.gamma && (!ep.yr || ((uintptr_t)ep.yr & 7) || ((uintptr_t)ep.gamma & 15) || (cout != 144 && cout != 288))) ||
+      (ep.gamma && (!ep.yr || ((uintptr_t)ep.yr & 7) || ((uintptr_t)ep.gamma & 15) ||
+                    (cout != 144 && cout != 288 && cout != 96 && cout != 192))) ||
       (!ep.gamma && out == VAE_RMS) ||
       in_px * c * 2 >= ((int64_t)1 << 31) || (int64_t)cout * kp * 2 >= ((int64_t)1 << 31) ||
       (int64_t)h * w * cout >= ((int64_t)1 << 31) ||
@@ -603,11 +609,47 @@ __global__ void k_avgdown_add(int cin, int cout, int ft, int H, int W, const flo
   y[i] += acc / (float)g;
 }
 
+// the encoder's two cases, 4 output channels a thread: g = 4 with ft 1 (cout = cin: each
+// channel's 2 x 2 mean, 16-byte loads) or ft 2 (cout = 2 cin: odd channel o takes channel
+// o / 2's mean, even ones nothing; 8-byte loads)
+template <int FT>
+__global__ void k_avgdown_add4(int cin, int H, int W, const float* __restrict__ x, float* __restrict__ y) {
+  const int cout = cin * FT, c4n = cout / 4, ow = W / 2;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)(H / 2) * ow * c4n) return;
+  const int o = 4 * (int)(i % c4n);
+  const int64_t p = i / c4n;
+  const int yy = (int)(p / ow), xx = (int)(p % ow);
+  const float* r0 = x + ((int64_t)(2 * yy) * W + 2 * xx) * cin;
+  const float* r1 = r0 + (int64_t)W * cin;
+  f32x4 add;
+  if constexpr (FT == 1) {
+    const f32x4 a = *(const f32x4*)(r0 + o), b = *(const f32x4*)(r0 + cin + o);
+    const f32x4 c = *(const f32x4*)(r1 + o), d = *(const f32x4*)(r1 + cin + o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) add[e] = (((a[e] + b[e]) + c[e]) + d[e]) / 4.f;
+  } else {
+    const int c0 = o / 2;
+    const f32x2 a = *(const f32x2*)(r0 + c0), b = *(const f32x2*)(r0 + cin + c0);
+    const f32x2 c = *(const f32x2*)(r1 + c0), d = *(const f32x2*)(r1 + cin + c0);
+    add = f32x4{0.f, (((a[0] + b[0]) + c[0]) + d[0]) / 4.f, 0.f, (((a[1] + b[1]) + c[1]) + d[1]) / 4.f};
+  }
+  f32x4* yo = (f32x4*)(y + p * cout + o);
+  *yo += add;
+}
+
 hipError_t vae_avgdown_add(hipStream_t s, int cin, int cout, int ft, int h, int w, const float* x, float* y) {
   if (cin <= 0 || cout <= 0 || ft < 1 || (int64_t)cin * ft * 4 % cout || h % 2 || w % 2) return hipErrorInvalidValue;
   const int64_t n = (int64_t)(h / 2) * (w / 2) * cout;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_avgdown_add, dim3(grid_of(n, 256)), dim3(256), 0, s, cin, cout, ft, h, w, x, y);
+  const bool al = ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 && cin % 4 == 0;
+  if (al && ft == 1 && cout == cin) {
+    hipLaunchKernelGGL(k_avgdown_add4<1>, dim3(grid_of(n / 4, 256)), dim3(256), 0, s, cin, h, w, x, y);
+  } else if (al && ft == 2 && cout == 2 * cin) {
+    hipLaunchKernelGGL(k_avgdown_add4<2>, dim3(grid_of(n / 4, 256)), dim3(256), 0, s, cin, h, w, x, y);
+  } else {
+    hipLaunchKernelGGL(k_avgdown_add, dim3(grid_of(n, 256)), dim3(256), 0, s, cin, cout, ft, h, w, x, y);
+  }
   return hipGetLastError();
 }
 
