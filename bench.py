@@ -620,7 +620,9 @@ def main():
         print(json.dumps({"metric": "prompt encoder ms (36 blocks of Qwen3-VL-8B's text model), 1 GPU",
                           "value": rec["prompt_256"]["ms"], "unit": "ms/prompt", "n_gpus": 1, "steps": a.steps,
                           "warmup": a.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
-                          "config": {"workload": "encoder-states-256-tokens", "weights": "Q8_0 synthetic",
+                          "config": {"workload": "encoder-states-256-tokens",
+                                     "weights": "Q8_0 synthetic; the products stream each matrix's resident bf16 "
+                                                "expansion (exn_enc_resident, the default)",
                                      "seed": SEED}, "records": rec}), flush=True)
         return
     if a.vae_encode_only:

@@ -2953,6 +2953,7 @@ struct exn_enc {
   std::map<std::string, Buf> bufs;
   float* one_gate = nullptr;  // +inf a column: the gated residual's tanh(gate) is exactly 1
   std::map<int, int32_t*> maps;  // device row maps by slot * 4 + copy
+  bool bf16 = true;           // the matrices run from resident bf16 expansions (exn_enc_resident)
 };
 
 static int enc_buf(exn_enc* e, const char* key, size_t bytes, void** out, bool zero = false) {
@@ -3108,6 +3109,7 @@ int exn_enc_set(exn_enc* e, const char* name, int kind, const void* data, int64_
   if (kind != EXN_Q8_0) FAIL(EXN_EINVAL, "encoder set %s: kind %d (the encoder's matrices are Q8_0)", name, kind);
   exn_w* w = nullptr;
   TRY(enc_matrix(e, L, slot, &w));
+  w->wx_ok = false;   // the expansion, if kept, is remade before the next use
   const int copies = (slot == E_K || slot == E_V) ? kEncGroup : 1;
   for (int rep = 0; rep < copies; ++rep) {
     int32_t* map = nullptr;
@@ -3153,6 +3155,7 @@ int exn_enc_synth(exn_enc* e, uint64_t seed, int64_t vocab) {
       }
       exn_w* w = nullptr;
       TRY(enc_matrix(e, L, slot, &w));
+      w->wx_ok = false;
       const int copies = (slot == E_K || slot == E_V) ? kEncGroup : 1;
       for (int rep = 0; rep < copies; ++rep) {
         int32_t* map = nullptr;
@@ -3175,12 +3178,25 @@ int exn_enc_check(exn_enc* e) {
   return EXN_OK;
 }
 
+// the layers' matrices multiplied from resident bf16 expansions (1, the default, 16 GB beside
+// the 8.4 GB of Q8_0) or from Q8_0 alone, dequantised in the products (0)
+int exn_enc_resident(exn_enc* e, int bf16) {
+  if (!e) FAIL(EXN_EINVAL, "null encoder");
+  TRY(use(e->ctx));
+  e->bf16 = bf16 != 0;
+  for (auto& L : e->L)
+    for (exn_w* m : {L.qkv, L.out, L.gate_up, L.down})
+      if (m) TRY(w_resident(m, e->bf16));
+  HIPCHK(hipStreamSynchronize(e->ctx->stream));
+  return EXN_OK;
+}
+
 int exn_enc_memory(exn_enc* e, int64_t* weights, int64_t* scratch_bytes) {
   if (!e) FAIL(EXN_EINVAL, "null encoder");
   int64_t w = e->vocab * EXN_W * (e->ef ? 4 : 1) + (e->ed ? e->vocab * EXN_W / 16 : 0), s = 0;
   for (auto& L : e->L)
     for (exn_w* m : {L.qkv, L.out, L.gate_up, L.down})
-      if (m) w += m->rows * m->cols * 17 / 16;
+      if (m) w += m->rows * m->cols * 17 / 16 + (m->wx ? m->rows * m->cols * 2 : 0);
   for (auto& kv : e->bufs) s += (int64_t)kv.second.bytes;
   if (weights) *weights = w;
   if (scratch_bytes) *scratch_bytes = s;
@@ -3212,6 +3228,9 @@ int exn_enc_rope_table(const int32_t* pos, int n, double base, float* cs) {
 static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, int pic0, int m, const float* merged,
                       const float* deep, float* out) {
   hipStream_t s = e->ctx->stream;
+  if (e->bf16)   // expansions made (or remade after a set) once, then kept
+    for (auto& L : e->L)
+      for (exn_w* w : {L.qkv, L.out, L.gate_up, L.down}) TRY(w_resident(w, true));
   const int64_t lcap = ((int64_t)n + 63) / 64 * 64;
   float* x;
   uint16_t *y, *att, *ff, *q, *kc, *vt, *qkv;

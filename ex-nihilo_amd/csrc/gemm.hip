@@ -572,11 +572,14 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     bn = in / sz;
   }
   const int64_t m0 = (int64_t)bm * 256, n0 = (int64_t)bn * 256;
-  // split K (EPI_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1 (Q8: in pairs, K % 128
-  // == 0, so that the main loop runs whole pairs of steps and no third copy of the step is live)
+  // split K (EPI_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1, in pairs where the
+  // step count is even (Q8 needs them, K % 128 == 0: the main loop runs whole pairs of steps and
+  // no third copy of the step is live; the bf16 weights cut the same way, so that both give the
+  // same partial sums)
   const int KTT = (int)(K / 64), SK = gridDim.z, zk = blockIdx.z;
-  const int kt0 = Q8 ? 2 * (int)((int64_t)(KTT / 2) * zk / SK) : (int)((int64_t)KTT * zk / SK);
-  const int kt1 = Q8 ? 2 * (int)((int64_t)(KTT / 2) * (zk + 1) / SK) : (int)((int64_t)KTT * (zk + 1) / SK);
+  const bool pairs = Q8 || KTT % 2 == 0;
+  const int kt0 = pairs ? 2 * (int)((int64_t)(KTT / 2) * zk / SK) : (int)((int64_t)KTT * zk / SK);
+  const int kt1 = pairs ? 2 * (int)((int64_t)(KTT / 2) * (zk + 1) / SK) : (int)((int64_t)KTT * (zk + 1) / SK);
   // DMA: round i of wave w moves rows (i*8 + w)*8 .. +7 of a tile, lane l row +l/8, LDS chunk l%8
   // (global chunk (l%8) ^ swizzle); the k-step is the scalar offset
   const uint16_t* xbase = X + m0 * lda;

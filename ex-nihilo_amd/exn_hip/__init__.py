@@ -141,6 +141,7 @@ SIGNATURES = {
     "exn_enc_release": (c_int, [vp]),
     "exn_enc_destroy": (c_int, [vp]),
     "exn_enc_memory": (c_int, [vp, POINTER(c_int64), POINTER(c_int64)]),
+    "exn_enc_resident": (c_int, [vp, c_int]),
 }
 
 
@@ -644,6 +645,10 @@ class Encoder:
 
     def check(self):
         call("exn_enc_check", self.h)
+
+    def resident(self, on: bool):
+        """The products from resident bf16 expansions (the default) or from Q8_0 alone."""
+        call("exn_enc_resident", self.h, 1 if on else 0)
 
     def memory(self):
         w, s = c_int64(), c_int64()

@@ -123,6 +123,38 @@ def test_the_distance_is_the_rounding(enc2, owt2):
     assert abs(g - m) < 0.25 * g and gm < g
 
 
+@pytest.mark.parametrize("n", [40, 300, 1100])   # the split-K path (5 and 2 splits) and whole tiles
+def test_resident_expansion_equals_q8_products(enc2, n):
+    """The products from the resident bf16 expansions (the default) and from Q8_0 dequantised
+    in the pipeline take the same operand values in the same order: the states bit for bit."""
+    ids = eo.synth_ids(SEED + 6 + n, n, VOCAB)
+    a = X.encoder_states(enc2, ids)
+    enc2.resident(False)
+    try:
+        b = X.encoder_states(enc2, ids)
+    finally:
+        enc2.resident(True)
+    assert np.array_equal(a, b)
+
+
+def test_a_set_matrix_remakes_its_expansion(ctx, owt2):
+    """A matrix set after its expansion was made is multiplied from the new values."""
+    e = X.load_encoder(seed=SEED, layers=2, vocab=VOCAB, ctx=ctx)
+    try:
+        ids = eo.synth_ids(SEED + 7, 40, VOCAB)
+        before = X.encoder_states(e, ids)
+        other = eo.SynthEncoder(SEED + 100, eo.EShape(layers=2))
+        name = "blk.1.ffn_down.weight"
+        shape = dict(eo.enc_expected(eo.EShape(layers=2)))[name]
+        e.set(name, X.Q8_0, xo.q8_0_to_blocks(*other.q8(name)), shape[1], shape[0])
+        after = X.encoder_states(e, ids)
+        e.resident(False)
+        q8 = X.encoder_states(e, ids)
+        assert np.array_equal(after, q8) and not np.array_equal(after, before)
+    finally:
+        e.destroy()
+
+
 def test_encoder_errors(ctx, enc2):
     e = X.Encoder(ctx, 2)
     try:
