@@ -1901,6 +1901,7 @@ struct exn_vae {
   std::map<std::string, Buf> bufs;
   float* part = nullptr;   // split-K partial sums of the small convolutions (a decode's scratch)
   int64_t part_cap = 0;
+  int wide_only = 0;       // exn_vae_tiles: 256-pixel tiles only
 };
 
 // split-K scratch: a split convolution has S x tiles <= 256 workgroups of 256 pixels x at most
@@ -2072,6 +2073,12 @@ int exn_vae_check(exn_vae* v) {
   return EXN_OK;
 }
 
+int exn_vae_tiles(exn_vae* v, int small) {
+  if (!v) FAIL(EXN_EINVAL, "null decoder");
+  v->wide_only = small ? 0 : 1;
+  return EXN_OK;
+}
+
 int exn_vae_check_encoder(exn_vae* v) {
   if (!v) FAIL(EXN_EINVAL, "null decoder");
   for (size_t i = v->n_dec; i < v->expect.size(); ++i)
@@ -2099,7 +2106,7 @@ static int vae_conv_named(exn_vae* v, const std::string& name, int up, int out, 
   const VT* wt = vae_t(v, name + ".weight");
   const VT* b = vae_t(v, name + ".bias");
   if (!wt || !b) FAIL(EXN_ESTATE, "decoder: missing %s", name.c_str());
-  const VaeEpi ep{res, keep, kcin, ft, y2, v->part, v->part_cap, gamma, yr};
+  const VaeEpi ep{res, keep, kcin, ft, y2, v->part, v->part_cap, gamma, yr, v->wide_only};
   HIPCHK(vae_conv(v->ctx->stream, wt->taps, up, out, x, (const uint16_t*)wt->p, (const float*)b->p, ep, y, h, w,
                   wt->ci, (int)wt->o, wt->kp));
   return EXN_OK;
@@ -2333,7 +2340,7 @@ static int vae_encode(exn_vae* v, const float* rgba, int h, int w, float* latent
     HIPCHK(vae_rgba_taps(s, h, w, rgba, u));
     const bool one = vae_one_tile((int)wt->o) && g0_of(0, 0);
     const VaeEpi ep{nullptr, nullptr, 0, 0, nullptr, v->part, v->part_cap, one ? g0_of(0, 0) : nullptr,
-                    one ? t1 : nullptr};
+                    one ? t1 : nullptr, v->wide_only};
     HIPCHK(vae_conv(s, 1, 0, VAE_F32, u, (const uint16_t*)wt->p, (const float*)b->p, ep, A, h, w, 64, (int)wt->o, 64));
     a_rs = one ? t1 : nullptr;
   }

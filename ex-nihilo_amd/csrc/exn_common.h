@@ -256,6 +256,9 @@ struct VaeEpi {
   // head's normed input; VAE_RMS writes yr only
   const float* gamma;
   uint16_t* yr;
+  // 1: 256-pixel tiles always (the 128-pixel ones of large pictures off; the same sums, a test's
+  // switch)
+  int wide_only;
 };
 hipError_t vae_conv(hipStream_t s, int taps, int up, int out, const uint16_t* x, const uint16_t* wt,
                     const float* bias, const VaeEpi& ep, void* y, int h, int w, int c, int cout, int kp);

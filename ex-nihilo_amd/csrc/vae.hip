@@ -35,27 +35,30 @@ __device__ __forceinline__ void conv_dma(const void* base, uint32_t extent, lds_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
 }
 
-#define VBM 256
 #define VOFF_NONE 0x80000000u   // past any extent: the load reads zeros
-#define VEPI_LDS (8 * 32 * 148 * 4)   // the epilogue's staging: 8 waves x 32 pixels x 148 floats
 
-// Tiles of 256 pixels x BN output channels, BN = 144 (3 LDS stages), 288 (2 stages; the
-// widths that 288 divides), 96 (3 stages) and 192 (2 stages; the encoder's 96 .. 768) or 16
-// (3 stages; the head's 4 channels): 8 waves of WM pixels x WNC channels (WNC = 144 where 144
-// divides BN, 96 where 96 does, else BN), each a (WM/16) x (WNC/16) grid of
+// Tiles of TM = 32 NW pixels x BN output channels, NW waves: BN = 144 (3 LDS stages), 288 (2
+// stages; the widths that 288 divides), 96 (3 stages) and 192 (2 stages; the encoder's 96 ..
+// 768) or 16 (3 stages; the head's 4 channels), NW 8 (256 pixels); or NW 4 (128 pixels, 2
+// stages, under 80 KB of LDS so that two workgroups share a CU and one's epilogue runs under the
+// other's products) at BN 96 and 144 on large pictures.  Waves of WM pixels x WNC channels (WNC
+// = 144 where 144 divides BN, 96 where 96 does, else BN), each a (WM/16) x (WNC/16) grid of
 // v_mfma_f32_16x16x32_bf16 -- 0.61 fragment reads an MFMA at BN 144, 0.36 at BN 288, 0.42 at
 // BN 192.
-template <int BN>
+template <int BN, int NW = 8>
 struct ConvTile {
   static constexpr int WNC = BN % 144 == 0 ? 144 : BN % 96 == 0 ? 96 : BN, NJ = WNC / 16;
-  static constexpr int NWN = BN / WNC, NWM = 8 / NWN, WM = VBM / NWM, MI = WM / 16;
+  static constexpr int NWN = BN / WNC, NWM = NW / NWN, TM = 32 * NW, WM = TM / NWM, MI = WM / 16;
   static constexpr int LS = WNC + 4, RC = WNC / 4, NCH = 32 * RC / 64;   // staging: row floats, chunks a row, a lane
-  static constexpr int STAGE = VBM * 128 + BN * 128;   // A rows | B rows, 64 bf16 of K each
-  static constexpr int NST = BN <= 144 ? 3 : 2;
-  static constexpr int BFULL = BN * 8 / 512;           // full B DMA rounds a step
-  static constexpr int BREM = (BN * 8 - 512 * BFULL) / 8;   // lanes a wave in the partial round
+  static constexpr int ABYTES = TM * 128;              // the A rows of a stage
+  static constexpr int STAGE = ABYTES + BN * 128;      // A rows | B rows, 64 bf16 of K each
+  static constexpr int NST = NW == 4 ? 2 : BN <= 144 ? 3 : 2;
+  static constexpr int BFULL = BN * 8 / (64 * NW);     // full B DMA rounds a step
+  static constexpr int BREM = (BN * 8 - 64 * NW * BFULL) / NW;   // lanes a wave in the partial round
   static constexpr int NDMA = 4 + BFULL + (BREM > 0);  // DMA instructions a wave a step
-  static constexpr int LDS = NST * STAGE > VEPI_LDS ? NST * STAGE : VEPI_LDS;
+  static constexpr int EPI = NW * 32 * 148 * 4;        // the epilogue's staging: 32 pixels x 148 floats a wave
+  static constexpr int LDS = NST * STAGE > EPI ? NST * STAGE : EPI;
+  static_assert(BREM % 8 == 0 && BREM <= 64 && (NW == 8 || LDS <= 80 * 1024), "tile layout");
 };
 
 // UP: 0 a 'same' convolution of an H x W picture; 1 the same of the picture nearest-upsampled
@@ -66,17 +69,17 @@ struct ConvTile {
 // VAE_PART the fp32 sums of k-steps kt0 .. kt1-1 only (workgroup z of a split K) into z's slice,
 // VAE_RMS none (yr only).  GAM: the tile holds every output channel, and ep.yr gets
 // silu(rms(output) x ep.gamma) in bf16.
-template <int BN, int TAPS, int UP, int OUT, int GAM>
-__global__ void __launch_bounds__(512)
+template <int BN, int TAPS, int UP, int OUT, int GAM, int NW = 8>
+__global__ void __launch_bounds__(NW * 64, NW == 4 ? 2 : 1)   // 4 waves: two workgroups a CU, 256 registers a lane
 k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const float* __restrict__ bias,
        VaeEpi ep, void* __restrict__ Y, int H, int W, int C, int cout, int Kp) {
-  typedef ConvTile<BN> T;
+  typedef ConvTile<BN, NW> T;
   extern __shared__ __align__(1024) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % T::NWM, wn = wave / T::NWM;
   const int P = H * W;
-  const int m0 = blockIdx.x * VBM, n0 = blockIdx.y * BN;
+  const int m0 = blockIdx.x * T::TM, n0 = blockIdx.y * BN;
   // split K (VAE_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1
   const int KTT = Kp / 64, S = gridDim.z, z = blockIdx.z;
   const int kt0 = (int)((int64_t)KTT * z / S), kt1 = (int)((int64_t)KTT * (z + 1) / S);
@@ -90,7 +93,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   int py[4], px[4], cc[4], tp[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = (8 * i + wave) * 8 + (lane >> 3);
+    const int r = (NW * i + wave) * 8 + (lane >> 3);
     const int m = m0 + r;
     const int y = m / W;
     py[i] = m < P ? y : -0x40000000;   // a row past the picture: every neighbour off it
@@ -105,9 +108,9 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
   uint32_t boff[T::BFULL + 1];
 #pragma unroll
   for (int rd = 0; rd <= T::BFULL; ++rd) {
-    int row = 64 * rd + 8 * wave + (lane >> 3);
+    int row = 8 * NW * rd + 8 * wave + (lane >> 3);
     if constexpr (T::BREM > 0)
-      if (rd == T::BFULL) row = 64 * T::BFULL + (T::BREM / 8) * wave + ((lane >> 3) % (T::BREM / 8));
+      if (rd == T::BFULL) row = 8 * NW * T::BFULL + (T::BREM / 8) * wave + ((lane >> 3) % (T::BREM / 8));
     boff[rd] = (uint32_t)((row * Kp + 8 * ((lane & 7) ^ ((row >> 1) & 7))) * 2);
   }
   // issue the next k-step's tiles into stage s (the A chunks' positions then move on)
@@ -130,7 +133,7 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
         sx >>= 1;
       }
       const uint32_t off = ok ? (uint32_t)(((sy * Ws + sx) * C + cc[i]) * 2) : VOFF_NONE;
-      conv_dma(X, xext, (lds_void*)(st + (8 * i + wave) * 1024), off, 0);
+      conv_dma(X, xext, (lds_void*)(st + (NW * i + wave) * 1024), off, 0);
       cc[i] += 64;
       if (cc[i] >= C) {   // C >= 64: one wrap at most
         cc[i] -= C;
@@ -139,15 +142,16 @@ k_conv(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Wt, const fl
     }
 #pragma unroll
     for (int rd = 0; rd < T::BFULL; ++rd)
-      conv_dma(wbase, wext, (lds_void*)(st + 32768 + rd * 8192 + wave * 1024), boff[rd], t * 128);
+      conv_dma(wbase, wext, (lds_void*)(st + T::ABYTES + rd * (1024 * NW) + wave * 1024), boff[rd], t * 128);
     if constexpr (T::BREM > 0)
       if (lane < T::BREM)
-        conv_dma(wbase, wext, (lds_void*)(st + 32768 + T::BFULL * 8192 + wave * T::BREM * 16), boff[T::BFULL], t * 128);
+        conv_dma(wbase, wext, (lds_void*)(st + T::ABYTES + T::BFULL * (1024 * NW) + wave * T::BREM * 16), boff[T::BFULL],
+                 t * 128);
   };
 
   // fragments: lane holds row lo of a 16-row block, K 8 q4 .. of a slice of 32
   const int lo = lane & 15, q4 = lane >> 4, fs = (lo >> 1) & 7;
-  const int a_rd = (T::WM * wm + lo) * 128, b_rd = 32768 + (T::WNC * wn + lo) * 128;
+  const int a_rd = (T::WM * wm + lo) * 128, b_rd = T::ABYTES + (T::WNC * wn + lo) * 128;
   f32x4 acc[T::MI][T::NJ];
 #pragma unroll
   for (int i = 0; i < T::MI; ++i)
@@ -360,20 +364,33 @@ static hipError_t part_sum(hipStream_t s, int S, int64_t n, int cout, const floa
   return hipGetLastError();
 }
 
-template <int BN, int TAPS, int UP, int OUT, int GAM = 0>
-static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const VaeEpi& ep,
-                              void* y, int h, int w, int c, int cout, int kp, int split = 1) {
-  auto kern = k_conv<BN, TAPS, UP, OUT, GAM>;
-  constexpr int lds = ConvTile<BN>::LDS;
+template <int BN, int TAPS, int UP, int OUT, int GAM = 0, int NW = 8>
+static hipError_t launch_conv1(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const VaeEpi& ep,
+                               void* y, int h, int w, int c, int cout, int kp, int split = 1) {
+  auto kern = k_conv<BN, TAPS, UP, OUT, GAM, NW>;
+  typedef ConvTile<BN, NW> T;
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  dim3 grid(grid_of((int64_t)h * w, VBM), grid_of(cout, BN), split);
-  hipLaunchKernelGGL(kern, grid, dim3(512), lds, s, x, wt, bias, ep, y, h, w, c, cout, kp);
+  dim3 grid(grid_of((int64_t)h * w, T::TM), grid_of(cout, BN), split);
+  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), T::LDS, s, x, wt, bias, ep, y, h, w, c, cout, kp);
   return hipGetLastError();
+}
+
+// 128-pixel tiles of 4 waves (two workgroups a CU) for the 96- and 144-wide convolutions of
+// pictures of 2^18 pixels or more, where the output, residual and normed copy move as many bytes
+// as the products take time; 256-pixel tiles otherwise
+template <int BN, int TAPS, int UP, int OUT, int GAM = 0>
+static hipError_t launch_conv(hipStream_t s, const uint16_t* x, const uint16_t* wt, const float* bias, const VaeEpi& ep,
+                              void* y, int h, int w, int c, int cout, int kp, int split = 1) {
+  if constexpr (BN == 96 || BN == 144) {
+    if (split == 1 && !ep.wide_only && (int64_t)h * w >= (1 << 18))
+      return launch_conv1<BN, TAPS, UP, OUT, GAM, 4>(s, x, wt, bias, ep, y, h, w, c, cout, kp, 1);
+  }
+  return launch_conv1<BN, TAPS, UP, OUT, GAM, 8>(s, x, wt, bias, ep, y, h, w, c, cout, kp, split);
 }
 
 // the decoder's tiles (BN 144, 288: waves of 144 channels) take the norm in the store, the
@@ -398,7 +415,7 @@ static hipError_t conv_bn(hipStream_t s, int taps, int up, int out, const uint16
     }
     return hipErrorInvalidValue;
   }
-  const int64_t P = (int64_t)h * w, tiles = grid_of(P, VBM) * (int64_t)grid_of(cout, BN);
+  const int64_t P = (int64_t)h * w, tiles = grid_of(P, ConvTile<BN>::TM) * (int64_t)grid_of(cout, BN);
   int64_t split = 256 / tiles < 4 ? 256 / tiles : 4;
   if (kp / 64 / 16 < split) split = kp / 64 / 16;
   if (taps == 9 && !up && (out == VAE_F32 || out == VAE_BF16) && !ep.y2 && ep.part && tiles < 192 && split >= 2 &&

@@ -105,6 +105,7 @@ SIGNATURES = {
     "exn_vae_synth": (c_int, [vp, c_uint64]),
     "exn_vae_check": (c_int, [vp]),
     "exn_vae_check_encoder": (c_int, [vp]),
+    "exn_vae_tiles": (c_int, [vp, c_int]),
     "exn_vae_encode": (c_int, [vp, vp, c_int, c_int, vp]),
     "exn_vae_encode_dev": (c_int, [vp, vp, c_int, c_int, vp]),
     "exn_vae_decode": (c_int, [vp, vp, c_int, c_int, vp]),

@@ -287,6 +287,10 @@ int exn_vae_release(exn_vae* v);
 int exn_vae_destroy(exn_vae* v);
 /* bytes of device memory the decoder holds: weights, scratch */
 int exn_vae_memory(exn_vae* v, int64_t* weights, int64_t* scratch);
+/* test hook, no reference counterpart: SMALL 1 (the default) lets the 96- and 144-wide
+ * convolutions of pictures of 2^18 pixels or more run on 128-pixel tiles (two workgroups a CU),
+ * 0 keeps every convolution on 256-pixel tiles; each output value is the same sum either way */
+int exn_vae_tiles(exn_vae* v, int small);
 /* the decoder's and encoder's kernels one at a time (src/cuda/vae.cu's x_conv3 with the 1 x 1
  * products, x_up2 folded in (UP 1), x_conv3s2 (UP 2), bias and residual fused; v_rms with
  * x_silu; x_dupup_add; x_avgdown_add).  X: bf16 pixel rows (H x W x C; H/2 x W/2 x C with UP 1;

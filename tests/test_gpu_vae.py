@@ -73,6 +73,10 @@ CONV_CASES = [  # (h, w, c, cout, taps, up, out, with res)
     (13, 7, 96, 192, 1, 0, 0, True),
     (21, 19, 64, 96, 1, 0, 0, False),   # encoder.conv1: a 1 x 1 product over RGBA neighbourhoods
     (6, 6, 768, 128, 9, 0, 1, False),   # the encoder's head: 128 of a 144-wide tile
+    # 2^18 pixels: the 128-pixel tiles of 4 waves, two workgroups a CU
+    (512, 512, 144, 144, 9, 0, 0, True),
+    (512, 512, 96, 96, 9, 0, 1, False),
+    (512, 512, 64, 96, 1, 0, 0, False),
 ]
 
 
@@ -315,3 +319,22 @@ def test_encode_rejects(ctx, enc_vae):
         assert e.value.code == X.ESTATE and "encoder.conv1.weight" in str(e.value)
     finally:
         v.destroy()
+
+
+def test_large_pictures_tiles_agree(ctx, enc_vae):
+    """Pictures of 2^18 pixels or more run their 96- and 144-wide convolutions on 128-pixel tiles
+    (the norm in the store, the residual, the first convolution's 1 x 1 included): a 32 x 32
+    latent's decode and a 512 x 512 picture's encode equal, bit for bit, the same on 256-pixel
+    tiles only."""
+    z = vo.synth_latent(33, 32, 32)
+    px = vo.synth_picture(34, 512, 512)
+    a, _, _ = X.vae_decode(enc_vae, z, 32, 32)
+    la = X.vae_encode(enc_vae, px, 512, 512)
+    X.call("exn_vae_tiles", enc_vae.h, 0)
+    try:
+        b, _, _ = X.vae_decode(enc_vae, z, 32, 32)
+        lb = X.vae_encode(enc_vae, px, 512, 512)
+    finally:
+        X.call("exn_vae_tiles", enc_vae.h, 1)
+    assert np.isfinite(a).all() and np.isfinite(la).all()
+    assert np.array_equal(a, b) and np.array_equal(la, lb)
