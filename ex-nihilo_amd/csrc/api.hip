@@ -3249,12 +3249,13 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
   TRY(enc_buf(e, "kc", (size_t)lcap * EXN_W * 2, (void**)&kc, true));
   TRY(enc_buf(e, "vt", (size_t)lcap * EXN_W * 2, (void**)&vt, true));
   // a prompt of at most 1024 tokens is about one row of 256-row tiles: its products split K
-  // over the chip (the DiT's prompt-row path), the partial sums then added in order
+  // over the chip (the DiT's prompt-row path), the partial sums then added in order; a longer
+  // one splits the products of fewer tiles than 192 (out and down, 16 column tiles)
   float* part = nullptr;
   const bool split = n <= 1024;
-  if (split) TRY(enc_buf(e, "part", (size_t)kSplitCap * 4, (void**)&part));
+  TRY(enc_buf(e, "part", (size_t)kSplitCap * 4, (void**)&part));
   auto mm = [&](const exn_w* w, const uint16_t* xin, int64_t lda, Epi epi, const EpiArgs& a) -> hipError_t {
-    if (split) {
+    if (split || ((int64_t)n + 255) / 256 * ((w->rows + 255) / 256) < 192) {
       const hipError_t r = gemm_split_rows(s, xin, lda, wop(w), n, w->rows, w->cols, epi, a, part, kSplitCap);
       if (r != hipErrorNotSupported) return r;
     }
