@@ -518,29 +518,58 @@ static hipError_t gemm_any(hipStream_t s, const exn_w* w, const uint16_t* x, int
   return hipErrorInvalidValue;
 }
 
-// split-K scratch of a block product's prompt rows: S x rows x N floats with S x tiles <= 256
-// workgroups of 256 x 256, so 256^3 floats hold any of them
-static const int64_t kSplitCap = (int64_t)256 * 256 * 256;
+// split-K scratch of a block product's prompt rows (S x rows x N floats with S x tiles <= 256
+// workgroups of 256 x 256: 256^3 floats hold any of them) and of image rows past whole waves
+// (2048 rows x 4096 columns, split 2 ways)
+static const int64_t kSplitCap = (int64_t)2 * 256 * 256 * 256;
 
-// a block product over a pass's n rows: its first nh rows (the prompt's, in a pass that has
-// them: about one row of tiles) with K split over the chip, the rest as whole tiles, so that
-// the 4096 image rows of a 1024^2 picture fill whole waves.  A full-K tile's rows are the same
-// bits however the rows are tiled, so a cached pass's image rows match the uncached pass's.
-static hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, int64_t nh,
-                           Epi epi, const EpiArgs& ea, float* part) {
-  if (nh > 0 && nh < n && nh <= 1024 && part && w->kind != EXN_F32) {
-    const hipError_t r = gemm_split_rows(s, x, lda, wop(w), nh, w->rows, w->cols, epi, ea, part, kSplitCap);
-    if (r == hipSuccess) {
-      EpiArgs eb = ea;   // the remaining rows: every row pointer nh rows on
-      eb.n0 = ea.n0 + (int)nh;
-      if (epi == EPI_GATE_ADD) eb.resid = ea.resid + nh * ea.ldy;
-      else if (epi == EPI_F32) eb.y = (float*)ea.y + nh * ea.ldy;
-      else eb.y = (uint16_t*)ea.y + nh * ea.ldy;
-      return gemm_any(s, w, x + nh * lda, lda, n - nh, epi, eb);
-    }
+// EA with every row pointer K rows on (the gated residual's or the output's)
+static EpiArgs rows_on(const EpiArgs& ea, Epi epi, int64_t k) {
+  EpiArgs eb = ea;
+  eb.n0 = ea.n0 + (int)k;
+  if (epi == EPI_GATE_ADD) eb.resid = ea.resid + k * ea.ldy;
+  else if (epi == EPI_F32) eb.y = (float*)ea.y + k * ea.ldy;
+  else eb.y = (uint16_t*)ea.y + k * ea.ldy;
+  return eb;
+}
+
+// a block product's image rows as whole tiles; where they would leave a last wave of
+// workgroups at most half full (6144 rows through to_out and down: 384 tiles, 1.5 waves), the
+// rows of the whole waves as tiles and the rest with K split over the chip (2048 rows: 128
+// tiles, 2 ways), the rest then taking half a wave's time instead of a whole one
+static hipError_t rows_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, Epi epi,
+                          const EpiArgs& ea, float* part) {
+  const int64_t ct = (w->rows + 255) / 256, tiles = (n + 255) / 256 * ct, full = tiles / 256 * 256;
+  if (part && w->kind != EXN_F32 && (epi == EPI_GATE_ADD || epi == EPI_SWIGLU) && full > 0 && tiles > full &&
+      tiles - full <= 128 && full % ct == 0) {
+    const int64_t n1 = full / ct * 256;   // the whole waves' rows
+    hipError_t r = gemm_any(s, w, x, lda, n1, epi, ea);
+    if (r != hipSuccess) return r;
+    const EpiArgs eb = rows_on(ea, epi, n1);
+    r = gemm_split_rows(s, x + n1 * lda, lda, wop(w), n - n1, w->rows, w->cols, epi, eb, part, kSplitCap);
     if (r != hipErrorNotSupported) return r;
+    return gemm_any(s, w, x + n1 * lda, lda, n - n1, epi, eb);
   }
   return gemm_any(s, w, x, lda, n, epi, ea);
+}
+
+// a block product over a pass's n rows: its first nh rows (the prompt's, in a pass that has
+// them) apart -- with K split over the chip when they are about one row of tiles -- and the
+// image rows after them by rows_mm, so that the 4096 image rows of a 1024^2 picture fill whole
+// waves.  The image rows are tiled alike in every pass whatever comes before them, and a tile's
+// rows are the same bits however the rows are tiled, so a cached pass's image rows match the
+// uncached pass's.
+static hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, int64_t nh,
+                           Epi epi, const EpiArgs& ea, float* part) {
+  if (nh > 0 && nh < n) {
+    hipError_t r = hipErrorNotSupported;
+    if (nh <= 1024 && part && w->kind != EXN_F32)
+      r = gemm_split_rows(s, x, lda, wop(w), nh, w->rows, w->cols, epi, ea, part, kSplitCap);
+    if (r == hipErrorNotSupported) r = gemm_any(s, w, x, lda, nh, epi, ea);
+    if (r != hipSuccess) return r;
+    return rows_mm(s, w, x + nh * lda, lda, n - nh, epi, rows_on(ea, epi, nh), part);
+  }
+  return rows_mm(s, w, x, lda, n, epi, ea, part);
 }
 
 // exn_mm's checks and its products that need no scratch: an F32 matrix in fp32 (d41_mm_f32), n <= 4
@@ -1464,9 +1493,9 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   TRY(dit_buf(d, "x", (size_t)(l * EXN_W) * 4, (void**)&x));
   TRY(dit_buf(d, "y", (size_t)(l * EXN_W) * 2, (void**)&y));
   TRY(dit_buf(d, "qkv", (size_t)(l * 3 * EXN_W) * 2, (void**)&qkv));
-  float* part = nullptr;   // split-K partials of the prompt rows of an uncached pass
+  float* part = nullptr;   // split-K partials: an uncached pass's prompt rows, image rows past whole waves
   const int64_t nh = std::max<int64_t>(0, std::min<int64_t>(p - n0, n));
-  if (nh > 0 && nh < n) TRY(dit_buf(d, "split", (size_t)kSplitCap * 4, (void**)&part));
+  TRY(dit_buf(d, "split", (size_t)kSplitCap * 4, (void**)&part));
   TRY(dit_buf(d, "q", (size_t)(l * EXN_W) * 2, (void**)&q));
   TRY(dit_buf(d, "att", (size_t)(l * EXN_W) * 2, (void**)&att));
   TRY(dit_buf(d, "ff", (size_t)(l * EXN_F) * 2, (void**)&ff));
