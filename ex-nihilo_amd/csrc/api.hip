@@ -554,8 +554,9 @@ static hipError_t rows_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int6
 }
 
 // a block product over a pass's n rows: its first nh rows (the prompt's, in a pass that has
-// them) apart -- with K split over the chip when they are about one row of tiles -- and the
-// image rows after them by rows_mm, so that the 4096 image rows of a 1024^2 picture fill whole
+// them) apart -- with K split over the chip when they are about one row of tiles, else by
+// rows_mm (an edit's 4608 prompt rows through to_out and down: 288 tiles) -- and the image
+// rows after them by rows_mm, so that the 4096 image rows of a 1024^2 picture fill whole
 // waves.  The image rows are tiled alike in every pass whatever comes before them, and a tile's
 // rows are the same bits however the rows are tiled, so a cached pass's image rows match the
 // uncached pass's.
@@ -565,7 +566,7 @@ static hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int
     hipError_t r = hipErrorNotSupported;
     if (nh <= 1024 && part && w->kind != EXN_F32)
       r = gemm_split_rows(s, x, lda, wop(w), nh, w->rows, w->cols, epi, ea, part, kSplitCap);
-    if (r == hipErrorNotSupported) r = gemm_any(s, w, x, lda, nh, epi, ea);
+    if (r == hipErrorNotSupported) r = rows_mm(s, w, x, lda, nh, epi, ea, part);
     if (r != hipSuccess) return r;
     return rows_mm(s, w, x + nh * lda, lda, n - nh, epi, rows_on(ea, epi, nh), part);
   }
