@@ -2419,8 +2419,10 @@ extern "C" {
 int exn_vae_encode_dev(exn_vae* v, const float* rgba, int h, int w, float* latent) {
   if (!v) FAIL(EXN_EINVAL, "null decoder");
   TRY(use(v->ctx));
-  if (!rgba || !latent || h <= 0 || w <= 0 || h % 16 || w % 16 || (int64_t)h * w > ((int64_t)1 << 24))
-    FAIL(EXN_EINVAL, "vae encode: picture %d x %d (multiples of 16, at most 2^24 pixels)", h, w);
+  // the first stage's bf16 picture (96 channels) is one buffer of under 2^31 bytes
+  if (!rgba || !latent || h <= 0 || w <= 0 || h % 16 || w % 16 ||
+      (int64_t)h * w * kVaeEncStages[0].out * 2 >= ((int64_t)1 << 31))
+    FAIL(EXN_EINVAL, "vae encode: picture %d x %d (multiples of 16, under 2^31 / 192 pixels)", h, w);
   TRY(exn_vae_check_encoder(v));
   return vae_encode(v, rgba, h, w, latent);
 }
@@ -2428,8 +2430,10 @@ int exn_vae_encode_dev(exn_vae* v, const float* rgba, int h, int w, float* laten
 int exn_vae_encode(exn_vae* v, const float* rgba, int h, int w, float* latent) {
   if (!v) FAIL(EXN_EINVAL, "null decoder");
   TRY(use(v->ctx));
-  if (!rgba || !latent || h <= 0 || w <= 0 || h % 16 || w % 16 || (int64_t)h * w > ((int64_t)1 << 24))
-    FAIL(EXN_EINVAL, "vae encode: picture %d x %d (multiples of 16, at most 2^24 pixels)", h, w);
+  // the first stage's bf16 picture (96 channels) is one buffer of under 2^31 bytes
+  if (!rgba || !latent || h <= 0 || w <= 0 || h % 16 || w % 16 ||
+      (int64_t)h * w * kVaeEncStages[0].out * 2 >= ((int64_t)1 << 31))
+    FAIL(EXN_EINVAL, "vae encode: picture %d x %d (multiples of 16, under 2^31 / 192 pixels)", h, w);
   const int64_t npx = (int64_t)h * w * kVaeIn, nz = (int64_t)kVaeZ * (h / 16) * (w / 16);
   float *dp, *dz;
   TRY(vae_buf(v, "h_px", (size_t)npx * 4, (void**)&dp));

@@ -277,7 +277,7 @@ int exn_vae_check_encoder(exn_vae* v);
 int exn_vae_decode(exn_vae* v, const float* latent, int h, int w, float* rgba);
 int exn_vae_decode_dev(exn_vae* v, const float* latent, int h, int w, float* rgba);
 /* vae-encode (src/cuda-vae.lisp:138-190): RGBA (H x W x 4 floats in -1..1, rows of pixels; H
- * and W multiples of 16) -> the latent's mean (64 x H/16 x W/16 floats, channel-major, as
+ * and W multiples of 16, H W < 2^31 / 192) -> the latent's mean (64 x H/16 x W/16 floats, channel-major, as
  * exn_vae_decode takes it: denormalized).  Host arrays; exn_vae_encode_dev takes device
  * arrays, on the context's stream. */
 int exn_vae_encode(exn_vae* v, const float* rgba, int h, int w, float* latent);
