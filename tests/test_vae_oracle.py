@@ -270,6 +270,72 @@ def test_encode_identity_blocks_closed_form():
     assert np.abs(got - want).max() < 1e-4 * max(1.0, np.abs(want).max())
 
 
+def identity_resample(shape):
+    """A stride-2 convolution's weights (o, o, 3, 3) taking each channel's centre tap: output
+    pixel (y, x) = input pixel (2y + 1, 2x + 1)."""
+    w = np.zeros(shape, np.float32)
+    o = shape[0]
+    w[np.arange(o), np.arange(o), 1, 1] = 1
+    return w
+
+
+def centre_tap_by_hand(wt, px, skip_from_blocks=False):
+    """test_encode_identity_blocks_centre_tap_closed_form's latent by the rules alone; with
+    SKIP_FROM_BLOCKS the planted mistake of AvgDown3D taken of the blocks' output instead of the
+    stage's input."""
+    x = vo.conv(px, wt("encoder.conv1.weight"), wt("encoder.conv1.bias"), 3).astype(np.float64)
+    for s, (i, o, down, tdown) in enumerate(vo.ENC_STAGES):
+        keep = x
+        if i != o:   # the first block's shortcut (1 x 1): its second convolution is zero
+            p = "encoder.downsamples.%d.downsamples.0.shortcut" % s
+            w = wt(p + ".weight").reshape(o, i).astype(np.float64)
+            x = x @ w.T + wt(p + ".bias")
+        if not down:
+            x = x + keep
+            continue
+        src, c = (x, o) if skip_from_blocks else (keep, i)
+        h, w2 = src.shape[0] // 2, src.shape[1] // 2
+        g = c * (2 if tdown else 1) * 4 // o
+        m = src.reshape(h, 2, w2, 2, c).mean(axis=(1, 3))
+        if tdown:   # odd output channel o: input channel o // 2 (g = 4); g = 8: the mean of two
+            full = np.zeros((h, w2, c, 2))
+            full[..., 1] = m
+            skip = full.reshape(h, w2, o, g // 4).mean(-1) if g > 4 else None
+            if g == 4:
+                skip = np.zeros((h, w2, o))
+                skip[..., 1::2] = m
+        else:
+            skip = m if c == o else m.reshape(h, w2, o, c // o).mean(-1)
+        x = x[1::2, 1::2] + skip
+    x = x.astype(np.float32)
+    x = vo.silu(vo.rms(x, wt("encoder.head.0.gamma")))
+    x = vo.conv(x, wt("encoder.head.2.weight"), wt("encoder.head.2.bias"), 3)
+    x = vo.conv(x, wt("conv1.weight"), wt("conv1.bias"), 1)
+    return x[..., :64].transpose(2, 0, 1)
+
+
+def test_encode_identity_blocks_centre_tap_closed_form():
+    """The wiring with the stride-2 convolutions live: residual blocks their input or their
+    shortcut (second convolutions zero), each stride-2 convolution the centre tap of its
+    channel, the attention's projection zero.  A downsampling stage's output is then the
+    stage's blocks' output at the odd rows and columns (the resample reads the blocks, at 2y +
+    1) plus AvgDown3D of the stage's input; computed by hand, and the same by hand with the
+    skip taken of the blocks' output instead fails it."""
+    wt = vo.SynthVae(5)
+    shapes = dict(vo.vae_encoder_expected())
+    for n, shape in shapes.items():
+        if ".residual.6." in n or n.startswith("encoder.middle.1.proj.") or (".resample.1." in n and n.endswith(".bias")):
+            wt.cache[n] = np.zeros(shape, np.float32)
+        elif ".resample.1." in n:
+            wt.cache[n] = identity_resample(shape)
+    px = vo.synth_picture(12, 32, 48)
+    got = vo.encode(wt, px)
+    want = centre_tap_by_hand(wt, px)
+    assert np.abs(got - want).max() < 1e-4 * max(1.0, np.abs(want).max())
+    wrong = centre_tap_by_hand(wt, px, skip_from_blocks=True)
+    assert np.abs(got - wrong).max() > 1e-2 * np.abs(want).max()
+
+
 def test_encode_flops_counts_every_product(monkeypatch):
     """encode_flops against the products encode takes (every convolution as it runs, the
     stride-2 ones at their output size, the attention's two added)."""
