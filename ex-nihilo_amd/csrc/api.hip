@@ -1502,9 +1502,9 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   TRY(dit_buf(d, "ff", (size_t)(l * EXN_F) * 2, (void**)&ff));
   TRY(dit_buf(d, "tok", (size_t)((nimg > nref ? nimg : nref) * EXN_LAT) * 4, (void**)&tok));
   TRY(dit_buf(d, "vrows", (size_t)(nimg * EXN_LAT) * 4, (void**)&vrows));
-  // split-K partials of the edge products with few tiles (proj_out's 64 columns): 8 slices
+  // split-K partials of the edge products with few tiles (proj_out's 64 columns): up to 16 slices
   float* epart = nullptr;
-  const int64_t epart_cap = 8 * std::max<int64_t>(nimg, 256) * EXN_LAT;
+  const int64_t epart_cap = 16 * std::max<int64_t>(nimg, 256) * EXN_LAT;
   TRY(dit_buf(d, "epart", (size_t)epart_cap * 4, (void**)&epart));
 
   // the int8 mode (exn_dit_w8a8) takes a Q8_0 matrix's products of at least 16 rows the

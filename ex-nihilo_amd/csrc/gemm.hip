@@ -1041,11 +1041,12 @@ hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs
                     int gelu, float* part, int64_t part_cap) {
   if (K % 32 || M <= 0) return M == 0 ? hipSuccess : hipErrorInvalidValue;
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-  // few tiles over a long K (proj_out: 64 tiles of 64 x 64 over 4096): K split over up to 8
-  // workgroups a tile, at least 8 blocks of 32 each, their sums added in order after
+  // few tiles over a long K (proj_out: 64 tiles of 64 x 64 over 4096): K split over up to 16
+  // workgroups a tile, about 1024 in all (four a CU: one a CU leaves the loads' latency bare),
+  // at least 8 blocks of 32 each, their sums added in order after
   const int64_t tiles = (int64_t)grid.x * grid.y;
-  int64_t S = tiles < 128 ? 256 / tiles : 1;
-  if (S > 8) S = 8;
+  int64_t S = tiles < 128 ? 1024 / tiles : 1;
+  if (S > 16) S = 16;
   if (S > K / 256) S = K / 256;
   if (S >= 2 && part && S * M * N <= part_cap) {
     grid.z = (unsigned)S;
