@@ -2,7 +2,7 @@
 Qwen3-VL-8B's text model, every token's state after its last block before the final
 norm, float32 numpy.
 
-TEST INFRASTRUCTURE ONLY.  Tests use this module as the checker; the product path
+TEST INFRASTRUCTURE ONLY.  Tests use this module for the expected values; the product path
 (libexn-hip.so and the exn_hip host package) never imports it.
 
 The reference runs this model through illatio (il::load-model, il::cuda-forward-n,

@@ -1,7 +1,7 @@
 """exn_oracle -- the CPU restatement of ex-nihilo's DiT step, float32 numpy.
 
 TEST INFRASTRUCTURE ONLY.  Tests, the smoke check and the CPU-baseline leg of
-the benchmark use this module as the checker; the product path (libexn-hip.so
+the benchmark use this module for the expected values; the product path (libexn-hip.so
 and the exn_hip host package) never imports it.
 
 It restates, function by function (citations are into the reference tree):

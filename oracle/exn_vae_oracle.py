@@ -1,7 +1,7 @@
 """exn_vae_oracle -- the CPU restatement of ex-nihilo's VAE decoder and encoder, float32 numpy.
 
 TEST INFRASTRUCTURE ONLY.  Tests and the benchmark's checks use this module as
-the checker; the product path (libexn-hip.so and the exn_hip host package)
+the expected values; the product path (libexn-hip.so and the exn_hip host package)
 never imports it.
 
 It restates:

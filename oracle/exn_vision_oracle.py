@@ -1,7 +1,7 @@
 """exn_vision_oracle -- the CPU restatement of Qwen3-VL's vision tower as ex-nihilo
 runs it for editing, float32 numpy.
 
-TEST INFRASTRUCTURE ONLY.  Tests use this module as the checker; the product path
+TEST INFRASTRUCTURE ONLY.  Tests use this module for the expected values; the product path
 (libexn-hip.so and the exn_hip host package) never imports it.
 
 It restates:

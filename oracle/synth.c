@@ -1,6 +1,6 @@
 /* synth.c -- the oracle's C restatement of the byte and integer arithmetic on
  * the DiT path.  TEST INFRASTRUCTURE ONLY: tests, the smoke check and the
- * CPU-baseline leg of the benchmark link it as the checker; the product
+ * CPU-baseline leg of the benchmark link it for the expected values; the product
  * (libexn-hip.so) never does.
  *
  * What it restates:
