@@ -1502,9 +1502,12 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   TRY(dit_buf(d, "ff", (size_t)(l * EXN_F) * 2, (void**)&ff));
   TRY(dit_buf(d, "tok", (size_t)((nimg > nref ? nimg : nref) * EXN_LAT) * 4, (void**)&tok));
   TRY(dit_buf(d, "vrows", (size_t)(nimg * EXN_LAT) * 4, (void**)&vrows));
-  // split-K partials of the edge products with few tiles (proj_out's 64 columns): up to 16 slices
+  // split-K partials of the edge products with few tiles (proj_out's 64 columns, txt_in over few
+  // prompt rows): S slices of M x N with S <= 1024 / tiles of 64 x 64, so S M N <= 1024 x 4096
+  // whatever the shape.  The cap never binds, so a product's split follows its own shape only and
+  // a prompt's rows come out the same over any picture (the kept K/V stay valid).
   float* epart = nullptr;
-  const int64_t epart_cap = 16 * std::max<int64_t>(nimg, 256) * EXN_LAT;
+  const int64_t epart_cap = (int64_t)1024 * 64 * 64;
   TRY(dit_buf(d, "epart", (size_t)epart_cap * 4, (void**)&epart));
 
   // the int8 mode (exn_dit_w8a8) takes a Q8_0 matrix's products of at least 16 rows the

@@ -1041,14 +1041,16 @@ hipError_t gemm_f32(hipStream_t s, const float* x, int64_t ldx, const int8_t* qs
                     int gelu, float* part, int64_t part_cap) {
   if (K % 32 || M <= 0) return M == 0 ? hipSuccess : hipErrorInvalidValue;
   dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-  // few tiles over a long K (proj_out: 64 tiles of 64 x 64 over 4096): K split over up to 16
-  // workgroups a tile, about 1024 in all (four a CU: one a CU leaves the loads' latency bare),
-  // at least 8 blocks of 32 each, their sums added in order after
+  // few tiles over a long K (proj_out: 64 tiles of 64 x 64 over 4096; txt_in over 256 prompt
+  // rows: 256 tiles): K split over up to 16 workgroups a tile, about 1024 in all (four a CU: one
+  // a CU leaves the loads' latency bare), at least 8 blocks of 32 each and no more than PART_CAP
+  // holds, their sums added in order after
   const int64_t tiles = (int64_t)grid.x * grid.y;
-  int64_t S = tiles < 128 ? 1024 / tiles : 1;
+  int64_t S = tiles < 512 ? 1024 / tiles : 1;
   if (S > 16) S = 16;
   if (S > K / 256) S = K / 256;
-  if (S >= 2 && part && S * M * N <= part_cap) {
+  if (part && S > part_cap / (M * N)) S = part_cap / (M * N);
+  if (S >= 2 && part) {
     grid.z = (unsigned)S;
     hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, s, x, ldx, qs, d, wbf16, wf32, M, N, K, part, N, gelu);
     hipLaunchKernelGGL(k_f32_part_sum, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, s, (int)S, M, N, part, y,
