@@ -66,6 +66,7 @@ struct exn_w {
   int64_t rows = 0, cols = 0;
   int8_t* qs = nullptr;
   uint16_t* d = nullptr;
+  uint8_t* qt = nullptr;   // a Q8_0 matrix's tiled copy of qs/d, the block products' operand (cols % 64 == 0)
   uint16_t* wb = nullptr;  // bf16 rows (EXN_BF16 matrices; a dense layer matrix)
   float* wf = nullptr;     // fp32 rows (EXN_F32 matrices)
   uint16_t* wx = nullptr;  // a Q8_0 matrix's resident bf16 expansion, bf16(fp32(d) * q) exactly
@@ -87,9 +88,9 @@ static const uint16_t* wbf(const exn_w* w) {
 // the operand a block product streams: the bf16 rows, else the Q8_0 codes and scales (dequantised
 // in the product); an F32 matrix has neither (its products run in fp32)
 static WOp wop(const exn_w* w) {
-  if (const uint16_t* b = wbf(w)) return WOp{b, nullptr, nullptr};
-  if (w->kind == EXN_Q8_0) return WOp{nullptr, w->qs, w->d};
-  return WOp{nullptr, nullptr, nullptr};
+  if (const uint16_t* b = wbf(w)) return WOp{b, nullptr, nullptr, nullptr};
+  if (w->kind == EXN_Q8_0) return WOp{nullptr, w->qs, w->d, w->qt};
+  return WOp{nullptr, nullptr, nullptr, nullptr};
 }
 
 static int dev_alloc(void** p, size_t bytes) {
@@ -278,6 +279,7 @@ static int w_new(exn_ctx* ctx, int kind, int64_t rows, int64_t cols, exn_w** out
   if (kind == EXN_Q8_0) {
     r = dev_alloc((void**)&w->qs, (size_t)(rows * cols));
     if (r == EXN_OK) r = dev_alloc((void**)&w->d, (size_t)(rows * cols / 32) * 2);
+    if (r == EXN_OK && cols % 64 == 0) r = dev_alloc((void**)&w->qt, (size_t)tile_q8_bytes(rows, cols));
   } else if (kind == EXN_F32) {
     r = dev_alloc((void**)&w->wf, (size_t)(rows * cols) * 4);
   } else {
@@ -286,6 +288,7 @@ static int w_new(exn_ctx* ctx, int kind, int64_t rows, int64_t cols, exn_w** out
   if (r != EXN_OK) {
     dev_free(w->qs);
     dev_free(w->d);
+    dev_free(w->qt);
     dev_free(w->wb);
     dev_free(w->wf);
     delete w;
@@ -304,6 +307,7 @@ int exn_weight_free(exn_w* w) {
   if (!w->view) {
     dev_free(w->qs);
     dev_free(w->d);
+    dev_free(w->qt);
     dev_free(w->wb);
     dev_free(w->wf);
     dev_free(w->wx);
@@ -325,11 +329,20 @@ static int upload_q8_blocks(exn_ctx* ctx, const void* blocks, int64_t rows, int6
   return EXN_OK;
 }
 
+// a Q8_0 matrix's tiled copy (the block products' operand) from its codes and scales, after any
+// write to them (on the context's stream, ahead of any product that reads it)
+static int retile(exn_w* w) {
+  if (w->kind != EXN_Q8_0 || !w->qt) return EXN_OK;
+  HIPCHK(tile_q8(w->ctx->stream, w->qs, w->d, w->rows, w->cols, w->qt));
+  return EXN_OK;
+}
+
 int exn_weight_q8_0(exn_ctx* ctx, const void* blocks, int64_t rows, int64_t cols, exn_w** out) {
   TRY(use(ctx));
   if (!blocks) FAIL(EXN_EINVAL, "null blocks");
   TRY(w_new(ctx, EXN_Q8_0, rows, cols, out));
   int r = upload_q8_blocks(ctx, blocks, rows, cols, nullptr, (*out)->qs, (*out)->d);
+  if (r == EXN_OK) r = retile(*out);
   if (r != EXN_OK) {
     exn_weight_free(*out);
     *out = nullptr;
@@ -389,6 +402,7 @@ int exn_weight_q8_0_synth(exn_ctx* ctx, uint64_t seed, uint64_t tensor, int64_t 
   TRY(use(ctx));
   TRY(w_new(ctx, EXN_Q8_0, rows, cols, out));
   hipError_t e = synth_q8(ctx->stream, gen_key(seed, tensor), rows, cols, cols / 32, nullptr, (*out)->qs, (*out)->d);
+  if (e == hipSuccess && (*out)->qt) e = tile_q8(ctx->stream, (*out)->qs, (*out)->d, rows, cols, (*out)->qt);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
     exn_weight_free(*out);
@@ -492,6 +506,8 @@ int exn_weight_pairs(exn_ctx* ctx, exn_w* w) {
   w->qs = qs;
   w->d = d;
   w->pairs = true;
+  TRY(retile(w));
+  HIPCHK(hipStreamSynchronize(w->ctx->stream));
   if (w->wx) {
     w->wx_ok = false;
     TRY(w_resident(w, true));
@@ -514,7 +530,7 @@ static hipError_t gemm_any(hipStream_t s, const exn_w* w, const uint16_t* x, int
                            const EpiArgs& ea) {
   if (n == 0) return hipSuccess;
   if (const uint16_t* b = wbf(w)) return gemm_wbf16(s, x, lda, b, n, w->rows, w->cols, epi, ea);
-  if (w->kind == EXN_Q8_0) return gemm_q8(s, x, lda, w->qs, w->d, n, w->rows, w->cols, epi, ea);
+  if (w->kind == EXN_Q8_0) return gemm_q8(s, x, lda, wop(w), n, w->rows, w->cols, epi, ea);
   return hipErrorInvalidValue;
 }
 
@@ -1107,7 +1123,8 @@ int exn_dit_memory(exn_dit* d, int64_t* weights, int64_t* scratch) {
   auto wb = [](const exn_w* x) -> int64_t {
     if (!x) return 0;
     const int64_t e = x->rows * x->cols;
-    return (x->qs ? e + e / 16 : 0) + (x->wb ? 2 * e : 0) + (x->wf ? 4 * e : 0) + (x->wx ? 2 * e : 0);
+    return (x->qs ? e + e / 16 : 0) + (x->qt ? tile_q8_bytes(x->rows, x->cols) : 0) + (x->wb ? 2 * e : 0) +
+           (x->wf ? 4 * e : 0) + (x->wx ? 2 * e : 0);
   };
   for (auto x : d->edge) w += wb(x);
   for (auto& l : d->L) w += wb(l.qkv) + wb(l.out) + wb(l.gate_up) + wb(l.down) + 2 * 4 * EXN_HD;
@@ -1241,6 +1258,7 @@ int exn_dit_set(exn_dit* d, const char* name, int kind, const void* data, int64_
   if (kind == EXN_Q8_0) {
     TRY(upload_q8_blocks(ctx, data, rows, cols, map, w->qs + row0 * cols, w->d + row0 * (cols / 32)));
     w->wx_ok = false;
+    TRY(retile(w));
     if (w->dense) {  // the slot's rows into the dense rows too (gate_up's slot is the whole matrix)
       HIPCHK(dequant_q8(ctx->stream, w->qs + row0 * cols, w->d + row0 * (cols / 32), rows * cols, nullptr,
                         w->wb + row0 * cols));
@@ -1274,6 +1292,7 @@ int exn_dit_synth(exn_dit* d, uint64_t seed) {
         TRY(w_new(d->ctx, EXN_Q8_0, ex.d1, ex.d0, &d->edge[i]));
       }
       HIPCHK(synth_q8(s, key, ex.d1, ex.d0, ex.d0 / 32, nullptr, d->edge[i]->qs, d->edge[i]->d));
+      TRY(retile(d->edge[i]));
     }
     d->have_edge[i] = true;
   }
@@ -1293,6 +1312,7 @@ int exn_dit_synth(exn_dit* d, uint64_t seed) {
         TRY(layer_target(d, layer, sl, &w, &row0, &map));
         HIPCHK(synth_q8(s, key, ex.d1, ex.d0, ex.d0 / 32, map, w->qs + row0 * ex.d0, w->d + row0 * (ex.d0 / 32)));
         w->wx_ok = false;
+        TRY(retile(w));
         if (w->dense) {  // every slot of the matrix is made Q8_0 again here
           HIPCHK(hipStreamSynchronize(s));
           dev_free(w->wb);
@@ -3160,6 +3180,7 @@ int exn_enc_set(exn_enc* e, const char* name, int kind, const void* data, int64_
     if (slot != E_OUT && slot != E_DOWN) TRY(enc_map(e, slot, rep, &map));
     TRY(upload_q8_blocks(e->ctx, data, d1, d0, map, w->qs, w->d));
   }
+  TRY(retile(w));
   L.have |= 1u << slot;
   return EXN_OK;
 }
@@ -3206,6 +3227,7 @@ int exn_enc_synth(exn_enc* e, uint64_t seed, int64_t vocab) {
         if (slot != E_OUT && slot != E_DOWN) TRY(enc_map(e, slot, rep, &map));
         HIPCHK(synth_q8(s, key, kEncDims[slot][1], kEncDims[slot][0], kEncDims[slot][0] / 32, map, w->qs, w->d));
       }
+      TRY(retile(w));
       L.have |= 1u << slot;
     }
   }
@@ -3240,7 +3262,8 @@ int exn_enc_memory(exn_enc* e, int64_t* weights, int64_t* scratch_bytes) {
   int64_t w = e->vocab * EXN_W * (e->ef ? 4 : 1) + (e->ed ? e->vocab * EXN_W / 16 : 0), s = 0;
   for (auto& L : e->L)
     for (exn_w* m : {L.qkv, L.out, L.gate_up, L.down})
-      if (m) w += m->rows * m->cols * 17 / 16 + (m->wx ? m->rows * m->cols * 2 : 0);
+      if (m) w += m->rows * m->cols * 17 / 16 + (m->qt ? tile_q8_bytes(m->rows, m->cols) : 0) +
+                  (m->wx ? m->rows * m->cols * 2 : 0);
   for (auto& kv : e->bufs) s += (int64_t)kv.second.bytes;
   if (weights) *weights = w;
   if (scratch_bytes) *scratch_bytes = s;

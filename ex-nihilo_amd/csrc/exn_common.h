@@ -171,17 +171,30 @@ struct EpiArgs {
   int64_t qld;   // EPI_QKV: Q's rows a head (the pass's; 0: M)
 };
 
-// a weight matrix as a block product streams it: bf16 rows WB (N x K), or, when WB is null, Q8_0
-// codes QS (N x K int8) and scales QD (N x K/32 fp16), dequantised inside the product
+// The block products' Q8_0 operand, tiled: for each block of 256 rows (rows past N zero) and each
+// k-step of 64 columns, QT_CHUNK contiguous bytes -- the 256 rows' 64 codes (row r at 64 r, the
+// order the product's LDS stage holds them), then their two fp16 scales (row r at QT_SCALES + 4 r).
+// Chunk (nb, t) is at (nb K/64 + t) QT_CHUNK.  One k-step of a tile is then one contiguous run of
+// 17 KB: its DMA touches whole cache lines, and a wave's scale loads one line.
+#define QT_CHUNK 17408
+#define QT_SCALES 16384
+inline int64_t tile_q8_bytes(int64_t rows, int64_t cols) { return (rows + 255) / 256 * (cols / 64) * QT_CHUNK; }
+// QT from the SoA codes QS (N x K int8) and scales D (N x K/32 fp16); K % 64 == 0
+hipError_t tile_q8(hipStream_t s, const int8_t* qs, const uint16_t* d, int64_t N, int64_t K, uint8_t* qt);
+
+// a weight matrix as a block product streams it: bf16 rows WB (N x K), or, when WB is null, Q8_0:
+// the tiled copy QT (the pipelined product's operand) and the SoA codes QS (N x K int8) and scales
+// QD (N x K/32 fp16) that the other kernels read
 struct WOp {
   const uint16_t* wb;
   const int8_t* qs;
   const uint16_t* qd;
+  const uint8_t* qt;
 };
 
-// Y = X W^T with X bf16 (M x K, lda), W Q8_0 SoA (qs N x K int8, d N x K/32 fp16) or bf16 (N x K)
-hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d,
-                   int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
+// Y = X W^T with X bf16 (M x K, lda) and W Q8_0 (W.qt, or W.qs/W.qd where the pipeline does not fit)
+hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K,
+                   Epi epi, const EpiArgs& ea);
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w,
                       int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
 // rows 0 .. M-1 of a product too short to fill the chip (a pass's prompt rows) with its K split

@@ -516,7 +516,11 @@ __device__ __forceinline__ i32x4 buffer_desc(const void* base, uint32_t extent) 
 // inserts no wait for it, where its model of the DMA counter is more careful than the schedule
 // needs (the kernel's own vmcnt waits cover the value before its use).  The destination stays
 // allocated to the value from the load to its last use; after the loop the kernel holds it
-// live until every load has landed.
+// live until every load has landed.  This is correct only while the register allocator neither
+// reads nor copies that register between the load and the wait that covers it (a value carried
+// round the loop in one register, as here, is not copied; two alternating registers selected by
+// the step's parity were, before the wait, and that form is not used).  The bit-exact Q8_0 tests
+// (the resident expansion against the in-pipeline dequantisation) are what catch a violation.
 __device__ __forceinline__ uint32_t buffer_load_u32_untracked(i32x4 rsrc, uint32_t voff, uint32_t soff) {
   uint32_t v;
   asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rsrc), "s"(soff));
@@ -533,19 +537,19 @@ __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_
 // SIMD.  4 waves of 128 x 128 (one a SIMD, a third less LDS read a FLOP) were slower under the
 // one-barrier schedule and spill their 256 accumulators under this one.
 //
-// Q8: W is Q8_0 (qs int8 N x K, d fp16 N x K/32) and is dequantised inside the pipeline.  The
-// int8 codes go HBM -> LDS by the same DMA path into two 16 KB raw stages (so the LDS holds
-// 2 x 64 KB of bf16 stages + 2 x 16 KB of codes = 160 KB), each thread's fp16 scale by a 2-byte
-// buffer load into a register, and once a k-step the 512 threads turn one raw stage into the
-// bf16 W stage the MFMAs read: thread t takes tile row t/2, Q8_0 block t%2 -- 32 codes, two
-// 16-byte LDS reads -- and writes bf16(fp32(d) q) as four swizzled 16-byte rows: a signed byte
-// conversion and one multiply a value (q d has at most 18 significant bits, exact in fp32),
-// rounded once, so the operand is bit for bit the resident expansion's value.
+// Q8: W is Q8_0 in the tiled layout QT (exn_common.h) and is dequantised inside the pipeline.
+// A k-step of the tile is 17 KB in one run: its 16 KB of int8 codes go HBM -> LDS by the same
+// DMA path into two raw stages (so the LDS holds 2 x 64 KB of bf16 stages + 2 x 16 KB of codes =
+// 160 KB), each thread's two fp16 scales by a 4-byte load into a register (a wave's 64 loads one
+// 128-byte line), and once a k-step the 512 threads turn one raw stage into the bf16 W stage the
+// MFMAs read: thread t takes tile row t/2, Q8_0 block t%2 -- 32 codes, two 16-byte LDS reads --
+// and writes bf16(fp32(d) q) as four swizzled 16-byte rows: a signed byte conversion and one
+// multiply a value (q d has at most 18 significant bits, exact in fp32), rounded once, so the
+// operand is bit for bit the resident expansion's value.
 template <int EPI, int NW, bool Q8>
 __global__ void __launch_bounds__(NW * 64)
 k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB,
-          const int8_t* __restrict__ QS, const uint16_t* __restrict__ QD, int64_t M, int64_t N, int64_t K,
-          EpiArgs ea) {
+          const uint8_t* __restrict__ QT, int64_t M, int64_t N, int64_t K, EpiArgs ea) {
   constexpr bool HEADS = EPI == EPI_QKV;   // a wave's columns one head of 128
   constexpr int WM = HEADS ? 64 : 128, WN = HEADS ? 128 : 512 / NW, MI = WM / 16, NI = WN / 16;
   constexpr int ROUNDS = 256 / (NW * 8);
@@ -596,47 +600,55 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   }
   auto dma_part = [&](int t, int stage, int p) {   // part p < ROUNDS: X round p, else W round p - ROUNDS
     uint8_t* dst = smem + stage * 65536 + (p < ROUNDS ? 0 : 32768) + ((p % ROUNDS) * NW + wave) * 1024;
-    if constexpr (Q8)   // round p's rows are round 0's plus p NW 8 (uniform): one offset register, not ROUNDS
-      tile_dma(xbase, xext, (lds_void*)dst, xoff[0], t * 128 + (int)(p * NW * 8 * lda * 2));
-    else if (p < ROUNDS) tile_dma(xbase, xext, (lds_void*)dst, xoff[p % ROUNDS], t * 128);
+    // Q8: round p's rows are round 0's plus p NW 8 (uniform): one offset register, not ROUNDS.  The
+    // buffer's range check covers the vector offset only, never the scalar one, so the round's
+    // rows move the base (and shrink the extent) rather than ride in the scalar offset: a row past
+    // M is then past the extent and reads as zeros
+    if constexpr (Q8) {
+      const int64_t r0 = (int64_t)p * NW * 8;
+      tile_dma(xbase + r0 * lda, (uint32_t)(max((int64_t)0, M - m0 - r0) * lda * 2), (lds_void*)dst, xoff[0], t * 128);
+    } else if (p < ROUNDS) tile_dma(xbase, xext, (lds_void*)dst, xoff[p % ROUNDS], t * 128);
     else tile_dma(wbase, wext, (lds_void*)dst, woff[p % ROUNDS], t * 128);
   };
-  // Q8: raw round i of wave w moves code rows (i*8 + w)*16 .. +15 (64 bytes a row), lane l row
-  // +l/4, bytes 16 (l%4) ..; the scales of tile row tid/2, both blocks of the k-step in one dword
-  // (rows past N read as zeros) -- a 32-bit value, so that no widening of it is hoisted to the
-  // loop's head, where it would wait for the load before its time
-  const int8_t* qbase = QS + n0 * K;
-  const uint32_t qext = Q8 ? (uint32_t)(max((int64_t)0, N - n0) * K) : 0u;
-
-  const i32x4 drsrc =
-      buffer_desc(QD + n0 * (K / 32), Q8 ? (uint32_t)(max((int64_t)0, N - n0) * (K / 32) * 2) : 0u);
-  const uint32_t roff0 = (uint32_t)((wave * 16 + (lane >> 2)) * K + 16 * (lane & 3));
+  // Q8: the tile's chunks of QT, one a k-step (QT_CHUNK bytes, every offset inside the buffer: rows
+  // past N are zeros in it).  Raw round i of wave w moves 1 KB of codes, rows (i*8 + w)*16 ..
+  // +15, lane l 16 bytes at 16 l of them, into the same place of the raw stage (row r at 64 r).
+  // The scales of tile row tid/2, both blocks of the k-step in one dword -- a 32-bit value, so
+  // that no widening of it is hoisted to the loop's head, where it would wait for the load before
+  // its time
+  const int64_t KT = K / 64;
+  const i32x4 qrsrc = buffer_desc(QT + (int64_t)bn * KT * QT_CHUNK, Q8 ? (uint32_t)(KT * QT_CHUNK) : 0u);
+  const uint32_t roff0 = (uint32_t)(wave * 1024 + lane * 16);
   const int dq_row = tid >> 1, dq_blk = tid & 1;
-  const uint32_t doff = (uint32_t)(dq_row * (K / 32) * 2);
+  const uint32_t doff = (uint32_t)(QT_SCALES + dq_row * 4);
   auto raw_dma = [&](int t, int stage, int i) {
     uint8_t* dst = smem + 131072 + stage * 16384 + (i * NW + wave) * 1024;
-    tile_dma(qbase, qext, (lds_void*)dst, roff0, t * 64 + (int)(i * NW * 16 * K));
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)(QT + (int64_t)bn * KT * QT_CHUNK), 0,
+                                                                 (int)(KT * QT_CHUNK), 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, roff0, t * QT_CHUNK + i * NW * 1024, 0, 0);
   };
-  auto scale_load = [&](int t) -> uint32_t { return buffer_load_u32_untracked(drsrc, doff, (uint32_t)(t * 4)); };
-  // Q8: the thread's 32 codes of raw stage rs into bf16 W stage ws, the block's fp16 scale the
-  // half dq_blk of DPAIR; parts 0 and 5 read 16 codes each, parts 1..4 and 6..9 convert one
-  // 4-code word each and store its 8 bytes of bf16
-  u32x4 dq_q;
+  auto scale_load = [&](int t) -> uint32_t { return buffer_load_u32_untracked(qrsrc, doff, (uint32_t)(t * QT_CHUNK)); };
+  // Q8: the thread's 32 codes of raw stage rs into bf16 W stage ws: two 16-code reads (dq_read,
+  // halves 0 and 1), the block's fp16 scale from the half dq_blk of DPAIR (dq_scale), then eight
+  // conversions of one 4-code word each, each storing its 8 bytes of bf16 (dq_convert)
+  u32x4 dq_q[2];
   float dq_d = 0.f;
-  auto dequant = [&](int part, int rs, int ws, uint32_t dpair) {
-    const uint8_t* src = smem + 131072 + rs * 16384 + tid * 32;
-    if (part == 0 || part == 5) {
-      dq_q = *(const u32x4*)(src + (part == 5 ? 16 : 0));
-      if (part == 0) dq_d = f16_to_f32((dpair >> (16 * dq_blk)) & 0xFFFFu);
-      return;
-    }
-    const int j = part < 5 ? part - 1 : part - 2;
-    const uint32_t u = dq_q[j & 3];
+  auto dq_read = [&](int h, int rs) { dq_q[h] = *(const u32x4*)(smem + 131072 + rs * 16384 + tid * 32 + 16 * h); };
+  auto dq_scale = [&](uint32_t dpair) { dq_d = f16_to_f32((dpair >> (16 * dq_blk)) & 0xFFFFu); };
+  auto dq_convert = [&](int j, int ws) {
+    const uint32_t u = dq_q[j >> 2][j & 3];
     const float f0 = (float)(int8_t)(u & 0xFFu) * dq_d, f1 = (float)(int8_t)((u >> 8) & 0xFFu) * dq_d;
     const float f2 = (float)(int8_t)((u >> 16) & 0xFFu) * dq_d, f3 = (float)(int8_t)(u >> 24) * dq_d;
     const int c = (4 * dq_blk + (j >> 1)) ^ chunk_swz(dq_row);
     *(u32x2*)(smem + ws * 65536 + 32768 + dq_row * 128 + c * 16 + 8 * (j & 1)) =
         u32x2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
+  };
+  auto dequant_all = [&](int rs, int ws, uint32_t dpair) {
+    dq_read(0, rs);
+    dq_read(1, rs);
+    dq_scale(dpair);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dq_convert(j, ws);
   };
   // v_mfma_f32_16x16x32_bf16 operands: lane l holds row l%16, k = 8*(l/16) .. +7 of a slice of 32
   const int lo = lane & 15, q4 = lane >> 4, fs = chunk_swz(lo);
@@ -665,22 +677,27 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // The DMA then has from B1 of one step to B2 of the next to land (about 1.6 steps), and the
   // barrier before the DMA waits on no memory.
   // Q8 adds: after B1, the dequantisation of step t+2's codes (raw stage cur, landed: B1 waits
-  // for them) into the freed W stage cur, spread over MFMAs DQ0 .. DQ0+18 of the second slice,
-  // when this step's first-slice fragments are dead (their registers hold it); at DQ0+1, the
-  // load of step t+3's scales into the register part 0 has just read; after B2, the codes' DMA
-  // of step t+4 into raw stage cur (free: every wave's dequantisation reads of it are behind
-  // B2), so the codes have about 1.5 steps to land and the scales about one.  The X DMA of step
-  // t+2 goes out in four parts, at B1 and after the scale load (DQ0+3, +5, +7).  So B1's wait
-  // leaves out the 3 X parts and 2 code DMAs issued after the scales it needs (the X part at
-  // B1 of the step before must have landed too), and B2's the codes of step t+3, the X DMA of
-  // step t+2 and the scale load between its parts.  The dequantisation's stores are done
-  // (lgkmcnt 0) at the next B1, a step before anything reads them.
+  // for them) into the freed W stage cur.  The thread's two 16-code reads go out at DQR0 and DQR1,
+  // in registers of first-slice X fragments already dead, a dozen MFMAs before the first
+  // conversion needs them; at DQ0 the scale's wait, then a conversion (a 4-code word to 8 bytes of
+  // bf16 in LDS) every other MFMA through DQ0+14.  At DQ0+1, the load of step t+3's scales into
+  // the register the conversions just read; after B2, the codes' DMA of step t+4 into raw stage
+  // cur (free: every wave's reads of it are behind B2), so the codes have about 1.5 steps to land
+  // and the scales about one.  The X DMA of step t+2 goes out in four parts, at B1 and after the
+  // scale load (DQ0+3, +5, +7).  In the order the vector memory counter sees them, a step issues
+  // X(B1), scales(DQ0+1), X(DQ0+3, +5, +7), codes(B2+1, B2+4):
+  //   B1 waits for the codes of step t+2 (issued at step t-2), leaving out the 7 issued since;
+  //   DQ0 waits for the scales (issued at step t-1), leaving out the 6 issued since;
+  //   B2 waits for step t+1's X (issued at step t-1), leaving out the 7 issued since.
+  // The scale load is invisible to the compiler (see buffer_load_u32_untracked): DQ0's wait is
+  // what covers it.  The dequantisation's stores are done (lgkmcnt 0) at the next B1, a step
+  // before anything reads them.
   constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DSPREAD = NMF;
-  constexpr int DQ0 = NMF;
-  constexpr int B1_VM = Q8 ? (NDMA - 1) + NRAW : 63, B2_VM = Q8 ? NRAW + NDMA + 1 : NDMA;
+  constexpr int DQ0 = NMF, DQR0 = B1 + 6, DQR1 = B1 + 8;
+  constexpr int B1_VM = Q8 ? NDMA + 1 + NRAW : 63, B2_VM = Q8 ? NRAW + NDMA + 1 : NDMA, DQ_VM = NDMA + NRAW;
   // B2 lets this step's NDMA DMA parts stay outstanding, and no more: they must all be out
   static_assert(B1 >= NRD && B1 + DSPREAD <= B2 && B2 + NRD <= 2 * NMF, "step schedule");
-  static_assert(!Q8 || (DQ0 > B1 && DQ0 + 18 < B2), "the dequantisation fits between the barriers");
+  static_assert(!Q8 || (DQR1 < DQ0 && DQ0 + 14 < B2), "the dequantisation fits between the barriers");
   // Q8: the scales of the k-step the next dequantisation takes (both blocks of each tile row)
   uint32_t sc = 0;
   auto step = [&](Frag& F0, Frag& F1, int t) {
@@ -694,9 +711,6 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
         __builtin_amdgcn_s_waitcnt((B1_VM & 15) | (0x7 << 4) | (0x0 << 8) | ((B1_VM >> 4) << 14));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        // Q8: the scale load is invisible to the compiler; this marks its register as written
-        // here, after the wait that covers it, so that no use of it moves above the wait
-        if constexpr (Q8) asm volatile("" : "+v"(sc));
       }
       if (x == B2) {
         asm volatile("" ::: "memory");
@@ -723,11 +737,21 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
           dma_part(nx, cur, p);
       }
       if constexpr (Q8) {
-        if (x >= DQ0 && x <= DQ0 + 18 && (x - DQ0) % 2 == 0) dequant((x - DQ0) / 2, cur, cur, sc);
+        if (x == DQR0) dq_read(0, cur);
+        if (x == DQR1) dq_read(1, cur);
+        if (x == DQ0) {
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_s_waitcnt((DQ_VM & 15) | (0x7 << 4) | (0xF << 8) | ((DQ_VM >> 4) << 14));
+          // the scale load is invisible to the compiler; this marks its register as written here,
+          // after the wait that covers it, so that no use of it moves above the wait
+          asm volatile("" : "+v"(sc));
+          dq_scale(sc);
+        }
+        if (x >= DQ0 && x < DQ0 + 16 && (x - DQ0) % 2 == 0) dq_convert((x - DQ0) / 2, cur);
         const int nq = min(t + 4, kt1 - 1);   // the codes' step
         if (x == B2 + 1) raw_dma(nq, cur, 0);
         if (x == B2 + 4) raw_dma(nq, cur, 1);
-        // the next step's scales, into the register part 0 of the dequantisation has just read
+        // the next step's scales, into the register the conversions have just read
         if (x == DQ0 + 1) sc = scale_load(min(t + 3, kt1 - 1));
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -749,11 +773,9 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
 #pragma unroll
     for (int p = 0; p < NDMA; ++p) dma_part(kt0, 0, p);
     LDS_VMCNT0_BARRIER();
-    asm volatile("" : "+v"(sa), "+v"(sb));   // the scales' uses stay after the wait (see B1)
-#pragma unroll
-    for (int part = 0; part <= 9; ++part) dequant(part, 0, 0, sa);
-#pragma unroll
-    for (int part = 0; part <= 9; ++part) dequant(part, 1, 1, sb);
+    asm volatile("" : "+v"(sa), "+v"(sb));   // the scales' uses stay after the wait (see DQ0)
+    dequant_all(0, 0, sa);
+    dequant_all(1, 1, sb);
     LDS_VMCNT0_BARRIER();   // the codes read, stages 0 and 1 of W written
     // in the order the loop's waits count: codes of kt0 + 2, X of kt0 + 1, codes of kt0 + 3
     raw_dma(min(kt0 + 2, kt1 - 1), 0, 0);
@@ -788,11 +810,10 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
-// bf16 weights WB, or (Q8) Q8_0 weights QS/QD dequantised in the pipeline
+// bf16 weights WB, or (Q8) tiled Q8_0 weights QT dequantised in the pipeline
 template <int EPI, bool Q8 = false>
 static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* wb, int64_t M, int64_t N,
-                            int64_t K, const EpiArgs& ea, int split = 1, const int8_t* qs = nullptr,
-                            const uint16_t* qd = nullptr) {
+                            int64_t K, const EpiArgs& ea, int split = 1, const uint8_t* qt = nullptr) {
   const size_t shm = Q8 ? 2 * 65536 + 2 * 16384 : 2 * 65536;
   constexpr int NW = 8;
   auto kern = k_gemm_bt<EPI, NW, Q8>;
@@ -803,19 +824,18 @@ static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const
     attr = true;
   }
   dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256), (unsigned)split);
-  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, qs, qd, M, N, K, ea);
+  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, qt, M, N, K, ea);
   return hipGetLastError();
 }
 
 // the LDS-DMA pipeline's conditions on X and the output (16-byte chunks of X rows, 4-column
-// stores, buffer extents within 31 bits) and on the weight (bf16 rows or Q8_0 codes)
+// stores, buffer extents within 31 bits) and on the weight (bf16 rows or tiled Q8_0)
 static bool dma_fits(const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K,
                      const EpiArgs& ea) {
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  // Q8_0 codes: K % 128 == 0 (the kernel runs k-steps in pairs)
+  // tiled Q8_0: K % 128 == 0 (the kernel runs k-steps in pairs), a tile's chunks within 31 bits
   const bool wok = w.wb ? (a16(w.wb) && N * K < (int64_t)1 << 30)
-                        : (w.qs && w.qd && a16(w.qs) && ((uintptr_t)w.qd & 1) == 0 && N * K < (int64_t)1 << 31 &&
-                           K % 128 == 0);
+                        : (w.qt && a16(w.qt) && K % 128 == 0 && (K / 64) * QT_CHUNK < (int64_t)1 << 31);
   return wok && K % 64 == 0 && lda % 8 == 0 && a16(x) && M * lda < (int64_t)1 << 30 && N % 4 == 0 &&
          ea.ldy % 4 == 0 && a16(ea.y) && a16(ea.resid) && a16(ea.gate) && ea.mstride % 4 == 0;
 }
@@ -824,13 +844,12 @@ template <int EPI>
 static hipError_t launch_w(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
                            int64_t K, const EpiArgs& ea, int split = 1) {
   if (w.wb) return launch_bt<EPI, false>(s, x, lda, w.wb, M, N, K, ea, split);
-  return launch_bt<EPI, true>(s, x, lda, nullptr, M, N, K, ea, split, w.qs, w.qd);
+  return launch_bt<EPI, true>(s, x, lda, nullptr, M, N, K, ea, split, w.qt);
 }
 
-hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const int8_t* qs, const uint16_t* d, int64_t M,
-                   int64_t N, int64_t K, Epi epi, const EpiArgs& ea) {
-  const WOp w{nullptr, qs, d};
-  if (!dma_fits(x, lda, w, M, N, K, ea)) return dispatch<false>(s, x, lda, qs, d, nullptr, M, N, K, epi, ea);
+hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K,
+                   Epi epi, const EpiArgs& ea) {
+  if (!dma_fits(x, lda, w, M, N, K, ea)) return dispatch<false>(s, x, lda, w.qs, w.qd, nullptr, M, N, K, epi, ea);
   switch (epi) {
     case EPI_F32: return launch_w<EPI_F32>(s, x, lda, w, M, N, K, ea);
     case EPI_BF16: return launch_w<EPI_BF16>(s, x, lda, w, M, N, K, ea);
@@ -931,7 +950,7 @@ hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w,
 
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
                       int64_t K, Epi epi, const EpiArgs& ea) {
-  const WOp wo{w, nullptr, nullptr};
+  const WOp wo{w, nullptr, nullptr, nullptr};
   if (!dma_fits(x, lda, wo, M, N, K, ea)) return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
   switch (epi) {
     case EPI_F32: return launch_w<EPI_F32>(s, x, lda, wo, M, N, K, ea);

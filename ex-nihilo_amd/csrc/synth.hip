@@ -156,4 +156,35 @@ hipError_t f32_to_bf16(hipStream_t s, const float* x, uint16_t* y, int64_t n) {
   return hipGetLastError();
 }
 
+// QT (the tiled Q8_0 operand, exn_common.h) from the SoA codes and scales: a workgroup a chunk,
+// 1024 16-byte units of codes (row u/4, bytes 16 (u%4) of the k-step) and 64 of scales (rows 4u' ..
+// 4u'+3, both blocks of the k-step each)
+__global__ void __launch_bounds__(256)
+k_tile_q8(const int8_t* __restrict__ qs, const uint16_t* __restrict__ d, int64_t N, int64_t K,
+          uint8_t* __restrict__ qt) {
+  const int64_t KT = K / 64, chunk = blockIdx.x, nb = chunk / KT, t = chunk % KT;
+  uint8_t* dst = qt + chunk * QT_CHUNK;
+  for (int u = threadIdx.x; u < QT_CHUNK / 16; u += 256) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (u < QT_SCALES / 16) {
+      const int64_t row = nb * 256 + u / 4;
+      if (row < N) v = *(const u32x4*)(qs + row * K + t * 64 + (u % 4) * 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t row = nb * 256 + 4 * (u - QT_SCALES / 16) + e;
+        if (row < N) v[e] = *(const uint32_t*)(d + row * (K / 32) + 2 * t);
+      }
+    }
+    *(u32x4*)(dst + (int64_t)u * 16) = v;
+  }
+}
+
+hipError_t tile_q8(hipStream_t s, const int8_t* qs, const uint16_t* d, int64_t N, int64_t K, uint8_t* qt) {
+  if (K % 64 || N <= 0) return hipErrorInvalidValue;
+  const int64_t chunks = (N + 255) / 256 * (K / 64);
+  hipLaunchKernelGGL(k_tile_q8, dim3((unsigned)chunks), dim3(256), 0, s, qs, d, N, K, qt);
+  return hipGetLastError();
+}
+
 }  // namespace exn
