@@ -533,6 +533,15 @@ __device__ __forceinline__ void tile_dma(const void* base, uint32_t extent, lds_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
 }
 
+// The vector memory operations a wait at position P of a step must leave out, when it waits for
+// the one at position Q of K steps before: the rest of that step, the K - 1 steps between, and
+// this step's before P (a step's operations at positions POS[0..N-1], one each, in issue order)
+constexpr int ops_after(int Q, int K, int P, const int* pos, int n) {
+  int c = (K - 1) * n;
+  for (int i = 0; i < n; ++i) c += (pos[i] > Q) + (pos[i] < P);
+  return c;
+}
+
 // NW waves of 128 x (512 / NW) a 256 x 256 tile.  The launch uses 8 waves of 128 x 64, two a
 // SIMD.  4 waves of 128 x 128 (one a SIMD, a third less LDS read a FLOP) were slower under the
 // one-barrier schedule and spill their 256 accumulators under this one.
@@ -557,8 +566,6 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   static_assert(!Q8 || NW == 8, "the Q8_0 dequantisation maps 512 threads to 256 rows x 2 blocks");
   // DMA instructions a k-step: X and W rounds (bf16), or X rounds only (Q8: the codes go apart)
   constexpr int NMF = MI * NI, NRD = MI + NI, NDMA = Q8 ? ROUNDS : 2 * ROUNDS;
-  // Q8: the codes' DMA (16 KB: 2 rounds of 8 waves x 1 KB) and the scale load, a k-step
-  constexpr int NRAW = 2;
   // 2 stages x (X tile 32 KB | W tile 32 KB), then (Q8) 2 raw code stages x 16 KB
   extern __shared__ __align__(1024) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -680,24 +687,34 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // for them) into the freed W stage cur.  The thread's two 16-code reads go out at DQR0 and DQR1,
   // in registers of first-slice X fragments already dead, a dozen MFMAs before the first
   // conversion needs them; at DQ0 the scale's wait, then a conversion (a 4-code word to 8 bytes of
-  // bf16 in LDS) every other MFMA through DQ0+14.  At DQ0+1, the load of step t+3's scales into
-  // the register the conversions just read; after B2, the codes' DMA of step t+4 into raw stage
-  // cur (free: every wave's reads of it are behind B2), so the codes have about 1.5 steps to land
-  // and the scales about one.  The X DMA of step t+2 goes out in four parts, at B1 and after the
-  // scale load (DQ0+3, +5, +7).  In the order the vector memory counter sees them, a step issues
-  // X(B1), scales(DQ0+1), X(DQ0+3, +5, +7), codes(B2+1, B2+4):
-  //   B1 waits for the codes of step t+2 (issued at step t-2), leaving out the 7 issued since;
-  //   DQ0 waits for the scales (issued at step t-1), leaving out the 6 issued since;
-  //   B2 waits for step t+1's X (issued at step t-1), leaving out the 7 issued since.
-  // The scale load is invisible to the compiler (see buffer_load_u32_untracked): DQ0's wait is
-  // what covers it.  The dequantisation's stores are done (lgkmcnt 0) at the next B1, a step
-  // before anything reads them.
+  // bf16 in LDS) every other MFMA through DQ0+14.  The step's vector memory operations: the X DMA
+  // of step t+2 in four parts (XP0..XP3: at B1 and after the first conversions), then after B2 the
+  // codes' DMA of step t+4 into raw stage cur (CP0, CP1; free: every wave's reads of it are behind
+  // B2) and, between those, the load of step t+3's scales into the register the conversions have
+  // read (SP; inside the conversions it cost 2-4% of every product).  The codes have about 1.5
+  // steps to land, the scales about 0.7.  Each wait leaves out exactly the operations issued
+  // after the one it waits for (ops_after, from the positions):
+  //   B1 for the codes of step t+2 (issued at step t-2); DQ0 for the scales (step t-1); B2 for
+  //   step t+1's X (step t-1).
+  // The prologue issues the operations of the steps before kt0 in the same order, so the first
+  // steps' waits count the same.  The scale load is invisible to the compiler (see
+  // buffer_load_u32_untracked): DQ0's wait is what covers it.  The dequantisation's stores are
+  // done (lgkmcnt 0) at the next B1, a step before anything reads them.
   constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DSPREAD = NMF;
   constexpr int DQ0 = NMF, DQR0 = B1 + 6, DQR1 = B1 + 8;
-  constexpr int B1_VM = Q8 ? NDMA + 1 + NRAW : 63, B2_VM = Q8 ? NRAW + NDMA + 1 : NDMA, DQ_VM = NDMA + NRAW;
+  constexpr int XP0 = B1, XP1 = DQ0 + 3, XP2 = DQ0 + 5, XP3 = DQ0 + 7, CP0 = B2 + 1, SP = B2 + 2, CP1 = B2 + 4;
+  constexpr int QPOS[7] = {XP0, XP1, XP2, XP3, CP0, SP, CP1};
+  constexpr int B1_VM = Q8 ? ops_after(CP1, 2, B1, QPOS, 7) : 63, B2_VM = Q8 ? ops_after(XP3, 1, B2, QPOS, 7) : NDMA,
+                DQ_VM = ops_after(SP, 1, DQ0, QPOS, 7);
   // B2 lets this step's NDMA DMA parts stay outstanding, and no more: they must all be out
   static_assert(B1 >= NRD && B1 + DSPREAD <= B2 && B2 + NRD <= 2 * NMF, "step schedule");
   static_assert(!Q8 || (DQR1 < DQ0 && DQ0 + 14 < B2), "the dequantisation fits between the barriers");
+  // the counts above take the codes' second part as a step's last operation, X's fourth as its
+  // last X part, no operation at a wait's own position, and each wait under 16 (vmcnt's 6 bits
+  // allow 63; the B1 / DQ0 / B2 order is what the schedule needs)
+  static_assert(!Q8 || (XP0 < XP1 && XP1 < XP2 && XP2 < XP3 && XP3 < CP0 && CP0 < SP && SP < CP1 && CP1 < 2 * NMF &&
+                        XP0 >= B1 && XP3 < B2 && SP > DQ0 && XP1 != DQ0 && B1_VM < 16 && B2_VM < 16 && DQ_VM < 16),
+                "Q8 operation order");
   // Q8: the scales of the k-step the next dequantisation takes (both blocks of each tile row)
   uint32_t sc = 0;
   auto step = [&](Frag& F0, Frag& F1, int t) {
@@ -728,9 +745,11 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
       if (x < NRD) rd1(F1, cur, 1, x);
       if (x >= B2 && x < B2 + NRD) rd1(F0, cur ^ 1, 0, x - B2);
       if constexpr (Q8) {
-        static_assert(NDMA == 4, "X parts at B1, DQ0+3, DQ0+5, DQ0+7");
-        if (x == B1) dma_part(nx, cur, 0);
-        if (x == DQ0 + 3 || x == DQ0 + 5 || x == DQ0 + 7) dma_part(nx, cur, (x - DQ0 - 1) / 2);
+        static_assert(NDMA == 4, "X parts at XP0 .. XP3");
+        if (x == XP0) dma_part(nx, cur, 0);
+        if (x == XP1) dma_part(nx, cur, 1);
+        if (x == XP2) dma_part(nx, cur, 2);
+        if (x == XP3) dma_part(nx, cur, 3);
       } else if (x >= B1 && x < B1 + DSPREAD) {
 #pragma unroll
         for (int p = ((x - B1) * NDMA) / DSPREAD; p < ((x - B1 + 1) * NDMA) / DSPREAD && p < NDMA; ++p)
@@ -749,10 +768,10 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
         }
         if (x >= DQ0 && x < DQ0 + 16 && (x - DQ0) % 2 == 0) dq_convert((x - DQ0) / 2, cur);
         const int nq = min(t + 4, kt1 - 1);   // the codes' step
-        if (x == B2 + 1) raw_dma(nq, cur, 0);
-        if (x == B2 + 4) raw_dma(nq, cur, 1);
-        // the next step's scales, into the register the conversions have just read
-        if (x == DQ0 + 1) sc = scale_load(min(t + 3, kt1 - 1));
+        if (x == CP0) raw_dma(nq, cur, 0);
+        if (x == CP1) raw_dma(nq, cur, 1);
+        // the next step's scales, into the register the conversions have read
+        if (x == SP) sc = scale_load(min(t + 3, kt1 - 1));
       }
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -777,14 +796,21 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     dequant_all(0, 0, sa);
     dequant_all(1, 1, sb);
     LDS_VMCNT0_BARRIER();   // the codes read, stages 0 and 1 of W written
-    // in the order the loop's waits count: codes of kt0 + 2, X of kt0 + 1, codes of kt0 + 3
+    // the operations the loop's first waits count, as the steps before kt0 would have issued
+    // them: step kt0 - 2's codes (of kt0 + 2), then step kt0 - 1's in position order (X of kt0 + 1,
+    // the codes of kt0 + 3, the scales of kt0 + 2)
     raw_dma(min(kt0 + 2, kt1 - 1), 0, 0);
     raw_dma(min(kt0 + 2, kt1 - 1), 0, 1);
-    sc = scale_load(min(kt0 + 2, kt1 - 1));
 #pragma unroll
-    for (int p = 0; p < NDMA; ++p) dma_part(t1, 1, p);
-    raw_dma(min(kt0 + 3, kt1 - 1), 1, 0);
-    raw_dma(min(kt0 + 3, kt1 - 1), 1, 1);
+    for (int x = 0; x < 2 * NMF; ++x) {
+      if (x == XP0) dma_part(t1, 1, 0);
+      if (x == XP1) dma_part(t1, 1, 1);
+      if (x == XP2) dma_part(t1, 1, 2);
+      if (x == XP3) dma_part(t1, 1, 3);
+      if (x == CP0) raw_dma(min(kt0 + 3, kt1 - 1), 1, 0);
+      if (x == SP) sc = scale_load(min(kt0 + 2, kt1 - 1));
+      if (x == CP1) raw_dma(min(kt0 + 3, kt1 - 1), 1, 1);
+    }
 #pragma unroll
     for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
     for (int t = kt0; t < kt1; ++t) step(F0, F1, t);

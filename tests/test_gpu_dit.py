@@ -361,16 +361,18 @@ def test_full_shapes_two_blocks(ctx, case):
     d.destroy()
 
 
-def test_cfg2_eight_steps_full_depth(ctx):
+@pytest.mark.parametrize("resident", [True, False], ids=["resident_bf16", "q8_0"])
+def test_cfg2_eight_steps_full_depth(ctx, resident):
     """The 1024^2 workload end to end: 32 blocks, 4096 image rows over 256 text rows, the
     first step's velocity (uncached, <= 1e-2) and the final latent after the 8 Turbo steps
     of the device Euler loop (<= 2e-2), against the oracle's run cached as float16 in
-    tests/golden/dit_cfg2_8step.npz (about 75 minutes of numpy)."""
+    tests/golden/dit_cfg2_8step.npz (about 75 minutes of numpy); from the resident bf16
+    expansion and from Q8_0 dequantised in the products."""
     g = np.load(os.path.join(GOLDEN, "dit_cfg2_8step.npz"))
     seed, p, h, w = (int(v) for v in g["meta"])
-    say("cfg2: 32 blocks, p", p, "image", h, "x", w, "8 steps")
+    say("cfg2: 32 blocks, p", p, "image", h, "x", w, "8 steps, resident", resident)
     d = model(ctx, 32, seed)
-    d.resident(True)
+    d.resident(resident)
     ctxa, lat = xo.synth_inputs(seed, p, h, w)
     v0 = X.dit_velocity(d, ctxa, p, lat, h, w, xo.TURBO_SIGMAS[0])
     e0 = xo.rel_l2(v0, g["v_step0"].astype(np.float32))
