@@ -636,26 +636,33 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   };
   auto scale_load = [&](int t) -> uint32_t { return buffer_load_u32_untracked(qrsrc, doff, (uint32_t)(t * QT_CHUNK)); };
   // Q8: the thread's 32 codes of raw stage rs into bf16 W stage ws: two 16-code reads (dq_read,
-  // halves 0 and 1), the block's fp16 scale from the half dq_blk of DPAIR (dq_scale), then eight
-  // conversions of one 4-code word each, each storing its 8 bytes of bf16 (dq_convert)
+  // halves 0 and 1), the block's fp16 scale from the half dq_blk of DPAIR (dq_scale), then four
+  // conversions of 8 codes each, each storing its 16-byte chunk of bf16 (dq_convert).  The 16
+  // lanes of a store quarter-wave (8 rows x 2 blocks) fill 16 distinct (row parity, chunk)
+  // places, so the stores are free of bank conflicts (8-byte stores of half chunks met in pairs)
   u32x4 dq_q[2];
   float dq_d = 0.f;
   auto dq_read = [&](int h, int rs) { dq_q[h] = *(const u32x4*)(smem + 131072 + rs * 16384 + tid * 32 + 16 * h); };
   auto dq_scale = [&](uint32_t dpair) { dq_d = f16_to_f32((dpair >> (16 * dq_blk)) & 0xFFFFu); };
   auto dq_convert = [&](int j, int ws) {
-    const uint32_t u = dq_q[j >> 2][j & 3];
-    const float f0 = (float)(int8_t)(u & 0xFFu) * dq_d, f1 = (float)(int8_t)((u >> 8) & 0xFFu) * dq_d;
-    const float f2 = (float)(int8_t)((u >> 16) & 0xFFu) * dq_d, f3 = (float)(int8_t)(u >> 24) * dq_d;
-    const int c = (4 * dq_blk + (j >> 1)) ^ chunk_swz(dq_row);
-    *(u32x2*)(smem + ws * 65536 + 32768 + dq_row * 128 + c * 16 + 8 * (j & 1)) =
-        u32x2{pack_bf16x2(f0, f1), pack_bf16x2(f2, f3)};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t u = dq_q[j >> 1][2 * (j & 1) + e];
+      const float f0 = (float)(int8_t)(u & 0xFFu) * dq_d, f1 = (float)(int8_t)((u >> 8) & 0xFFu) * dq_d;
+      const float f2 = (float)(int8_t)((u >> 16) & 0xFFu) * dq_d, f3 = (float)(int8_t)(u >> 24) * dq_d;
+      o[2 * e] = pack_bf16x2(f0, f1);
+      o[2 * e + 1] = pack_bf16x2(f2, f3);
+    }
+    const int c = (4 * dq_blk + j) ^ chunk_swz(dq_row);
+    *(u32x4*)(smem + ws * 65536 + 32768 + dq_row * 128 + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
   };
   auto dequant_all = [&](int rs, int ws, uint32_t dpair) {
     dq_read(0, rs);
     dq_read(1, rs);
     dq_scale(dpair);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dq_convert(j, ws);
+    for (int j = 0; j < 4; ++j) dq_convert(j, ws);
   };
   // v_mfma_f32_16x16x32_bf16 operands: lane l holds row l%16, k = 8*(l/16) .. +7 of a slice of 32
   const int lo = lane & 15, q4 = lane >> 4, fs = chunk_swz(lo);
@@ -686,8 +693,8 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // Q8 adds: after B1, the dequantisation of step t+2's codes (raw stage cur, landed: B1 waits
   // for them) into the freed W stage cur.  The thread's two 16-code reads go out at DQR0 and DQR1,
   // in registers of first-slice X fragments already dead, a dozen MFMAs before the first
-  // conversion needs them; at DQ0 the scale's wait, then a conversion (a 4-code word to 8 bytes of
-  // bf16 in LDS) every other MFMA through DQ0+14.  The step's vector memory operations: the X DMA
+  // conversion needs them; at DQ0 the scale's wait, then a conversion (8 codes to a 16-byte chunk
+  // of bf16 in LDS) every DQS MFMAs through DQ0+3 DQS.  The step's vector memory operations: the X DMA
   // of step t+2 in four parts (XP0..XP3: at B1 and after the first conversions), then after B2 the
   // codes' DMA of step t+4 into raw stage cur (CP0, CP1; free: every wave's reads of it are behind
   // B2) and, between those, the load of step t+3's scales into the register the conversions have
@@ -701,14 +708,15 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
   // buffer_load_u32_untracked): DQ0's wait is what covers it.  The dequantisation's stores are
   // done (lgkmcnt 0) at the next B1, a step before anything reads them.
   constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DSPREAD = NMF;
-  constexpr int DQ0 = NMF, DQR0 = B1 + 6, DQR1 = B1 + 8;
+  constexpr int DQ0 = NMF, DQS = 4, DQR0 = B1 + 6, DQR1 = B1 + 8;
   constexpr int XP0 = B1, XP1 = DQ0 + 3, XP2 = DQ0 + 5, XP3 = DQ0 + 7, CP0 = B2 + 1, SP = B2 + 2, CP1 = B2 + 4;
   constexpr int QPOS[7] = {XP0, XP1, XP2, XP3, CP0, SP, CP1};
   constexpr int B1_VM = Q8 ? ops_after(CP1, 2, B1, QPOS, 7) : 63, B2_VM = Q8 ? ops_after(XP3, 1, B2, QPOS, 7) : NDMA,
                 DQ_VM = ops_after(SP, 1, DQ0, QPOS, 7);
   // B2 lets this step's NDMA DMA parts stay outstanding, and no more: they must all be out
   static_assert(B1 >= NRD && B1 + DSPREAD <= B2 && B2 + NRD <= 2 * NMF, "step schedule");
-  static_assert(!Q8 || (DQR1 < DQ0 && DQ0 + 14 < B2), "the dequantisation fits between the barriers");
+  static_assert(!Q8 || (B1 < DQR0 && DQR0 < DQR1 && DQR1 < DQ0 && DQ0 + 3 * DQS < B2),
+                "the dequantisation fits between the barriers");
   // the counts above take the codes' second part as a step's last operation, X's fourth as its
   // last X part, no operation at a wait's own position, and each wait under 16 (vmcnt's 6 bits
   // allow 63; the B1 / DQ0 / B2 order is what the schedule needs)
@@ -766,7 +774,7 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
           asm volatile("" : "+v"(sc));
           dq_scale(sc);
         }
-        if (x >= DQ0 && x < DQ0 + 16 && (x - DQ0) % 2 == 0) dq_convert((x - DQ0) / 2, cur);
+        if (x >= DQ0 && x <= DQ0 + 3 * DQS && (x - DQ0) % DQS == 0) dq_convert((x - DQ0) / DQS, cur);
         const int nq = min(t + 4, kt1 - 1);   // the codes' step
         if (x == CP0) raw_dma(nq, cur, 0);
         if (x == CP1) raw_dma(nq, cur, 1);
@@ -836,6 +844,214 @@ k_gemm_bt(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restric
     epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
 }
 
+// 16- and 4-byte buffer loads into V that the compiler does not see as loads (as
+// buffer_load_u32_untracked), the destination tied to V's register (an in-out operand), so that
+// the value keeps one register from the load to its use and no copy of it is made in between
+__device__ __forceinline__ void buffer_load_u128_into(u32x4& v, i32x4 rsrc, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "+v"(v) : "v"(voff), "s"(rsrc), "s"(soff));
+}
+__device__ __forceinline__ void buffer_load_u32_into(uint32_t& v, i32x4 rsrc, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "+v"(v) : "v"(voff), "s"(rsrc), "s"(soff));
+}
+
+// The Q8_0 block products over many rows: 512 x 128 tiles, so that a tile dequantises 128 weight
+// rows for 512 activation rows -- half the conversions an MFMA of k_gemm_bt's 256 x 256 tiles
+// (whose exact conversion, a byte-to-float conversion, a multiply and half a pack a weight, is
+// the Q8_0 path's largest cost).  8 waves of 128 x 64 (4 x 2; the QKV epilogue's 64 x 128, one
+// head a wave: 8 x 1), BK = 64 in two slices of 32, the step schedule of k_gemm_bt:
+//   a stage is the X tile (512 rows, 64 KB, by the LDS DMA) and the W tile (128 rows of bf16,
+//   16 KB, written by the dequantisation); two stages fill the 160 KB of LDS, so the codes go to
+//   registers: thread t loads the 16 codes of tile row t/4, k 16 (t%4) .. +15 (one 16-byte load,
+//   a wave's 64 one contiguous KB of the tiled operand) and the dword of that row's two scales,
+//   a step ahead, and converts them into the W tile of step t+2 once B1 has freed it.
+// The tiled operand's 256-row chunks hold two 128-row tiles: tile bn is chunk bn/2, rows
+// 128 (bn%2) .. (codes at 8 KB (bn%2), scales at QT_SCALES + 512 (bn%2)).
+template <int EPI>
+__global__ void __launch_bounds__(512)
+k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __restrict__ QT, int64_t M, int64_t N,
+               int64_t K, EpiArgs ea) {
+  constexpr bool HEADS = EPI == EPI_QKV;
+  constexpr int WM = HEADS ? 64 : 128, WN = HEADS ? 128 : 64, MI = WM / 16, NI = WN / 16;
+  static_assert((512 / WM) * (128 / WN) == 8, "the waves tile 512 x 128");
+  constexpr int NMF = MI * NI, NRD = MI + NI, XPARTS = 8, STAGE = 81920, WOFF = 65536;
+  extern __shared__ __align__(1024) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / (128 / WN), wn = wave % (128 / WN);
+  // tile order: workgroups go to the 8 XCDs in turn, so XCD x takes the x-th eighth of a tile
+  // order that walks 2 row tiles at a time -- its concurrent tiles share W and X in its L2
+  int bm = blockIdx.y, bn = blockIdx.x;
+  {
+    const int gx = gridDim.x, gy = gridDim.y, G = gx * gy, b = blockIdx.y * gx + blockIdx.x;
+    const int L = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
+    constexpr int GM = 2;
+    const int grp = L / (GM * gx), first = grp * GM, sz = min(gy - first, GM), in = L % (GM * gx);
+    bm = first + in % sz;
+    bn = in / sz;
+  }
+  const int64_t m0 = (int64_t)bm * 512, n0 = (int64_t)bn * 128;
+  // split K (EPI_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1, cut in pairs as
+  // k_gemm_bt cuts them (K % 128 == 0), so that both give the same partial sums
+  const int KT = (int)(K / 64), SK = gridDim.z, zk = blockIdx.z;
+  const int kt0 = 2 * (int)((int64_t)(KT / 2) * zk / SK), kt1 = 2 * (int)((int64_t)(KT / 2) * (zk + 1) / SK);
+  // X DMA part p of wave w: tile rows (8p + w) 8 .. +7, lane l row +l/8, LDS chunk l%8 (global
+  // chunk (l%8) ^ swizzle, the same for every part: 64 p rows keep (row/2)%8); the part's rows
+  // move the buffer's base and shrink its extent (the range check covers the vector offset only)
+  const uint16_t* xbase = X + m0 * lda;
+  uint32_t xoff;
+  {
+    const int row = wave * 8 + (lane >> 3);
+    xoff = (uint32_t)((row * lda + 8 * ((lane & 7) ^ chunk_swz(row))) * 2);
+  }
+  auto dma_part = [&](int t, int stage, int p) {
+    uint8_t* dst = smem + stage * STAGE + (p * 8 + wave) * 1024;
+    const int64_t r0 = (int64_t)p * 64;
+    tile_dma(xbase + r0 * lda, (uint32_t)(max((int64_t)0, M - m0 - r0) * lda * 2), (lds_void*)dst, xoff, t * 128);
+  };
+  // the codes and scales of step t into registers (every offset inside the tile's chunks)
+  const i32x4 qrsrc = buffer_desc(QT + (int64_t)(bn >> 1) * KT * QT_CHUNK, (uint32_t)((int64_t)KT * QT_CHUNK));
+  const uint32_t coff = (uint32_t)((bn & 1) * 8192 + tid * 16);
+  const uint32_t soff = (uint32_t)(QT_SCALES + (bn & 1) * 512 + (tid >> 2) * 4);
+  const int dq_row = tid >> 2, dq_q = tid & 3;
+  u32x4 cq = {0u, 0u, 0u, 0u};
+  uint32_t sq = 0;
+  auto code_load = [&](int t) {
+    buffer_load_u128_into(cq, qrsrc, coff, (uint32_t)(t * QT_CHUNK));
+    buffer_load_u32_into(sq, qrsrc, soff, (uint32_t)(t * QT_CHUNK));
+  };
+  // conversion h (0, 1): codes 8h .. 8h+7 of the thread's 16 into the 16-byte chunk of bf16 at
+  // k 16 q + 8h, one store a chunk: the 16 lanes of a store quarter-wave (4 rows x 4 quarters)
+  // then fill 16 distinct (row parity, chunk) places, so the stores are free of bank conflicts
+  // (8-byte stores of half chunks met in pairs and cost about 8% of the product)
+  float dq_d = 0.f;
+  auto dq_scale = [&]() { dq_d = f16_to_f32((sq >> (16 * (dq_q >> 1))) & 0xFFFFu); };
+  auto dq_convert = [&](int h, int ws) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t u = cq[2 * h + e];
+      const float f0 = (float)(int8_t)(u & 0xFFu) * dq_d, f1 = (float)(int8_t)((u >> 8) & 0xFFu) * dq_d;
+      const float f2 = (float)(int8_t)((u >> 16) & 0xFFu) * dq_d, f3 = (float)(int8_t)(u >> 24) * dq_d;
+      o[2 * e] = pack_bf16x2(f0, f1);
+      o[2 * e + 1] = pack_bf16x2(f2, f3);
+    }
+    const int c = (2 * dq_q + h) ^ chunk_swz(dq_row);
+    *(u32x4*)(smem + ws * STAGE + WOFF + dq_row * 128 + c * 16) = u32x4{o[0], o[1], o[2], o[3]};
+  };
+  // v_mfma_f32_16x16x32_bf16 operands: lane l holds row l%16, k = 8*(l/16) .. +7 of a slice of 32
+  const int lo = lane & 15, q4 = lane >> 4, fs = chunk_swz(lo);
+  const uint8_t* a_rd = smem + (wm * WM + lo) * 128;
+  const uint8_t* b_rd = smem + WOFF + (wn * WN + lo) * 128;
+  struct Frag {
+    bf16x8 v[NRD];
+  };
+  auto rd1 = [&](Frag& f, int stage, int kk, int q) {
+    const int off = stage * STAGE + (((4 * kk + q4) ^ fs) << 4);
+    if (q < MI) f.v[q] = *(const bf16x8*)(a_rd + off + q * 16 * 128);
+    else f.v[q] = *(const bf16x8*)(b_rd + off + (q - MI) * 16 * 128);
+  };
+  f32x4 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // A step (k_gemm_bt's): MFMAs 0..NRD-1 read this step's second-slice fragments (stage cur);
+  // B1: every wave is done with stage cur; the X DMA of step t+2 into it at XP0..XP7; at DQ0 the
+  // codes' wait, then two conversions (DQ0, DQ0+4) of step t+2's codes into W stage cur;
+  // at CLP the codes and scales of step t+3 into the registers just read; B2: step t+1's X has
+  // landed (its W was written a step before, behind this step's B1); then step t+1's first-slice
+  // fragments from stage cur^1.  The waits leave out what ops_after counts from the positions.
+  constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DQ0 = B1 + 10, CLP = DQ0 + 7;
+  constexpr int QPOS[10] = {B1, B1 + 4, B1 + 8, B1 + 12, CLP, CLP + 1, B1 + 20, B1 + 24, B1 + 28, B1 + 32};
+  constexpr int DQ_VM = ops_after(CLP + 1, 1, DQ0, QPOS, 10), B2_VM = ops_after(B1 + 32, 1, B2, QPOS, 10);
+  static_assert(B1 >= NRD && B1 + 32 < B2 && B2 + NRD <= 2 * NMF && DQ0 > B1 + 8 && DQ0 + 6 < CLP &&
+                    CLP + 1 < B1 + 20 && DQ_VM < 16 && B2_VM < 16,
+                "step schedule");
+  auto step = [&](Frag& F0, Frag& F1, int t) {
+    const int cur = (t - kt0) & 1, nx = min(t + 2, kt1 - 1);
+    auto pos = [&](const int x) {
+      if (x == B1) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt((63 & 15) | (0x7 << 4) | (0x0 << 8) | ((63 >> 4) << 14));   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      if (x == B2) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt((B2_VM & 15) | (0x7 << 4) | (0x0 << 8) | ((B2_VM >> 4) << 14));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      const int y = x % NMF;
+      if (x < NMF)
+        acc[y / NI][y % NI] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(F0.v[y / NI], F0.v[MI + y % NI], acc[y / NI][y % NI], 0, 0, 0);
+      else
+        acc[y / NI][y % NI] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(F1.v[y / NI], F1.v[MI + y % NI], acc[y / NI][y % NI], 0, 0, 0);
+      if (x < NRD) rd1(F1, cur, 1, x);
+      if (x >= B2 && x < B2 + NRD) rd1(F0, cur ^ 1, 0, x - B2);
+#pragma unroll
+      for (int p = 0; p < XPARTS; ++p)
+        if (x == QPOS[p < 4 ? p : p + 2]) dma_part(nx, cur, p);
+      if (x == DQ0) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt((DQ_VM & 15) | (0x7 << 4) | (0xF << 8) | ((DQ_VM >> 4) << 14));
+        // the loads are invisible to the compiler; this marks their registers as written here,
+        // after the wait that covers them, so that no use of them moves above the wait
+        asm volatile("" : "+v"(cq), "+v"(sq));
+        dq_scale();
+      }
+      if (x == DQ0 || x == DQ0 + 4) dq_convert((x - DQ0) / 4, cur);
+      if (x == CLP) code_load(min(t + 3, kt1 - 1));
+      __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int x = 0; x < NMF; ++x) pos(x);
+#pragma unroll
+    for (int x = NMF; x < 2 * NMF; ++x) pos(x);
+  };
+  Frag F0, F1;
+  {
+    // stages 0, 1: X of kt0 by DMA, the codes of kt0 and kt0 + 1 converted into both W tiles
+    const int t1 = min(kt0 + 1, kt1 - 1);
+#pragma unroll
+    for (int p = 0; p < XPARTS; ++p) dma_part(kt0, 0, p);
+    code_load(kt0);
+    LDS_VMCNT0_BARRIER();
+    asm volatile("" : "+v"(cq), "+v"(sq));
+    dq_scale();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) dq_convert(h, 0);
+    code_load(t1);
+    LDS_VMCNT0_BARRIER();
+    asm volatile("" : "+v"(cq), "+v"(sq));
+    dq_scale();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) dq_convert(h, 1);
+    LDS_VMCNT0_BARRIER();   // the codes read, stages 0 and 1 of W written, stage 0 of X landed
+    // step kt0 - 1's operations in position order: X of kt0 + 1, the codes of kt0 + 2
+#pragma unroll
+    for (int x = 0; x < 2 * NMF; ++x) {
+#pragma unroll
+      for (int p = 0; p < XPARTS; ++p)
+        if (x == QPOS[p < 4 ? p : p + 2]) dma_part(t1, 1, p);
+      if (x == CLP) code_load(min(kt0 + 2, kt1 - 1));
+    }
+#pragma unroll
+    for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
+  }
+  for (int t = kt0; t < kt1; ++t) step(F0, F1, t);
+  LDS_VMCNT0_BARRIER();   // the last DMA and loads have landed before the epilogue takes the LDS over
+  asm volatile("" ::"v"(cq), "v"(sq));
+  if constexpr (HEADS)
+    epilogue_qkv<MI, NI>(acc, (float*)smem + wave * (16 * 132), m0 + wm * WM, n0 + wn * WN, lane, M, ea);
+  else if constexpr (EPI == EPI_SWIGLU)
+    epilogue_swiglu<MI, NI>(acc, (uint16_t*)smem + wave * (WM * 40), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
+  else
+    epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * (WN + 8)), m0 + wm * WM, n0 + wn * WN, lane, M, N, ea);
+}
+
 // bf16 weights WB, or (Q8) tiled Q8_0 weights QT dequantised in the pipeline
 template <int EPI, bool Q8 = false>
 static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* wb, int64_t M, int64_t N,
@@ -867,9 +1083,28 @@ static bool dma_fits(const uint16_t* x, int64_t lda, const WOp& w, int64_t M, in
 }
 
 template <int EPI>
+static hipError_t launch_tall(hipStream_t s, const uint16_t* x, int64_t lda, const uint8_t* qt, int64_t M, int64_t N,
+                              int64_t K, const EpiArgs& ea, int split) {
+  const size_t shm = 2 * 81920;
+  auto kern = k_gemm_q8_tall<EPI>;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 511) / 512), (unsigned)split);
+  hipLaunchKernelGGL(kern, grid, dim3(512), shm, s, x, lda, qt, M, N, K, ea);
+  return hipGetLastError();
+}
+
+// Q8_0 products of at least 512 rows take the 512 x 128 tiles (half the conversions an MFMA);
+// the same sums in the same order either way
+template <int EPI>
 static hipError_t launch_w(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
                            int64_t K, const EpiArgs& ea, int split = 1) {
   if (w.wb) return launch_bt<EPI, false>(s, x, lda, w.wb, M, N, K, ea, split);
+  if (M >= 512 && N % 128 == 0) return launch_tall<EPI>(s, x, lda, w.qt, M, N, K, ea, split);
   return launch_bt<EPI, true>(s, x, lda, nullptr, M, N, K, ea, split, w.qt);
 }
 
