@@ -23,7 +23,8 @@ from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(HERE), "libexn-hip.so")
+# the build beside the package, or another build of it named by EXN_HIP_LIB (the sanitized host build)
+LIB_PATH = os.environ.get("EXN_HIP_LIB") or os.path.join(os.path.dirname(HERE), "libexn-hip.so")
 
 OK, ENODEV, EINVAL, ENOMEM, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
 Q8_0, F32, BF16, F16 = 8, 0, 30, 1

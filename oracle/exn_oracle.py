@@ -623,6 +623,40 @@ def forward(wt, ctx, latent, sigma, shape=Shape(), ref=None, cache: PrefixCache 
     return v.T.reshape(c, h, w).astype(np.float32)
 
 
+class Overrides:
+    """The synthetic weights WT with some matrices replaced (OVER: name -> fp32 matrix)."""
+
+    def __init__(self, wt, over):
+        self.wt, self.over = wt, over
+
+    def __call__(self, name):
+        return self.over[name] if name in self.over else self.wt(name)
+
+
+# Weights at the magnitudes real checkpoints reach, for parity off the unit-scale synthetic data.
+# txt_in_8e5: txt_in's in_layer scaled so its GELU's rows reach about 8e5 (the magnitude the
+# reference records for the real weights, src/metal-dit.lisp:5-7), and the prompt rows of the
+# residual stream about 7e5 after out_layer.  img_in_outliers: eight of img_in's 4096 output
+# channels scaled by 80, so every image row of the residual stream carries outlier channels
+# through the blocks (they then hold most of each row's variance).
+MAGNITUDE_CASES = {
+    "txt_in_8e5": ("txt_in.in_layer.weight", None, 2e5),
+    "img_in_outliers": ("img_in.weight", (17, 400, 1033, 1999, 2048, 2900, 3511, 4000), 80.0),
+}
+
+
+def magnitude_overrides(wt, case):
+    """The replaced matrices of MAGNITUDE_CASES[case] (fp32, scaled exactly by a power-of-two-
+    free factor applied once in fp32)."""
+    name, rows, scale = MAGNITUDE_CASES[case]
+    m = np.array(wt(name), np.float32, copy=True)
+    if rows is None:
+        m *= np.float32(scale)
+    else:
+        m[list(rows)] *= np.float32(scale)
+    return {name: m}
+
+
 def euler(wt, ctx, latent, shape=Shape(), sigmas=TURBO_SIGMAS, ref=None, prefix_key="prompt",
           layers=None, on_step=None, w8a8=False):
     """The Turbo schedule's Euler loop: z <- z + (s' - s) v, (s' - s) as a

@@ -8,6 +8,7 @@ itself pinned against the reference's ref_dit.py vectors), cached:
     python tests/golden/make_dit_vectors.py full2      # dit_full_shapes_2blocks.npz (a few minutes)
     python tests/golden/make_dit_vectors.py cfg3       # dit_cfg3_8step.npz (hours)
     python tests/golden/make_dit_vectors.py cfg4       # dit_cfg4_edit_8step.npz (hours)
+    python tests/golden/make_dit_vectors.py mag        # dit_magnitudes_2blocks.npz (a few minutes)
 
 small: 32 blocks of the real shape, synthetic Q8_0 weights (seed 1), 32 text
 rows, an 8 x 8 latent: the velocity of each of the 8 Turbo steps (the first
@@ -20,6 +21,9 @@ cfg3: the 1536 x 1024 workload -- 6144 image rows (96 x 64), 256 text rows,
 cfg4: the edit workload -- a 64 x 64 image after 512 text rows with a 64 x 64
 reference picture after the first 8 of them (8704 keys), 32 blocks (seed 7) --
 the same 8 steps (the prefix, text and reference picture, kept after the first).
+mag: the 1024^2 workload's shapes, two blocks deep (seed 2, sigma 0.978453), with the
+weights of each of the oracle's MAGNITUDE_CASES (activations at real-checkpoint magnitudes):
+the velocity, as float16.
 """
 import os
 import sys
@@ -88,6 +92,21 @@ def full_shapes(out):
     print("wrote", out)
 
 
+def magnitudes(out):
+    seed, p, h, w, _, sigma = FULL_CASES["cfg2_1024sq"]
+    ctx, lat = xo.synth_inputs(seed, p, h, w)
+    arrays = {}
+    for case in xo.MAGNITUDE_CASES:
+        t0 = time.time()
+        base = xo.SynthWeights(seed, cache_bytes=0)
+        wt = xo.Overrides(base, xo.magnitude_overrides(base, case))
+        v = xo.forward(wt, ctx, lat, sigma, layers=2)
+        arrays[case] = v.astype(np.float16)
+        print("%s: |v| %.4f, %.0fs" % (case, float(np.sqrt((v * v).mean())), time.time() - t0), flush=True)
+    np.savez_compressed(os.path.join(HERE, out), **arrays)
+    print("wrote", out)
+
+
 if __name__ == "__main__":
     which = sys.argv[1] if len(sys.argv) > 1 else "small"
     if which == "small":
@@ -100,3 +119,5 @@ if __name__ == "__main__":
         run(6, 256, 96, 64, "dit_cfg3_8step.npz", half=True)
     elif which == "cfg4":
         run(7, 512, 64, 64, "dit_cfg4_edit_8step.npz", half=True, ref=(8, 64, 64))
+    elif which == "mag":
+        magnitudes("dit_magnitudes_2blocks.npz")

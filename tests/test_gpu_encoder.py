@@ -95,7 +95,10 @@ def test_set_from_gguf_records_equals_synth(ctx, enc2, owt2):
 
 
 def test_states_full_depth(ctx):
-    """All 36 blocks on 48 tokens against the oracle (its layers made as read)."""
+    """All 36 blocks on 48 tokens against the oracle (its layers made as read); then what the
+    encoder's distance does downstream: the DiT (2 blocks, an 8 x 8 latent) on the GPU's states
+    against the oracle's DiT on the oracle's states -- the whole prompt-to-velocity chain within
+    the DiT's per-block bar (relative L2 <= 1e-2), the GPU DiT on the oracle's states beside it."""
     say("encoder synth, 36 layers")
     e = X.load_encoder(seed=SEED, layers=36, vocab=VOCAB, ctx=ctx)
     try:
@@ -109,6 +112,21 @@ def test_states_full_depth(ctx):
     err = xo.rel_l2(got, want)
     say("36 layers rel l2", err)
     assert err < 3e-2 and np.isfinite(got).all()
+    dseed, hh, ww, sigma = 9, 8, 8, 0.95418
+    d = X.Dit(ctx, 2)
+    try:
+        d.synth(dseed)
+        d.check()
+        lat = xo.synth_inputs(dseed, 1, hh, ww)[1]
+        p = got.shape[0]
+        v_chain = X.dit_velocity(d, np.ascontiguousarray(got, np.float32), p, lat, hh, ww, sigma)
+        v_dit = X.dit_velocity(d, np.ascontiguousarray(want, np.float32), p, lat, hh, ww, sigma)
+    finally:
+        d.destroy()
+    ref = xo.forward(xo.SynthWeights(dseed), want.astype(np.float32), lat, sigma, layers=2)
+    e_chain, e_dit = xo.rel_l2(v_chain, ref), xo.rel_l2(v_dit, ref)
+    say("DiT velocity from the GPU encoder's states rel-L2 %.2e (from the oracle's states %.2e)" % (e_chain, e_dit))
+    assert e_chain < 1e-2 and e_dit < 1e-2
 
 
 def test_the_distance_is_the_rounding(enc2, owt2):

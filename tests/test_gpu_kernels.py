@@ -1,6 +1,7 @@
 """The HIP kernels against the oracle, through the C ABI (libexn-hip.so).
 Integer and byte work bit-exact; floating point to the tolerance written in
 each test.  Needs an MI355X."""
+import ctypes
 import math
 import sys
 
@@ -102,9 +103,10 @@ def test_repack_dequant_exhaustive(ctx):
 
 # --- the products -----------------------------------------------------------------------
 
-GEMM_CASES = [  # (M, N, K): ragged, the block shapes, proj_out's N = 64, img_in's K = 64, down's K = 12288
+GEMM_CASES = [  # (M, N, K): ragged, the block shapes, proj_out's N = 64, img_in's K = 64, down's K = 12288;
+    # from 512 rows the Q8_0 products take 512 x 128 tiles: ragged rows and a last half chunk of 128 rows
     (77, 96, 128), (256, 512, 4096), (300, 4096, 4096), (257, 64, 4096), (130, 4096, 12288), (64, 4096, 64),
-    (4352, 12288, 4096)]
+    (4352, 12288, 4096), (1100, 640, 4096), (513, 128, 128)]
 
 
 @pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])
@@ -583,3 +585,21 @@ def test_mm_w8a8_bit_exact(ctx, M, N, K):
     y16 = X.DevBuf(ctx, (M, N), np.uint16)
     X.call("exn_mm_w8a8", ctx.h, w.h, q.h, dd.h, M, y16.h, X.DT_F16)
     assert np.array_equal(y16.get(), want.astype(np.float16).view(np.uint16))
+
+
+def test_allocation_failure_is_a_status(ctx):
+    """exn_alloc of an absurd size (1 PiB) returns EXN_ENOMEM with a message naming the size,
+    raises nothing, and leaves the context usable: a buffer, an upload and a product after it."""
+    h = ctypes.c_void_p()
+    code = X.lib().exn_alloc(ctx.h, ctypes.c_size_t(1 << 50), ctypes.byref(h))
+    msg = X.lib().exn_last_error().decode()
+    say("exn_alloc(1 PiB): status %d, %s" % (code, msg))
+    assert code == X.ENOMEM and "hipMalloc" in msg and str(1 << 50) in msg and not h.value
+    rng = np.random.default_rng(21)
+    w = X.Weight.synth(ctx, 9, 403, 256, 512)
+    x = dev(ctx, rng.normal(0, 1, (64, 512)).astype(np.float32))
+    y = X.DevBuf(ctx, (64, 256), np.float32)
+    X.call("exn_mm", ctx.h, w.h, x.h, X.DT_F32, y.h, X.DT_F32, 64)
+    want = x.get() @ xo.dequant_q8_0(*xo.q8_0_synth(9, 403, 256, 512)).T
+    assert xo.rel_l2(y.get(), want) < 1e-2
+    w.free()

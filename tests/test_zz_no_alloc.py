@@ -1,8 +1,9 @@
 """exn_mm_noalloc: exn_mm's products with no device allocation (the bf16 staging of fp32
 rows in the library's static per-device scratch array), against exn_mm itself on the
 same inputs -- bit for bit: the same kernels on the same operands.  Two calls in a row,
-the second smaller, so that the second reads none of the first's stale staging.  Needs an
-MI355X."""
+the second smaller, so that the second reads none of the first's stale staging; and the call
+captured in a HIP graph on the context's stream, replayed.  Needs an MI355X."""
+import ctypes
 import sys
 
 import numpy as np
@@ -74,3 +75,48 @@ def test_noalloc_f32_matrix_and_limit(ctx):
         X.call("exn_mm_noalloc", ctx.h, w.h, x.h, X.DT_F32, y.h, X.DT_F32, big)
     assert e.value.code == X.EINVAL and "scratch" in str(e.value)
     w.free()
+
+
+def test_noalloc_under_graph_capture(ctx):
+    """After one call on the device (which takes the scratch address and sets the kernels'
+    attributes), exn_mm_noalloc captures into a HIP graph on the context's stream: the graph
+    replayed three times, with the program's own eager work and a synchronisation between the
+    replays, gives exn_mm's output bit for bit every time."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    for f in ("hipStreamCreate", "hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate",
+              "hipGraphLaunch", "hipStreamSynchronize", "hipGraphExecDestroy", "hipGraphDestroy",
+              "hipStreamDestroy"):
+        getattr(hip, f).restype = ctypes.c_int
+    s = vp()
+    assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+    N, K, n = 4096, 4096, 1024
+    w = X.Weight.synth(ctx, 9, 402, N, K)
+    rng = np.random.default_rng(14)
+    x = X.DevBuf.of(ctx, rng.normal(0, 1, (n, K)).astype(np.float32))
+    y = X.DevBuf(ctx, (n, N), np.uint16)
+    g, ge = vp(), vp()
+    try:
+        X.call("exn_set_stream", ctx.h, s)
+        want = _mm(ctx, "exn_mm", w, x, X.DT_F32, n, X.DT_BF16)
+        assert np.array_equal(_mm(ctx, "exn_mm_noalloc", w, x, X.DT_F32, n, X.DT_BF16), want)   # the warm call
+        assert hip.hipStreamBeginCapture(s, 0) == 0            # hipStreamCaptureModeGlobal
+        X.call("exn_mm_noalloc", ctx.h, w.h, x.h, X.DT_F32, y.h, X.DT_BF16, n)
+        assert hip.hipStreamEndCapture(s, ctypes.byref(g)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(ge), g, None, None, 0) == 0
+        for r in range(3):
+            y.upload(np.zeros((n, N), np.uint16))              # eager work between the replays
+            assert hip.hipGraphLaunch(ge, s) == 0
+            assert hip.hipStreamSynchronize(s) == 0
+            got = y.get()
+            say("replay %d: equal %s" % (r, np.array_equal(got, want)))
+            assert np.array_equal(got, want)
+    finally:
+        if ge.value:
+            hip.hipGraphExecDestroy(ge)
+        if g.value:
+            hip.hipGraphDestroy(g)
+        X.call("exn_set_stream", ctx.h, None)
+        hip.hipStreamSynchronize(s)
+        hip.hipStreamDestroy(s)
+        w.free()
