@@ -885,6 +885,10 @@ struct exn_dit {
   // the residual stream after each block, copied out when set (exn_dit_trace)
   float* trace = nullptr;
   int64_t trace_cap = 0;
+  // *dit-trace*'s numbers (exn_dit_stats): (layers + 1) x 4 records of the last velocity
+  bool stats_on = false;
+  uint32_t* stats = nullptr;   // the "stats" scratch buffer while a velocity with stats_on holds it
+  int64_t stats_records = 0;
   // per-launch event pairs by kernel class (exn_dit_profile)
   struct Rec {
     int cls;
@@ -1109,11 +1113,35 @@ int exn_dit_trace(exn_dit* d, float* buf, int64_t cap) {
   return EXN_OK;
 }
 
+int exn_dit_stats(exn_dit* d, int on) {
+  if (!d) FAIL(EXN_EINVAL, "null model");
+  d->stats_on = on != 0;
+  return EXN_OK;
+}
+
+int exn_dit_stats_read(exn_dit* d, float* maxabs, int64_t* nonfinite, int64_t records) {
+  if (!d || records < 0 || (records && (!maxabs || !nonfinite))) FAIL(EXN_EINVAL, "stats read arguments");
+  TRY(use(d->ctx));
+  if (!d->stats) FAIL(EXN_ESTATE, "no velocity has recorded its numbers since the last release (exn_dit_stats)");
+  const int64_t k = std::min(records, d->stats_records);
+  std::vector<uint32_t> h((size_t)(4 * d->stats_records));
+  HIPCHK(hipMemcpyAsync(h.data(), d->stats, h.size() * 4, hipMemcpyDeviceToHost, d->ctx->stream));
+  HIPCHK(hipStreamSynchronize(d->ctx->stream));
+  for (int64_t i = 0; i < k; ++i) {
+    uint32_t m = h[(size_t)(4 * i)];
+    memcpy(&maxabs[i], &m, 4);
+    nonfinite[i] = (int64_t)((uint64_t)h[(size_t)(4 * i + 2)] | ((uint64_t)h[(size_t)(4 * i + 3)] << 32));
+  }
+  return EXN_OK;
+}
+
 int exn_dit_release(exn_dit* d) {
   if (!d) FAIL(EXN_EINVAL, "null model");
   TRY(use(d->ctx));
   HIPCHK(hipStreamSynchronize(d->ctx->stream));
   dit_free_scratch(d);
+  d->stats = nullptr;
+  d->stats_records = 0;
   return EXN_OK;
 }
 
@@ -1520,6 +1548,19 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   TRY(dit_buf(d, "q", (size_t)(l * EXN_W) * 2, (void**)&q));
   TRY(dit_buf(d, "att", (size_t)(l * EXN_W) * 2, (void**)&att));
   TRY(dit_buf(d, "ff", (size_t)(l * EXN_F) * 2, (void**)&ff));
+  // *dit-trace*'s numbers (src/metal-dit.lisp:206-213,254-257) when exn_dit_stats is on: record
+  // 4 row + slot, row 0 before the blocks (slot 0 the stream, 3 txt_in's GELU rows), row 1 + l
+  // after block l (0 the stream, 1 the attention's output, 2 the MLP's inner rows)
+  uint32_t* st = nullptr;
+  if (d->stats_on) {
+    d->stats_records = (int64_t)(d->layers + 1) * 4;
+    TRY(dit_buf(d, "stats", (size_t)d->stats_records * 16, (void**)&st));
+    d->stats = st;
+    HIPCHK(tensor_stats_clear(s, st, d->stats_records));
+  }
+  auto stat = [&](int row, int slot, const void* t, int bf16, int64_t count) -> hipError_t {
+    return st ? tensor_stats(s, t, bf16, count, st + 4 * (4 * row + slot)) : hipSuccess;
+  };
   TRY(dit_buf(d, "tok", (size_t)((nimg > nref ? nimg : nref) * EXN_LAT) * 4, (void**)&tok));
   TRY(dit_buf(d, "vrows", (size_t)(nimg * EXN_LAT) * 4, (void**)&vrows));
   // split-K partials of the edge products with few tiles (proj_out's 64 columns, txt_in over few
@@ -1575,6 +1616,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
     TRY(dit_buf(d, "h1", (size_t)(ptext * EXN_W) * 4, (void**)&h1));
     HIPCHK(rms_norm(s, ptext, EXN_W, 1e-6f, context, d->text_norm, t1, 0));
     HIPCHK(edge_mm(2, t1, ptext, h1, 1));
+    HIPCHK(stat(0, 3, h1, 0, ptext * EXN_W));
     float* txt = x;
     if (edit) TRY(dit_buf(d, "txt", (size_t)(ptext * EXN_W) * 4, (void**)&txt));
     HIPCHK(edge_mm(3, h1, ptext, txt, 0));
@@ -1603,6 +1645,7 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
   const double ln_bytes = nd * Wd * (4 + 2), qkv_bytes = nd * 3 * Wd * 2 * 2 + nd * 128 * 4;
   if (d->trace && n * EXN_W <= d->trace_cap)
     HIPCHK(hipMemcpyAsync(d->trace, x, (size_t)(n * EXN_W) * 4, hipMemcpyDeviceToDevice, s));
+  HIPCHK(stat(0, 0, x, 0, n * EXN_W));
   float *a32 = nullptr, *h32 = nullptr, *gu32 = nullptr, *ff32 = nullptr;   // the int8 block's fp32 rows
   for (int il = 0; il < d->layers; ++il) {
     Layer& L = d->L[(size_t)il];
@@ -1655,6 +1698,9 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
         HIPCHK(gemm_w8a8(s, xq, xd, n, L.down->qs, L.down->d, EXN_W, EXN_F, h32, EXN_W, 0));
         HIPCHK(gate_add(s, n * EXN_W, EXN_W, n0, p, ms, x, h32, mod + 3 * EXN_W));
       }
+      HIPCHK(stat(il + 1, 0, x, 0, n * EXN_W));
+      HIPCHK(stat(il + 1, 1, a32, 0, n * EXN_W));
+      HIPCHK(stat(il + 1, 2, ff32, 0, n * EXN_F));
       if (d->trace && (int64_t)(il + 2) * n * EXN_W <= d->trace_cap)
         HIPCHK(hipMemcpyAsync(d->trace + (int64_t)(il + 1) * n * EXN_W, x, (size_t)(n * EXN_W) * 4,
                               hipMemcpyDeviceToDevice, s));
@@ -1734,6 +1780,9 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       ea.mstride = ms;
       HIPCHK(block_mm(s, L.down, ff, EXN_F, n, nh, EPI_GATE_ADD, ea, part));
     }
+    HIPCHK(stat(il + 1, 0, x, 0, n * EXN_W));
+    HIPCHK(stat(il + 1, 1, att, 1, n * EXN_W));
+    HIPCHK(stat(il + 1, 2, ff, 1, n * EXN_F));
     if (d->trace && (int64_t)(il + 2) * n * EXN_W <= d->trace_cap)
       HIPCHK(hipMemcpyAsync(d->trace + (int64_t)(il + 1) * n * EXN_W, x, (size_t)(n * EXN_W) * 4,
                             hipMemcpyDeviceToDevice, s));

@@ -338,4 +338,63 @@ hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float d
   return hipGetLastError();
 }
 
+// *dit-trace*'s numbers (src/metal-dit.lisp:119-124) for COUNT values of X (fp32, or bf16 when
+// BF16): the largest finite |x| into REC[0] (its bits: finite magnitudes order as unsigned
+// integers) and the count of values that are not finite added to REC[2..3] (a 64-bit count).
+// A grid of at most 1024 workgroups strides over X, 16 bytes a lane; one atomic of each kind
+// a wave.
+__global__ void __launch_bounds__(256)
+k_stats(const void* __restrict__ x, int bf16, int64_t count, uint32_t* __restrict__ rec) {
+  float mx = 0.f;
+  uint32_t bad = 0;
+  auto take = [&](float v) {
+    const bool fin = (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u;
+    mx = fin ? fmaxf(mx, fabsf(v)) : mx;
+    bad += fin ? 0u : 1u;
+  };
+  const int64_t per = bf16 ? 8 : 4;   // values a 16-byte load
+  const int64_t chunks = count / per, stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += stride) {
+    const u32x4 u = ((const u32x4*)x)[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (bf16) {
+        take(bf16_lo(u[e]));
+        take(bf16_hi(u[e]));
+      } else {
+        take(__uint_as_float(u[e]));
+      }
+    }
+  }
+  // the tail past whole 16-byte chunks, by the first threads
+  const int64_t t = chunks * per + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < count)
+    take(bf16 ? __uint_as_float((uint32_t)((const uint16_t*)x)[t] << 16) : ((const float*)x)[t]);
+  mx = wave_max(mx);
+  for (int o = 32; o >= 1; o >>= 1) bad += __shfl_xor(bad, o, 64);
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(rec, __float_as_uint(mx));
+    if (bad) atomicAdd((unsigned long long*)(rec + 2), (unsigned long long)bad);
+  }
+}
+
+__global__ void k_stats_clear(uint32_t* __restrict__ rec, int64_t words) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < words) rec[i] = 0u;
+}
+
+hipError_t tensor_stats(hipStream_t s, const void* x, int bf16, int64_t count, uint32_t* rec) {
+  if (count <= 0) return hipSuccess;
+  const int64_t chunks = count / (bf16 ? 8 : 4);
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(1024, (chunks + 255) / 256));
+  hipLaunchKernelGGL(k_stats, dim3((unsigned)blocks), dim3(256), 0, s, x, bf16, count, rec);
+  return hipGetLastError();
+}
+
+hipError_t tensor_stats_clear(hipStream_t s, uint32_t* rec, int64_t records) {
+  if (records <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_stats_clear, dim3(grid_of(records * 4, 256)), dim3(256), 0, s, rec, records * 4);
+  return hipGetLastError();
+}
+
 }  // namespace exn

@@ -182,6 +182,10 @@ inline int64_t tile_q8_bytes(int64_t rows, int64_t cols) { return (rows + 255) /
 // QT from the SoA codes QS (N x K int8) and scales D (N x K/32 fp16); K % 64 == 0
 hipError_t tile_q8(hipStream_t s, const int8_t* qs, const uint16_t* d, int64_t N, int64_t K, uint8_t* qt);
 
+// A kernel's dynamic LDS limit raised to BYTES (hipFuncSetAttribute) once for each device it
+// launches on, the current one: thread-safe, and each device's kernels get their own attribute
+hipError_t ensure_lds(const void* kern, int bytes);
+
 // a weight matrix as a block product streams it: bf16 rows WB (N x K), or, when WB is null, Q8_0:
 // the tiled copy QT (the pipelined product's operand) and the SoA codes QS (N x K int8) and scales
 // QD (N x K/32 fp16) that the other kernels read
@@ -241,6 +245,11 @@ hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* 
 hipError_t latent_rows(hipStream_t s, const float* latent, int64_t nimg, float* rows);
 hipError_t rows_to_latent(hipStream_t s, const float* rows, int64_t nimg, float* latent);
 hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float ds);
+// the largest finite |x| and the count of values that are not finite of COUNT values of X (fp32,
+// or bf16 when BF16), folded into a 16-byte record REC = {max |x| bits, 0, 64-bit count};
+// tensor_stats_clear zeroes RECORDS of them
+hipError_t tensor_stats(hipStream_t s, const void* x, int bf16, int64_t count, uint32_t* rec);
+hipError_t tensor_stats_clear(hipStream_t s, uint32_t* rec, int64_t records);
 // W8A8 (w8a8.hip): activation rows to Q8_0, and the int8 product with per-block scales
 hipError_t quant_q8(hipStream_t s, const void* x, int xbf16, int64_t ldx, int64_t n, int64_t K, int8_t* q,
                     uint16_t* d);

@@ -216,11 +216,9 @@ static hipError_t launch(hipStream_t s, const uint16_t* x, int64_t lda, const in
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
   const size_t shm = 2 * (size_t)(BM + BN) * SA * sizeof(uint16_t);
   auto kern = k_gemm<BM, BN, WM, WN, WBF16, EPI>;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  {
+    const hipError_t e = ensure_lds((const void*)kern, (int)shm);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
   hipLaunchKernelGGL(kern, grid, dim3(NT), shm, s, x, lda, qs, d, wb, M, N, K, ea);
@@ -1059,11 +1057,9 @@ static hipError_t launch_bt(hipStream_t s, const uint16_t* x, int64_t lda, const
   const size_t shm = Q8 ? 2 * 65536 + 2 * 16384 : 2 * 65536;
   constexpr int NW = 8;
   auto kern = k_gemm_bt<EPI, NW, Q8>;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  {
+    const hipError_t e = ensure_lds((const void*)kern, (int)shm);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 255) / 256), (unsigned)split);
   hipLaunchKernelGGL(kern, grid, dim3(NW * 64), shm, s, x, lda, wb, qt, M, N, K, ea);
@@ -1087,11 +1083,9 @@ static hipError_t launch_tall(hipStream_t s, const uint16_t* x, int64_t lda, con
                               int64_t K, const EpiArgs& ea, int split) {
   const size_t shm = 2 * 81920;
   auto kern = k_gemm_q8_tall<EPI>;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  {
+    const hipError_t e = ensure_lds((const void*)kern, (int)shm);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 511) / 512), (unsigned)split);
   hipLaunchKernelGGL(kern, grid, dim3(512), shm, s, x, lda, qt, M, N, K, ea);

@@ -369,11 +369,9 @@ static hipError_t launch_conv1(hipStream_t s, const uint16_t* x, const uint16_t*
                                void* y, int h, int w, int c, int cout, int kp, int split = 1) {
   auto kern = k_conv<BN, TAPS, UP, OUT, GAM, NW>;
   typedef ConvTile<BN, NW> T;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS);
+  {
+    const hipError_t e = ensure_lds((const void*)kern, T::LDS);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   dim3 grid(grid_of((int64_t)h * w, T::TM), grid_of(cout, BN), split);
   hipLaunchKernelGGL(kern, grid, dim3(NW * 64), T::LDS, s, x, wt, bias, ep, y, h, w, c, cout, kp);

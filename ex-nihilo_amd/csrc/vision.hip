@@ -284,12 +284,9 @@ template <int RM, int RN, int ACT>
 static hipError_t vis_gemm_t(hipStream_t s, const float* x, const float* w, const float* bias, const float* r, float* y,
                              int M, int N, int K) {
   constexpr int lds = 2 * (32 * RM + 32 * RN) * 128;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_vis_gemm<RM, RN, ACT>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  {
+    const hipError_t e = ensure_lds((const void*)k_vis_gemm<RM, RN, ACT>, lds);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   dim3 grid(vgrid(N, 32 * RN), vgrid(M, 32 * RM));
   hipLaunchKernelGGL((k_vis_gemm<RM, RN, ACT>), grid, dim3(256), lds, s, x, w, bias, r, y, M, N, K);
@@ -529,12 +526,9 @@ k_vis_attend(int n, int D, const float* __restrict__ q, const float* __restrict_
 hipError_t vis_attend(hipStream_t s, int n, int heads, const float* q, const float* k, const float* vt, float* att) {
   if (n <= 0) return hipSuccess;
   if (n % 4 || (int64_t)n * 288 >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_vis_attend, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       2 * VA_STAGE);
+  {
+    const hipError_t e = ensure_lds((const void*)k_vis_attend, 2 * VA_STAGE);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   hipLaunchKernelGGL(k_vis_attend, dim3(vgrid(n, 128), heads), dim3(256), 2 * VA_STAGE, s, n, heads * 72, q, k, vt,
                      att);

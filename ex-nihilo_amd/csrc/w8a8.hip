@@ -356,15 +356,10 @@ hipError_t gemm_w8a8(hipStream_t s, const int8_t* xq, const uint16_t* xd, int64_
                       N * K < ((int64_t)1 << 31);
   if (dma_ok) {
     const size_t shm = W8_NS * 17408;
-    static bool attr = false;
-    if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)k_gemm_w8a8_dma<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)shm);
-      if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)k_gemm_w8a8_dma<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)shm);
+    {
+      const hipError_t e = ensure_lds(f16out ? (const void*)k_gemm_w8a8_dma<true> : (const void*)k_gemm_w8a8_dma<false>,
+                                      (int)shm);
       if (e != hipSuccess) return e;
-      attr = true;
     }
     if (f16out)
       hipLaunchKernelGGL(k_gemm_w8a8_dma<true>, grid, dim3(256), shm, s, xq, xd, wq, wd, M, N, K, y, ldy);

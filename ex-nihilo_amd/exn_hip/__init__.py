@@ -133,6 +133,8 @@ SIGNATURES = {
     "exn_vis_gemm": (c_int, [vp, vp, vp, vp, vp, vp, c_int64, c_int64, c_int64, c_int]),
     "exn_vis_attend": (c_int, [vp, c_int, c_int, vp, vp, vp, vp]),
     "exn_vis_ln": (c_int, [vp, c_int64, c_int, vp, vp, vp, vp]),
+    "exn_dit_stats": (c_int, [vp, c_int]),
+    "exn_dit_stats_read": (c_int, [vp, vp, vp, c_int64]),
     "exn_enc_create": (c_int, [vp, c_int, c_double, POINTER(vp)]),
     "exn_enc_set": (c_int, [vp, c_char_p, c_int, vp, c_int64, c_int64]),
     "exn_enc_synth": (c_int, [vp, c_uint64, c_int64]),
@@ -371,6 +373,26 @@ class Dit:
             call("exn_dit_profile_read", self.h, i, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(f), ctypes.byref(b))
             out[name] = (ms.value, n.value, f.value, b.value)
         return out
+
+    def profile_top(self, k=6):
+        """EXN_PROFILE's report (src/tenant.lisp:53-62): the K classes with the most GPU time,
+        [(class, ms)] largest first, and the total ms."""
+        rows = sorted(((c, v[0]) for c, v in self.profile_read().items() if v[1]), key=lambda r: -r[1])
+        return rows[:k], sum(r[1] for r in rows)
+
+    STATS_SLOTS = ("x", "att", "ff", "txt")
+
+    def stats(self, on: bool = True):
+        """*dit-trace*'s numbers (exn_dit_stats) for every velocity while on."""
+        call("exn_dit_stats", self.h, 1 if on else 0)
+
+    def stats_read(self):
+        """The last velocity's (max finite |x|, values not finite), each (layers + 1) x 4: row 0
+        before the blocks, row 1 + l after block l; columns STATS_SLOTS."""
+        k = (self.layers + 1) * 4
+        mx, bad = np.zeros(k, np.float32), np.zeros(k, np.int64)
+        call("exn_dit_stats_read", self.h, ptr(mx), ptr(bad), k)
+        return mx.reshape(-1, 4), bad.reshape(-1, 4)
 
     def release(self):
         call("exn_dit_release", self.h)

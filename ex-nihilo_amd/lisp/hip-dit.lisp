@@ -31,12 +31,31 @@
 (sb-alien:define-alien-routine ("exn_dit_release" %exn-dit-release) sb-alien:int (d sb-sys:system-area-pointer))
 (sb-alien:define-alien-routine ("exn_dit_w8a8" %exn-dit-w8a8) sb-alien:int
   (d sb-sys:system-area-pointer) (on sb-alien:int))
+(sb-alien:define-alien-routine ("exn_dit_profile" %exn-dit-profile) sb-alien:int
+  (d sb-sys:system-area-pointer) (on sb-alien:int))
+(sb-alien:define-alien-routine ("exn_dit_profile_read" %exn-dit-profile-read) sb-alien:int
+  (d sb-sys:system-area-pointer) (cls sb-alien:int) (ms sb-sys:system-area-pointer)
+  (launches sb-sys:system-area-pointer) (flops sb-sys:system-area-pointer) (bytes sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_dit_stats" %exn-dit-stats) sb-alien:int
+  (d sb-sys:system-area-pointer) (on sb-alien:int))
+(sb-alien:define-alien-routine ("exn_dit_stats_read" %exn-dit-stats-read) sb-alien:int
+  (d sb-sys:system-area-pointer) (maxabs sb-sys:system-area-pointer) (nonfinite sb-sys:system-area-pointer)
+  (records (sb-alien:signed 64)))
 
 (defvar *int8* nil
   "cuda-dit.lisp's switch (src/cuda-dit.lisp:110-113): true takes every Q8_0 product of 16 rows
    or more as int8 activations (quant_q8 by blocks of 32, the int8 MFMA) -- the CUDA backend's
    default numerics; false (here the default: several times faster on the MI355X, and nearer the
    float reference) multiplies bf16 activations by the exact bf16 dequantisation.")
+
+(defvar *dit-trace* nil
+  "metal-dit.lisp's switch (src/metal-dit.lisp:114-117): when true, each velocity's largest
+   values -- before the blocks the stream and txt_in's GELU rows, after each layer the stream,
+   the attention's output and the MLP's inner rows -- and their counts of values that are not
+   finite are printed after it: where a step first overflows.")
+
+(defparameter +exn-profile-classes+ #("qkv" "attend" "out" "gate_up" "down" "ln_mod" "qkv_prep" "edge")
+  "The library's kernel classes (EXN_PROF_* in exn_hip.h), in order.")
 
 (defconstant +exn-q8-0+ 8)
 (defconstant +exn-f32+ 0)
@@ -76,15 +95,50 @@
     (exn-check (%exn-dit-check (hdit-handle d)))
     d))
 
+(defun print-dit-trace (d)
+  "*dit-trace*'s lines for D's last velocity, in metal-dit.lisp's form (its trace-max, :119-124)."
+  (let* ((rows (1+ 32)) (mx (f32vec (* 4 rows)))
+         (bad (make-array (* 4 rows) :element-type '(signed-byte 64))))
+    (sb-sys:with-pinned-objects (mx bad)
+      (exn-check (%exn-dit-stats-read (hdit-handle d) (sb-sys:vector-sap mx) (sb-sys:vector-sap bad) (* 4 rows))))
+    (flet ((one (name i)
+             (format *error-output* " ~A ~,1F~:[~; (~D not finite)~]" name (aref mx i) (plusp (aref bad i)) (aref bad i))))
+      (format *error-output* "~&before:")
+      (one "x-all" 0)
+      (when (or (plusp (aref mx 3)) (plusp (aref bad 3))) (one "h" 3))
+      (terpri *error-output*)
+      (loop for il from 0 below 32
+            for r = (* 4 (1+ il))
+            do (format *error-output* "~&layer ~D:" il) (one "x" r) (one "att" (+ r 1)) (one "ff" (+ r 2))
+               (terpri *error-output*)))))
+
+(defun add-gpu-profile (d table)
+  "D's last velocity's GPU time by kernel class into TABLE (illatio's *gpu-profile*, seconds by
+   name, which tenant-run reports for the request under EXN_PROFILE, src/tenant.lisp:53-62)."
+  (let ((cell (make-array 4 :element-type 'double-float :initial-element 0d0))
+        (n (make-array 1 :element-type '(signed-byte 64) :initial-element 0)))
+    (sb-sys:with-pinned-objects (cell n)
+      (loop for cls from 0 below (length +exn-profile-classes+)
+            do (exn-check (%exn-dit-profile-read (hdit-handle d) cls (sb-sys:vector-sap cell) (sb-sys:vector-sap n)
+                                                 (sb-sys:sap+ (sb-sys:vector-sap cell) 8)
+                                                 (sb-sys:sap+ (sb-sys:vector-sap cell) 16)))
+               (when (plusp (aref n 0))
+                 (incf (gethash (format nil "exn:~A" (aref +exn-profile-classes+ cls)) table 0d0)
+                       (/ (aref cell 0) 1d3)))))))
+
 (defun dit-velocity (d context p latent h w sigma &key (prefix-key nil) ref)
   "cuda-dit.lisp's dit-velocity on the MI355X: the same arguments, the same result."
   (let ((v (f32vec (* 64 h w)))
+        (profile (and (uiop:getenv "EXN_PROFILE") (boundp 'il::*gpu-profile*)
+                      (hash-table-p (symbol-value 'il::*gpu-profile*)) (symbol-value 'il::*gpu-profile*)))
         (key (if prefix-key
                  (or (gethash prefix-key (hdit-keys d))
                      (setf (gethash prefix-key (hdit-keys d)) (1+ (hash-table-count (hdit-keys d)))))
                  0))
         (ref-latent (and ref (second ref))))
     (exn-check (%exn-dit-w8a8 (hdit-handle d) (if *int8* 1 0)))
+    (exn-check (%exn-dit-stats (hdit-handle d) (if *dit-trace* 1 0)))
+    (exn-check (%exn-dit-profile (hdit-handle d) (if profile -1 0)))
     (sb-sys:with-pinned-objects (context latent v ref-latent)
       (exn-check (%exn-dit-velocity (hdit-handle d) (sb-sys:vector-sap context) p (sb-sys:vector-sap latent) h w
                                     (coerce sigma 'double-float) key
@@ -92,6 +146,10 @@
                                     (if ref (sb-sys:vector-sap ref-latent) (sb-sys:int-sap 0))
                                     (if ref (third ref) 0) (if ref (fourth ref) 0)
                                     (sb-sys:vector-sap v))))
+    (when profile
+      (add-gpu-profile d profile)
+      (exn-check (%exn-dit-profile (hdit-handle d) 0)))
+    (when *dit-trace* (print-dit-trace d))
     v))
 
 (defun dit-release (d)

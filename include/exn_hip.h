@@ -219,6 +219,16 @@ int exn_dit_generate_dev(exn_dit* d, const float* context, int p, float* z, int 
  * BUF and after block i to BUF + (i + 1) * n * 4096, as far as CAP floats reach;
  * NULL turns it off */
 int exn_dit_trace(exn_dit* d, float* buf, int64_t cap);
+/* *dit-trace*'s numbers (src/metal-dit.lisp:114-124,206-213,254-257): while ON, each velocity
+ * records the largest finite |x| and the count of values that are not finite of, before the
+ * blocks, the residual stream entering them (record 0) and, in an uncached pass, txt_in's GELU
+ * rows (record 3); after block l, the stream (record 4 (l + 1)), the attention's output (+1)
+ * and the MLP's inner rows, SwiGLU's output (+2; the gate_up product's own rows are never
+ * stored).  exn_dit_stats_read copies the last velocity's first RECORDS of the (layers + 1) x 4
+ * records (a slot with nothing recorded reads 0, 0) into MAXABS and NONFINITE; EXN_ESTATE when
+ * none was recorded since the model's last release */
+int exn_dit_stats(exn_dit* d, int on);
+int exn_dit_stats_read(exn_dit* d, float* maxabs, int64_t* nonfinite, int64_t records);
 /* EXN_PROFILE's per-kernel GPU time (src/tenant.lisp:53-62), on the context's stream:
  * exn_dit_profile(d, ON) clears and starts recording a HIP event pair around every
  * launch of the step of the kernel classes in the bit mask ON (1 << EXN_PROF_...; -1

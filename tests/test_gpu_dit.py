@@ -464,3 +464,36 @@ def test_w8a8_mode(ctx):
     d.w8a8(False)
     assert np.array_equal(X.dit_velocity(d, ctxa, p, lat, h, w, 0.7), v_bf)
     d.destroy()
+
+
+def test_stats_count_a_planted_nan_at_its_block(ctx):
+    """*dit-trace*'s numbers (exn_dit_stats): with every value finite they are the largest |x| of
+    the stream, the attention's output and the MLP's rows after each block (against the trace's
+    copy of the stream), and none is counted not finite; a NaN planted in block 1's norm_q
+    weights reaches block 1's attention and stream -- counted there, not at block 0 -- and
+    every block after it."""
+    seed, p, h, w = 17, 24, 8, 8
+    say("stats: 3 blocks, a NaN in block 1's norm_q")
+    d = model(ctx, 3, seed)
+    ctxa, lat = xo.synth_inputs(seed, p, h, w)
+    n = p + h * w
+    tr = _trace(ctx, d, n)
+    d.stats(True)
+    X.dit_velocity(d, ctxa, p, lat, h, w, 0.8)
+    X.call("exn_dit_trace", d.h, None, 0)
+    mx, bad = d.stats_read()
+    xs = tr.get()
+    say("finite: stream max |x| by block", np.round(mx[:, 0], 2), "att", np.round(mx[1:, 1], 2), "ff", np.round(mx[1:, 2], 2))
+    assert (bad == 0).all() and (mx[1:, :3] > 0).all() and mx[0, 3] > 0
+    for i in range(4):   # the stream's maximum is the trace's, exactly
+        assert mx[i, 0] == np.float32(np.abs(xs[i]).max())
+    nq = xo.synth_vector(seed, "transformer_blocks.1.attn.norm_q.weight", 128).astype(np.float32)
+    nq[5] = np.nan
+    d.set("transformer_blocks.1.attn.norm_q.weight", X.F32, nq, (128,))
+    X.dit_velocity(d, ctxa, p, lat, h, w, 0.8)
+    mx, bad = d.stats_read()
+    say("NaN in block 1: values not finite, rows before, blocks 0..2 (x att ff):", bad[:, :3].tolist())
+    assert (bad[0] == 0).all() and (bad[1] == 0).all()
+    assert bad[2, 1] > 0 and bad[2, 0] > 0 and bad[3, 0] > 0
+    d.stats(False)
+    d.destroy()

@@ -127,3 +127,28 @@ def test_the_header_parse_sees_the_trio():
 def test_files_parse_and_stay_in_the_package(name):
     fs = forms(name)
     assert fs[0] == ["in-package", "#:ex-nihilo"]
+
+
+def flatten(form):
+    if isinstance(form, list):
+        for f in form:
+            yield from flatten(f)
+    else:
+        yield form
+
+
+def test_diagnostics_mirror_the_reference():
+    """dit-velocity turns the library's numbers on as the reference's switches ask: *dit-trace*
+    (src/metal-dit.lisp:114-117, printed per layer as its trace-max prints) through exn_dit_stats,
+    and EXN_PROFILE (src/tenant.lisp:53-62) through exn_dit_profile, its classes' seconds added
+    to illatio's *gpu-profile* table that tenant-run reports."""
+    fs = {f[1]: f for f in forms("hip-dit.lisp") if isinstance(f, list) and len(f) > 1 and f[0] in ("defun", "defvar")}
+    assert "*dit-trace*" in fs
+    vel = list(flatten(fs["dit-velocity"]))
+    for atom in ('"EXN_PROFILE"', "il::*gpu-profile*", "%exn-dit-stats", "%exn-dit-profile", "*dit-trace*",
+                 "print-dit-trace", "add-gpu-profile"):
+        assert atom in vel or "'" + atom in vel, atom
+    trace = list(flatten(fs["print-dit-trace"]))
+    assert "%exn-dit-stats-read" in trace and '"x"' in trace and '"att"' in trace and '"ff"' in trace
+    prof = list(flatten(fs["add-gpu-profile"]))
+    assert "%exn-dit-profile-read" in prof and "gethash" in prof
