@@ -1,12 +1,16 @@
 ;;;; hip-encoder.lisp -- the prompt encoder's text model on an AMD MI355X through libexn-hip.so
 ;;;;
-;;;; load-encoder, encode-prompt and encoder-states of src/encoder.lisp (:41, :55, :143) with the
-;;;; reference's lambda lists, for a GPU encoder: the text model's forward runs in libexn-hip.so
-;;;; (exn_enc_*) in place of illatio's il::cuda-forward-n; tokenizing stays illatio's
-;;;; (il::tokenize on the GGUF's vocabulary).  An edit prompt's picture rows go to the forward as
-;;;; arguments instead of through il::*after-embed* / il::*after-layer* (call-with-picture-rows,
-;;;; :69-110).  Loads after hip-dit.lisp and hip-vision.lisp, whose shared object, status check,
-;;;; %exn-open and vision-encode it uses; listed in ex-nihilo.asd after them.
+;;;; Loaded after src/encoder.lisp, it redefines only the text model's compute -- load-encoder
+;;;; (:41), encoder-gpu-p (:50), call-with-picture-rows (:69) and encoder-states (:143), with
+;;;; the reference's lambda lists -- so that encoder.lisp's own encode-prompt and
+;;;; encode-edit-prompt (:55-141: the ids, the edit prompt's positions and mrope-table, the
+;;;; system turn and the picture's rows left out) run unchanged over the library's forward
+;;;; (exn_enc_*) in place of illatio's il::cuda-forward-n.  The model encode-prompt receives is
+;;;; still illatio's (il::load-model: the vocabulary for il::tokenize, the width and rotary
+;;;; settings it reads); the library's encoder for it is found in *hip-encoders*.  The picture's
+;;;; rows go to the forward as arguments instead of through il::*after-embed* /
+;;;; il::*after-layer*.  Loads after hip-dit.lisp and hip-vision.lisp, whose shared object,
+;;;; status check and %exn-open it uses; listed in ex-nihilo.asd after them and encoder.lisp.
 
 (in-package #:ex-nihilo)
 
@@ -20,14 +24,34 @@
   (e sb-sys:system-area-pointer) (ids sb-sys:system-area-pointer) (n sb-alien:int) (pos sb-sys:system-area-pointer)
   (pic0 sb-alien:int) (m sb-alien:int) (merged sb-sys:system-area-pointer) (deep sb-sys:system-area-pointer)
   (out sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_enc_states_dev" %exn-enc-states-dev) sb-alien:int
+  (e sb-sys:system-area-pointer) (ids sb-sys:system-area-pointer) (n sb-alien:int) (cs sb-sys:system-area-pointer)
+  (pic0 sb-alien:int) (m sb-alien:int) (merged sb-sys:system-area-pointer) (deep sb-sys:system-area-pointer)
+  (out sb-sys:system-area-pointer))
 (sb-alien:define-alien-routine ("exn_enc_release" %exn-enc-release) sb-alien:int (e sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_alloc" %exn-alloc) sb-alien:int
+  (ctx sb-sys:system-area-pointer) (bytes (sb-alien:unsigned 64)) (out sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_free" %exn-free) sb-alien:int
+  (ctx sb-sys:system-area-pointer) (p sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_upload" %exn-upload) sb-alien:int
+  (ctx sb-sys:system-area-pointer) (dst sb-sys:system-area-pointer) (src sb-sys:system-area-pointer)
+  (bytes (sb-alien:unsigned 64)))
+(sb-alien:define-alien-routine ("exn_download" %exn-download) sb-alien:int
+  (ctx sb-sys:system-area-pointer) (dst sb-sys:system-area-pointer) (src sb-sys:system-area-pointer)
+  (bytes (sb-alien:unsigned 64)))
 
-(defstruct (hencoder (:constructor %make-hencoder)) handle tokenizer)
+(defvar *hip-encoders* (make-hash-table :test 'eq :weakness :key)
+  "illatio's model (what load-encoder returns) -> (context . exn_enc handle) of its text model
+   on the GPU.")
+
+(defvar *hip-picture* nil
+  "Inside call-with-picture-rows: (merged deep rows-in), the picture's rows for the forward.")
 
 (defun load-encoder (path &key device (threads (il::default-thread-count)))
   "The prompt encoder in the qwen3vl GGUF at PATH: its text model on HIP device DEVICE (0 when
-   NIL), every block's matrices as the file's Q8_0 records, its norms as floats; the
-   vocabulary through illatio for il::tokenize."
+   NIL), every block's matrices as the file's Q8_0 records, its norms as floats.  Returns
+   illatio's model of the file (the vocabulary, the widths and rotary settings encoder.lisp
+   reads), the library's encoder recorded for it."
   (let* ((g (read-gguf path)) (file (il::map-file-vector path))
          (ctx (exn-out-pointer #'%exn-open (or device 0)))
          (e (exn-out-pointer #'%exn-enc-create ctx 36 (coerce (meta g "qwen3vl.rope.freq_base") 'double-float))))
@@ -43,55 +67,75 @@
                                                     (+ (il::gguf-data-offset g) (il::tensor-info-offset ti)))
                                        (first dims) (reduce #'* (rest dims))))))))
     (exn-check (%exn-enc-check e))
-    (%make-hencoder :handle e :tokenizer (il::load-model path :threads threads))))
+    (let ((model (il::load-model path :threads threads)))
+      (setf (gethash model *hip-encoders*) (cons ctx e))
+      model)))
 
-(defun encoder-states (model ids &key positions picture)
-  "Every token's state after the text model's last block, before its final norm: (length IDS)
-   x 4096 floats.  POSITIONS: a (t h w) list a token (text positions 0 .. when NIL); PICTURE:
-   (a0 merged deep m), the vision tower's rows for tokens a0 .. a0 + m - 1."
-  (let* ((n (length ids))
-         (iv (make-array n :element-type '(signed-byte 32) :initial-contents (coerce ids 'list)))
-         (pv (and positions (make-array (* 3 n) :element-type '(signed-byte 32)
-                                                :initial-contents (apply #'append positions))))
-         (out (f32vec (* n 4096)))
-         (merged (and picture (second picture)))
-         (deep (and picture (apply #'concatenate '(simple-array single-float (*)) (third picture)))))
-    (sb-sys:with-pinned-objects (iv pv out merged deep)
-      (exn-check (%exn-enc-states (hencoder-handle model) (sb-sys:vector-sap iv) n
-                                  (if pv (sb-sys:vector-sap pv) (sb-sys:int-sap 0))
-                                  (if picture (first picture) 0) (if picture (fourth picture) 0)
-                                  (if merged (sb-sys:vector-sap merged) (sb-sys:int-sap 0))
-                                  (if deep (sb-sys:vector-sap deep) (sb-sys:int-sap 0))
-                                  (sb-sys:vector-sap out))))
-    out))
+(defun encoder-gpu-p (model)
+  "Whether MODEL, the prompt encoder, runs on a GPU: here, whether load-encoder made it."
+  (and (gethash model *hip-encoders*) t))
 
-(defun encode-prompt (model prompt &key vision picture)
-  "encoder.lisp's encode-prompt with the text model on the MI355X: (values states p a)."
-  (let* ((tk (hencoder-tokenizer model))
-         (skip (length (il::tokenize tk +system-turn+ :add-bos nil))))
-    (if (null picture)
-        (let* ((ids (il::tokenize tk (prompt-text prompt) :add-bos nil)) (n (length ids)))
-          (values (subseq (encoder-states model ids) (* skip 4096)) (- n skip) 0))
-        (destructuring-bind (px h w) picture
-          (multiple-value-bind (before after) (edit-prompt-pieces prompt)
-            (let* ((b (il::tokenize tk before :add-bos nil)) (e (il::tokenize tk after :add-bos nil))
-                   (gh (floor h 32)) (gw (floor w 32)) (m (* gh gw)) (a0 (length b))
-                   (ids (concatenate 'vector b (make-array m :initial-element +image-pad+) e))
-                   (n (length ids))
-                   (positions (append (loop for i below a0 collect (list i i i))
-                                      (loop for r below gh
-                                            append (loop for c below gw collect (list a0 (+ a0 r) (+ a0 c))))
-                                      (loop with p0 = (+ a0 (max gh gw)) for i below (length e)
-                                            collect (list (+ p0 i) (+ p0 i) (+ p0 i))))))
-              (multiple-value-bind (merged deep) (vision-encode vision px h w)
-                (let ((all (encoder-states model ids :positions positions :picture (list a0 merged deep m)))
-                      (out (f32vec (* (- n skip m) 4096))))
-                  ;; the text's states, the system turn and the picture's rows left out
-                  (replace out all :start2 (* skip 4096) :end2 (* a0 4096))
-                  (replace out all :start1 (* (- a0 skip) 4096) :start2 (* (+ a0 m) 4096))
-                  (vision-release vision)
-                  (values out (- n skip m) (- a0 skip))))))))))
+(defun call-with-picture-rows (model merged deep d rows-in fn)
+  "FN called with the encoder's forward taking a picture's rows: MERGED's (the vision tower's)
+   in place of the image pads after the embedding, DEEP's (a list of three) added after the first
+   layers.  ROWS-IN: of a pass's first position and count, (values its first picture row, the
+   picture's row there, how many), or NIL."
+  (declare (ignore model d))
+  (let ((*hip-picture* (list merged deep rows-in)))
+    (funcall fn)))
+
+(defun rope-cs (rope n)
+  "illatio's rope rows (a position's 64 cosines, then its 64 sines) as the library's table: the
+   cosine and sine of pair j at 2j and 2j + 1."
+  (let ((cs (f32vec (* n 128))))
+    (dotimes (s n cs)
+      (dotimes (j 64)
+        (setf (aref cs (+ (* s 128) (* 2 j))) (aref rope (+ (* s 128) j))
+              (aref cs (+ (* s 128) (* 2 j) 1)) (aref rope (+ (* s 128) 64 j)))))))
+
+(defun call-on-device (ctx arrays fn)
+  "FN called with a device copy of each of ARRAYS (specialised vectors, or NIL for a null
+   pointer); the copies freed after."
+  (let ((saps '()))
+    (unwind-protect
+         (progn
+           (dolist (a arrays)
+             (if (null a)
+                 (push (sb-sys:int-sap 0) saps)
+                 (let ((bytes (max 4 (* 4 (length a)))))
+                   (push (exn-out-pointer #'%exn-alloc ctx bytes) saps)
+                   (sb-sys:with-pinned-objects (a)
+                     (exn-check (%exn-upload ctx (first saps) (sb-sys:vector-sap a) (* 4 (length a))))))))
+           (apply fn (reverse saps)))
+      (dolist (p saps)
+        (unless (zerop (sb-sys:sap-int p)) (%exn-free ctx p))))))
+
+(defun encoder-states (model ids &key rope)
+  "Every token's state after the text model's last block, before its final norm: (length IDS) x
+   4096 floats.  ROPE: rope rows for the positions (mrope-table's, an edit prompt's), else text
+   positions; inside call-with-picture-rows the picture's rows too."
+  (destructuring-bind (ctx . e) (or (gethash model *hip-encoders*) (error "not a GPU encoder: ~A" model))
+    (let* ((n (length ids))
+           (iv (make-array n :element-type '(signed-byte 32) :initial-contents (coerce ids 'list)))
+           (out (f32vec (* n 4096))))
+      (multiple-value-bind (pic0 from m) (and *hip-picture* (funcall (third *hip-picture*) 0 n))
+        (let* ((merged (and pic0 (subseq (first *hip-picture*) (* from 4096) (* (+ from m) 4096))))
+               (deep (and pic0 (apply #'concatenate '(simple-array single-float (*))
+                                      (mapcar (lambda (s) (subseq s (* from 4096) (* (+ from m) 4096)))
+                                              (second *hip-picture*))))))
+          (if (null rope)
+              (sb-sys:with-pinned-objects (iv out merged deep)
+                (exn-check (%exn-enc-states e (sb-sys:vector-sap iv) n (sb-sys:int-sap 0) (or pic0 0) (if pic0 m 0)
+                                            (if merged (sb-sys:vector-sap merged) (sb-sys:int-sap 0))
+                                            (if deep (sb-sys:vector-sap deep) (sb-sys:int-sap 0))
+                                            (sb-sys:vector-sap out))))
+              (call-on-device ctx (list iv (rope-cs rope n) merged deep out)
+                              (lambda (di dcs dm dd dout)
+                                (exn-check (%exn-enc-states-dev e di n dcs (or pic0 0) (if pic0 m 0) dm dd dout))
+                                (sb-sys:with-pinned-objects (out)
+                                  (exn-check (%exn-download ctx (sb-sys:vector-sap out) dout (* 4 n 4096)))))))))
+      out)))
 
 (defun encoder-release (model)
   "MODEL's scratch freed (the weights stay)."
-  (exn-check (%exn-enc-release (hencoder-handle model))))
+  (exn-check (%exn-enc-release (cdr (gethash model *hip-encoders*)))))

@@ -4,7 +4,7 @@ SBCL (neither this image nor the GPU host has it): every define-alien-routine na
 that include/exn_hip.h declares, with its arity and, argument by argument, a Lisp alien type
 that passes the C type (int, 64-bit integers, double, pointers, C strings); and the backend trio
 keeps the reference's lambda lists (src/cuda-dit.lisp:52,137,99; src/cuda-vae.lisp:15,94,138,28;
-src/cuda-vision.lisp:15,34,103; src/encoder.lisp:41,55)."""
+src/cuda-vision.lisp:15,34,103; src/encoder.lisp:41,50,69,143)."""
 import os
 import re
 
@@ -113,7 +113,12 @@ def test_the_trio_keeps_the_reference_lambda_lists():
     assert defs["vision-encode"] == ["v", "px", "h", "w"]
     assert defs["vision-release"] == ["v"]
     assert defs["load-encoder"] == ["path", "&key", "device", ["threads", ["il::default-thread-count"]]]
-    assert defs["encode-prompt"] == ["model", "prompt", "&key", "vision", "picture"]
+    # the encoder's compute only (src/encoder.lisp:50,69,143); encode-prompt and encode-edit-prompt
+    # stay the reference's own (:55-141), which load before and call these
+    assert defs["encoder-gpu-p"] == ["model"]
+    assert defs["call-with-picture-rows"] == ["model", "merged", "deep", "d", "rows-in", "fn"]
+    assert defs["encoder-states"] == ["model", "ids", "&key", "rope"]
+    assert "encode-prompt" not in defs and "encode-edit-prompt" not in defs
 
 
 def test_the_header_parse_sees_the_trio():
