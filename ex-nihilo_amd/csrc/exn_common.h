@@ -134,7 +134,7 @@ void set_error(const char* fmt, ...);
 #define EXN_LAT 64
 #define EXN_FREQ 256
 
-// --- kernel launchers (defined in the .hip files, called by api.hip) -----------
+// --- kernel launchers (defined in the .hip files, called by the api*.hip entry points) -----------
 
 namespace exn {
 
