@@ -34,6 +34,15 @@ WOp wop(const exn_w* w) {
   return WOp{nullptr, nullptr, nullptr, nullptr};
 }
 
+// the operand of a product over N rows: a Q8_0 matrix's product of at most 256 rows in the few-row
+// kernel's shapes streams the tiled codes even where a resident bf16 expansion exists -- the same
+// B operands and the same sums bit for bit, from half the bytes, which is faster there; else wop
+WOp wop_n(const exn_w* w, int64_t n) {
+  if (n <= 256 && w->kind == EXN_Q8_0 && !w->dense && w->qt && w->cols % 256 == 0 && w->rows % (n > 128 ? 128 : 256) == 0)
+    return WOp{nullptr, w->qs, w->d, w->qt};
+  return wop(w);
+}
+
 int dev_alloc(void** p, size_t bytes) {
   *p = nullptr;
   if (bytes == 0) bytes = 256;
@@ -216,8 +225,9 @@ static int check_gemm(const exn_w* w, int64_t n) {
 hipError_t gemm_any(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t lda, int64_t n, Epi epi,
                            const EpiArgs& ea) {
   if (n == 0) return hipSuccess;
-  if (const uint16_t* b = wbf(w)) return gemm_wbf16(s, x, lda, b, n, w->rows, w->cols, epi, ea);
-  if (w->kind == EXN_Q8_0) return gemm_q8(s, x, lda, wop(w), n, w->rows, w->cols, epi, ea);
+  const WOp o = wop_n(w, n);
+  if (o.wb) return gemm_wbf16(s, x, lda, o.wb, n, w->rows, w->cols, epi, ea);
+  if (w->kind == EXN_Q8_0) return gemm_q8(s, x, lda, o, n, w->rows, w->cols, epi, ea);
   return hipErrorInvalidValue;
 }
 
@@ -244,7 +254,7 @@ static hipError_t rows_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int6
     hipError_t r = gemm_any(s, w, x, lda, n1, epi, ea);
     if (r != hipSuccess) return r;
     const EpiArgs eb = rows_on(ea, epi, n1);
-    r = gemm_split_rows(s, x + n1 * lda, lda, wop(w), n - n1, w->rows, w->cols, epi, eb, part, kSplitCap);
+    r = gemm_split_rows(s, x + n1 * lda, lda, wop_n(w, n - n1), n - n1, w->rows, w->cols, epi, eb, part, kSplitCap);
     if (r != hipErrorNotSupported) return r;
     return gemm_any(s, w, x + n1 * lda, lda, n - n1, epi, eb);
   }
@@ -263,7 +273,7 @@ hipError_t block_mm(hipStream_t s, const exn_w* w, const uint16_t* x, int64_t ld
   if (nh > 0 && nh < n) {
     hipError_t r = hipErrorNotSupported;
     if (nh <= 1024 && part && w->kind != EXN_F32)
-      r = gemm_split_rows(s, x, lda, wop(w), nh, w->rows, w->cols, epi, ea, part, kSplitCap);
+      r = gemm_split_rows(s, x, lda, wop_n(w, nh), nh, w->rows, w->cols, epi, ea, part, kSplitCap);
     if (r == hipErrorNotSupported) r = rows_mm(s, w, x, lda, nh, epi, ea, part);
     if (r != hipSuccess) return r;
     return rows_mm(s, w, x + nh * lda, lda, n - nh, epi, rows_on(ea, epi, nh), part);

@@ -900,36 +900,57 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
     }
     // the QKV product with qk-norm, RoPE and the K/V^T stores in its epilogue (bf16 or Q8_0
     // weights), else (shapes the fused path does not take) the product to fp16 rows and
-    // qkv_prep over them.  (Splitting an uncached pass's
-    // prompt rows off, as the other products do, measured no faster here: 768 + 48 tiles.)
+    // qkv_prep over them.  An uncached pass's prompt rows (at most 256) go apart first, through
+    // the few-row product to fp16 rows and qkv_prep, so that the image rows' fused product runs
+    // whole waves of tiles (4096 rows: 768 tiles, 3 waves, where the 256 prompt rows with them
+    // make 816, a fourth wave of 48).  Every pass computes its image rows alike.
+    int64_t qh = 0;   // the rows done apart
+    if (nh > 0 && nh < n && nh <= 256) {
+      {
+        ProfScope ps(d, EXN_PROF_QKV, 2.0 * nh * 3 * Wd * Wd, nh * Wd * 2 + 3 * Wd * Wd * 1.0625 + nh * 3 * Wd * 2);
+        ea = EpiArgs{};
+        ea.y = qkv;
+        ea.ldy = 3 * EXN_W;
+        const hipError_t r =
+            gemm_split_rows(s, y, EXN_W, wop_n(L.qkv, nh), nh, 3 * EXN_W, EXN_W, EPI_F16, ea, part, kSplitCap);
+        if (r != hipErrorNotSupported) HIPCHK(r);
+        if (r == hipSuccess) qh = nh;
+      }
+      if (qh) {
+        ProfScope ps(d, EXN_PROF_QKV_PREP, 0, (double)nh * (3 * Wd * 2 * 2 + 128 * 4));
+        HIPCHK(qkv_prep(s, qkv, nh, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap, n));
+      }
+    }
+    const double nq = nd - (double)qh;
     bool fused = false;
     {
-      ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
+      ProfScope ps(d, EXN_PROF_QKV, 2 * nq * 3 * Wd * Wd, nq * Wd * 2 + 3 * Wd * Wd * 1.0625 + nq * 3 * Wd * 2);
       ea = EpiArgs{};
-      ea.n0 = n0;
+      ea.n0 = n0 + (int)qh;
       ea.wq = L.norm_q;
       ea.wk = L.norm_k;
       ea.cs = d->cs;
       ea.qscale = QK_QSCALE;
-      ea.q = q;
+      ea.q = q + qh * EXN_HD;
       ea.qld = n;
       ea.kc = d->kc[(size_t)il];
       ea.vt = d->vt[(size_t)il];
       ea.lcap = d->lcap;
-      const hipError_t r = gemm_qkv(s, y, EXN_W, wop(L.qkv), n, EXN_W, ea);
+      const hipError_t r = gemm_qkv(s, y + qh * EXN_W, EXN_W, wop(L.qkv), n - qh, EXN_W, ea);
       if (r != hipErrorNotSupported) HIPCHK(r);
       fused = r == hipSuccess;
     }
     if (!fused) {
       {
-        ProfScope ps(d, EXN_PROF_QKV, 2 * nd * 3 * Wd * Wd, nd * Wd * 2 + 3 * Wd * Wd * 1.0625 + nd * 3 * Wd * 2);
+        ProfScope ps(d, EXN_PROF_QKV, 2 * nq * 3 * Wd * Wd, nq * Wd * 2 + 3 * Wd * Wd * 1.0625 + nq * 3 * Wd * 2);
         ea = EpiArgs{};
-        ea.y = qkv;
+        ea.y = qkv + qh * 3 * EXN_W;
         ea.ldy = 3 * EXN_W;
-        HIPCHK(gemm_any(s, L.qkv, y, EXN_W, n, EPI_F16, ea));
+        HIPCHK(gemm_any(s, L.qkv, y + qh * EXN_W, EXN_W, n - qh, EPI_F16, ea));
       }
-      ProfScope ps(d, EXN_PROF_QKV_PREP, 0, qkv_bytes);
-      HIPCHK(qkv_prep(s, qkv, n, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap, n));
+      ProfScope ps(d, EXN_PROF_QKV_PREP, 0, qkv_bytes * nq / nd);
+      HIPCHK(qkv_prep(s, qkv + qh * 3 * EXN_W, n - qh, L.norm_q, L.norm_k, d->cs, q + qh * EXN_HD, d->kc[(size_t)il],
+                      d->vt[(size_t)il], n0 + qh, d->lcap, n));
     }
     {
       ProfScope ps(d, EXN_PROF_ATTEND, 4.0 * EXN_HD * EXN_H * pairs, nd * Wd * 2 * 2 + 2.0 * l * Wd * 2);

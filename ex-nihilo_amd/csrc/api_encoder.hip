@@ -358,7 +358,7 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
   TRY(enc_buf(e, "part", (size_t)kSplitCap * 4, (void**)&part));
   auto mm = [&](const exn_w* w, const uint16_t* xin, int64_t lda, Epi epi, const EpiArgs& a) -> hipError_t {
     if (split || ((int64_t)n + 255) / 256 * ((w->rows + 255) / 256) < 192) {
-      const hipError_t r = gemm_split_rows(s, xin, lda, wop(w), n, w->rows, w->cols, epi, a, part, kSplitCap);
+      const hipError_t r = gemm_split_rows(s, xin, lda, wop_n(w, n), n, w->rows, w->cols, epi, a, part, kSplitCap);
       if (r != hipErrorNotSupported) return r;
     }
     return gemm_any(s, w, xin, lda, n, epi, a);

@@ -84,6 +84,7 @@ constexpr int64_t kSplitCap = (int64_t)2 * 256 * 256 * 256;
 // shared helpers (api.hip: contexts, memory, the block products; api_weights.hip: weights)
 const uint16_t* wbf(const exn_w* w);
 WOp wop(const exn_w* w);
+WOp wop_n(const exn_w* w, int64_t n);
 int dev_alloc(void** p, size_t bytes);
 void dev_free(void* p);
 int use(exn_ctx* ctx);

@@ -1102,8 +1102,252 @@ static hipError_t launch_w(hipStream_t s, const uint16_t* x, int64_t lda, const 
   return launch_bt<EPI, true>(s, x, lda, nullptr, M, N, K, ea, split, w.qt);
 }
 
+// --- products over few rows -------------------------------------------------------------
+// A product of at most 256 rows (a prompt's) reads each weight for only that many rows: the
+// weights' stream and (at 256 rows) the MFMAs bound it, and the chip is covered by splitting N
+// finely, not by 256 x 256 tiles with K cut 8 or 16 ways (whose fp32 partial sums then outweigh
+// the weights).  Tiles of MT = 128 WMS rows x NT = 32 (8 / WMS) weight rows, 8 waves of 128 x 32
+// (WMS along M, 8 / WMS along N, two a SIMD), K split over the tile's S workgroups where the
+// tiles are fewer than the CUs:
+//   X: the tile's MT rows x 64 k a step by 16-byte buffer loads into registers a step ahead,
+//      stored into one of two LDS stages (rows of 128 bytes, the 16-byte chunks swizzled as
+//      k_gemm_bt's) after the step's MFMAs; rows past M read as zeros (the buffer's extent);
+//   W: each wave's 32 weight rows go straight to registers, WD steps ahead: lane l takes row
+//      l%16 of its fragments j = 0, 1 at k 16 (l/16) .. +15 of the step -- Q8_0: 16 codes (one
+//      16-byte load from the tiled operand) and the dword of the row's two block scales; bf16: 32
+//      bytes -- and makes the MFMA's B operand of them itself, a step ahead: bf16(fp32(d) q), the
+//      resident expansion's value bit for bit, so bf16 and Q8_0 weights give the same sums.  A
+//      wave's fragments are rows 32 wn .. +31, or with the SwiGLU epilogue the 16 gate rows and
+//      their 16 up rows (gate_up interleaved by 32), so that a lane holds both of its column.
+// v_mfma_f32_16x16x32_bf16 sums its 32 k in whatever order the two operands agree on: slice kk
+// of a step holds, in lane l, k = 16 (l/16) + 8 kk .. +7, so that a lane's 16 codes are one load
+// and lie in one Q8_0 block.  The WMS waves along M each convert a weight row's codes.
+template <int EPI, int WMS, bool Q8>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_gemm_few(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restrict__ WB,
+           const uint8_t* __restrict__ QT, int64_t M, int64_t N, int64_t K, EpiArgs ea) {
+  constexpr bool SWI = EPI == EPI_SWIGLU;
+  constexpr int WNS = 8 / WMS, MT = 128 * WMS, NT = 32 * WNS, MI = 8, NI = 2;
+  constexpr int XST = MT * 128;   // an X stage: MT rows of 64 bf16
+  constexpr int XR = MT / 64;     // a thread's 16-byte loads of it
+  constexpr int WD = 4;           // the weights' steps in flight
+  static_assert(WMS == 1 || WMS == 2, "128 or 256 rows");
+  extern __shared__ __align__(1024) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WNS, wn = wave % WNS, lo = lane & 15, q4 = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * MT, n0 = (int64_t)blockIdx.x * NT;
+  // split K: workgroup z takes k-steps kt0 .. kt1-1, cut at whole groups of WD steps (K % 256 ==
+  // 0), so that the main loop runs whole groups and keeps each weight set in its registers
+  const int KT = (int)(K / 64), S = gridDim.z, z = blockIdx.z;
+  const int kt0 = WD * (int)((int64_t)(KT / WD) * z / S), kt1 = WD * (int)((int64_t)(KT / WD) * (z + 1) / S);
+  // X: load i of thread t is tile row 64 i + t/8, LDS chunk t%8 holding global chunk (t%8) ^
+  // chunk_swz(row) (chunk_swz(64 i + t/8) = chunk_swz(t/8)); its LDS place i 8192 + 16 t
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(X + m0 * lda), 0, (int)(max((int64_t)0, M - m0) * lda * 2), 0x00020000);
+  uint32_t xoff[XR];
+#pragma unroll
+  for (int i = 0; i < XR; ++i)
+    xoff[i] = (uint32_t)(((64 * i + (tid >> 3)) * lda + 8 * ((tid & 7) ^ chunk_swz(tid >> 3))) * 2);
+  u32x4 xv[XR];
+  auto x_load = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < XR; ++i) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i], t * 128, 0);
+  };
+  auto x_store = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < XR; ++i) *(u32x4*)(smem + st * XST + i * 8192 + tid * 16) = xv[i];
+  };
+  // W: fragment j of the wave is tile rows f0 + JS j .. +15 (lane l: row + l%16)
+  constexpr int JS = SWI ? 32 : 16;
+  const int f0 = SWI ? 64 * (wn >> 1) + 16 * (wn & 1) : 32 * wn;
+  const int wr = (int)(n0 % 256) + f0 + lo;   // Q8: the row of fragment 0 in its 256-row chunk
+  const __amdgpu_buffer_rsrc_t wqs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(QT + (n0 / 256) * (int64_t)KT * QT_CHUNK), 0, Q8 ? KT * QT_CHUNK : 0, 0x00020000);
+  const uint16_t* wrow = WB + (n0 + f0 + lo) * K + 16 * q4;
+  u32x4 wc[WD][NI][Q8 ? 1 : 2];
+  uint32_t wd[WD][NI];
+  auto w_load = [&](auto sc, int t) {
+    constexpr int s = decltype(sc)::value;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      if constexpr (Q8) {
+        wc[s][j][0] = __builtin_amdgcn_raw_buffer_load_b128(wqs, (uint32_t)(wr * 64 + 16 * q4 + 64 * JS * j), t * QT_CHUNK, 0);
+        wd[s][j] = __builtin_amdgcn_raw_buffer_load_b32(wqs, (uint32_t)(QT_SCALES + wr * 4 + 4 * JS * j), t * QT_CHUNK, 0);
+      } else {
+        const u32x4* p = (const u32x4*)(wrow + (int64_t)JS * j * K + t * 64);
+        wc[s][j][0] = p[0];
+        wc[s][j][1] = p[1];
+      }
+    }
+  };
+  // the B operands of two steps: the current one's and the next one's, converted meanwhile
+  u32x4 bq[2][NI][2];
+  float wsc[NI];   // the next step's block scales, a fragment each
+  // piece q (0..3) of slice kk of the conversion of weight set S into bq[B]: fragment q/2, the
+  // 4 codes of dword 2 kk + q%2 (the scale taken with the slice's first piece of the fragment)
+  auto w_piece = [&](auto sc, auto bc, int kk, int q) {
+    constexpr int s = decltype(sc)::value, b = decltype(bc)::value;
+    const int j = q >> 1, e = q & 1;
+    if constexpr (Q8) {
+      if (kk == 0 && e == 0) wsc[j] = f16_to_f32((wd[s][j] >> (16 * (q4 >> 1))) & 0xFFFFu);
+      const float d = wsc[j];
+      const uint32_t u = wc[s][j][0][2 * kk + e];
+      const float g0 = (float)(int8_t)(u & 0xFFu) * d, g1 = (float)(int8_t)((u >> 8) & 0xFFu) * d;
+      const float g2 = (float)(int8_t)((u >> 16) & 0xFFu) * d, g3 = (float)(int8_t)(u >> 24) * d;
+      bq[b][j][kk][2 * e] = pack_bf16x2(g0, g1);
+      bq[b][j][kk][2 * e + 1] = pack_bf16x2(g2, g3);
+    } else {
+      bq[b][j][kk][2 * e] = wc[s][j][kk][2 * e];
+      bq[b][j][kk][2 * e + 1] = wc[s][j][kk][2 * e + 1];
+    }
+  };
+  f32x4 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int fs = chunk_swz(lo);   // chunk_swz of the wave's fragment rows 16 i + l%16
+  // X's fragments of slice kk: row 16 i + l%16 of the wave's 128 (i < MI), 16 bytes a lane
+  bf16x8 af[MI];
+  auto a_read = [&](int st, int kk, int i) {
+    af[i] = *(const bf16x8*)(smem + st * XST + (wm * 128 + lo) * 128 + (((2 * q4 + kk) ^ fs) << 4) + i * 16 * 128);
+  };
+  // slice kk's MFMAs from bq[B], row by row, each row followed by its share of the other work (the
+  // next slice's fragment i read, a piece of the next step's conversion into bq[NB]), fenced so
+  // that the compiler keeps the order and with it the registers' lifetimes short
+  auto mfma_slice = [&](auto bc, auto sc, auto nbc, int kk, int st) {
+    constexpr int b = decltype(bc)::value;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], __builtin_bit_cast(bf16x8, bq[b][j][kk]), acc[i][j], 0, 0, 0);
+      if (kk == 0) a_read(st, 1, i);
+      if (i % 2 == 1) w_piece(sc, nbc, kk, i / 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  // step t (W(t) in register set t%4, its B operands in bq[t%2], X(t + 1) in xv): the barrier
+  // (X(t) stored, the other stage free), W(t + 4) loaded into set t%4, X(t)'s fragments read, the
+  // MFMAs with W(t + 1) converted between them, X(t + 1) stored and X(t + 2) loaded.  The order
+  // is for the in-order wait counter: the wait for X(t + 1) (loaded at step t - 1's end) leaves
+  // every later weight load outstanding and forces only W(t + 3), loaded two steps before.
+  // Past the end the loads repeat the last step and nothing reads them.
+  auto step = [&](auto uc, int t) {
+    constexpr int u = decltype(uc)::value;
+    using Cur = std::integral_constant<int, u % 2>;
+    using Nb = std::integral_constant<int, (u + 1) % 2>;
+    using Ns = std::integral_constant<int, (u + 1) % WD>;
+    __syncthreads();
+    const int st = (t - kt0) & 1;
+    w_load(uc, min(t + WD, kt1 - 1));
+#pragma unroll
+    for (int i = 0; i < MI; ++i) a_read(st, 0, i);
+    mfma_slice(Cur{}, Ns{}, Nb{}, 0, st);
+    mfma_slice(Cur{}, Ns{}, Nb{}, 1, st);
+    x_store(st ^ 1);
+    x_load(min(t + 2, kt1 - 1));
+  };
+  // the prologue in the same order: the weights, then X(kt0 + 1) last
+  x_load(kt0);
+  w_load(I0{}, kt0);
+  w_load(I1{}, min(kt0 + 1, kt1 - 1));
+  w_load(I2{}, min(kt0 + 2, kt1 - 1));
+  w_load(I3{}, min(kt0 + 3, kt1 - 1));
+  x_store(0);
+  x_load(min(kt0 + 1, kt1 - 1));
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w_piece(I0{}, I0{}, kk, q);
+  static_assert(WD == 4, "a loop round is the four steps of the weight sets");
+  for (int t = kt0; t < kt1; t += WD) {
+    step(I0{}, t);
+    step(I1{}, t + 1);
+    step(I2{}, t + 2);
+    step(I3{}, t + 3);
+  }
+  __syncthreads();   // every wave done with the stages before the epilogue takes the LDS
+  const int64_t wrow0 = m0 + wm * 128;
+  if constexpr (SWI) {
+    // output column n0/2 + 32 (wn/2) + 16 (wn%2) + l%16 (gate row 64 (wn/2) + 16 (wn%2) + l%16 of
+    // the tile is output column 32 (wn/2) + 16 (wn%2) + l%16) from gate fragment 0 and up fragment
+    // 1: silu(gate) x up into bf16, through the wave's LDS block (128 rows of 16) so that each lane
+    // stores 16-byte runs of 8 columns
+    uint16_t* stg = (uint16_t*)smem + wave * (128 * 24);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float o = silu_bf16out(acc[i][0][r]) * acc[i][1][r];
+        stg[(16 * i + 4 * q4 + r) * 24 + lo] = (uint16_t)(pack_bf16x2(o, 0.f) & 0xFFFF);
+      }
+    const int64_t col = n0 / 2 + 32 * (wn >> 1) + 16 * (wn & 1) + 8 * (lane & 1);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int row = 32 * it + (lane >> 1);
+      const int64_t m = wrow0 + row;
+      const u32x4 v = *(const u32x4*)(stg + row * 24 + 8 * (lane & 1));
+      if (m < M) *(u32x4*)((uint16_t*)ea.y + m * ea.ldy + col) = v;
+    }
+  } else {
+    epilogue_lds<EPI, MI, NI>(acc, (float*)smem + wave * (32 * 40), wrow0, n0 + f0, lane, M, N, ea);
+  }
+}
+
+// the few-row kernel's conditions: at most 256 rows, whole tiles of N, 16-byte chunks of X and
+// of the weights, 31-bit buffer extents
+static bool few_fits(const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K,
+                     const EpiArgs& ea) {
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const int64_t NT = M > 128 ? 128 : 256;
+  const bool wok = w.wb ? a16(w.wb) : (w.qt && a16(w.qt) && (K / 64) * QT_CHUNK < ((int64_t)1 << 31));
+  return M > 0 && M <= 256 && N % NT == 0 && K % 256 == 0 && wok && lda % 8 == 0 && a16(x) && 256 * lda < ((int64_t)1 << 30) &&
+         ea.ldy % 4 == 0 && a16(ea.y) && a16(ea.resid) && a16(ea.gate) && ea.mstride % 4 == 0;
+}
+
+template <int EPI, bool Q8>
+static hipError_t launch_few(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
+                             int64_t K, const EpiArgs& ea, int S) {
+  const bool two = M > 128;
+  auto kern = two ? k_gemm_few<EPI, 2, Q8> : k_gemm_few<EPI, 1, Q8>;
+  // two X stages (64 or 32 KB), at least the epilogues' 48 KB (SwiGLU) and 40 KB
+  const int shm = two ? 2 * 256 * 128 : 49152;
+  const hipError_t e = ensure_lds((const void*)kern, shm);
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)(N / (two ? 128 : 256)), 1, (unsigned)S);
+  hipLaunchKernelGGL(kern, grid, dim3(512), shm, s, x, lda, w.wb, w.qt, M, N, K, ea);
+  return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_few_w(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
+                               int64_t K, const EpiArgs& ea, int S) {
+  return w.wb ? launch_few<EPI, false>(s, x, lda, w, M, N, K, ea, S) : launch_few<EPI, true>(s, x, lda, w, M, N, K, ea, S);
+}
+
+// a few-row product with K whole (no partial sums), through epilogue EPI
+static hipError_t few_direct(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
+                             int64_t K, Epi epi, const EpiArgs& ea) {
+  switch (epi) {
+    case EPI_F32: return launch_few_w<EPI_F32>(s, x, lda, w, M, N, K, ea, 1);
+    case EPI_BF16: return launch_few_w<EPI_BF16>(s, x, lda, w, M, N, K, ea, 1);
+    case EPI_GATE_ADD: return launch_few_w<EPI_GATE_ADD>(s, x, lda, w, M, N, K, ea, 1);
+    case EPI_SWIGLU: return launch_few_w<EPI_SWIGLU>(s, x, lda, w, M, N, K, ea, 1);
+    case EPI_GELU_BF16: return launch_few_w<EPI_GELU_BF16>(s, x, lda, w, M, N, K, ea, 1);
+    case EPI_F16: return launch_few_w<EPI_F16>(s, x, lda, w, M, N, K, ea, 1);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K,
                    Epi epi, const EpiArgs& ea) {
+  if (few_fits(x, lda, w, M, N, K, ea)) return few_direct(s, x, lda, w, M, N, K, epi, ea);
   if (!dma_fits(x, lda, w, M, N, K, ea)) return dispatch<false>(s, x, lda, w.qs, w.qd, nullptr, M, N, K, epi, ea);
   switch (epi) {
     case EPI_F32: return launch_w<EPI_F32>(s, x, lda, w, M, N, K, ea);
@@ -1155,10 +1399,42 @@ k_split_sum(int S, int64_t M, int64_t N, const float* __restrict__ part, EpiArgs
   }
 }
 
+// the S partial sums in PART (S x M x N floats) added in order through the epilogue EPI
+static hipError_t split_sum(hipStream_t s, Epi epi, int S, int64_t M, int64_t N, const float* part, const EpiArgs& ea) {
+  const int64_t threads = M * (epi == EPI_SWIGLU ? N / 2 : N) / 4;
+  const dim3 g((unsigned)((threads + 255) / 256));
+  switch (epi) {
+    case EPI_GATE_ADD: hipLaunchKernelGGL(k_split_sum<EPI_GATE_ADD>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL(k_split_sum<EPI_SWIGLU>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    case EPI_F32: hipLaunchKernelGGL(k_split_sum<EPI_F32>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    case EPI_BF16: hipLaunchKernelGGL(k_split_sum<EPI_BF16>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+    default: hipLaunchKernelGGL(k_split_sum<EPI_F16>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
+  }
+  return hipGetLastError();
+}
+
 hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
                            int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap, int smax) {
   if (M == 0) return hipSuccess;
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool epi_ok = epi == EPI_GATE_ADD || epi == EPI_SWIGLU || epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_F16;
+  if (!epi_ok) return hipErrorNotSupported;
+  if (few_fits(x, lda, w, M, N, K, ea) && a16(part)) {
+    // at most 256 rows: the few-row tiles, K split so that the tiles' workgroups are about one a
+    // CU, each at least 4 k-steps, at most SMAX ways and within PART_CAP
+    const int64_t tiles = N / (M > 128 ? 128 : 256);
+    int64_t S = 256 / tiles;
+    if (S > K / 256) S = K / 256;
+    if (S > smax) S = smax;
+    if (S > part_cap / (M * N)) S = part_cap / (M * N);
+    if (S <= 1) return few_direct(s, x, lda, w, M, N, K, epi, ea);
+    EpiArgs pa{};
+    pa.y = part;
+    pa.ldy = N;
+    const hipError_t e = launch_few_w<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
+    if (e != hipSuccess) return e;
+    return split_sum(s, epi, (int)S, M, N, part, ea);
+  }
   // S workgroups a tile, about one wave in all, at least 4 k-steps each, at most SMAX (in a DiT
   // pass, past 8 the partial sums' traffic, S x M x N fp32 written and read back, outweighs the
   // wider spread: 256 prompt rows through to_out and down, 0.2 ms less a pass than at 16, 0.9 ms
@@ -1172,21 +1448,11 @@ hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const 
   EpiArgs pa{};
   pa.y = part;
   pa.ldy = N;
-  const bool ok = N % 256 == 0 && a16(part) && S * M * N <= part_cap && dma_fits(x, lda, w, M, N, K, pa) &&
-                  (epi == EPI_GATE_ADD || epi == EPI_SWIGLU || epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_F16);
+  const bool ok = N % 256 == 0 && a16(part) && S * M * N <= part_cap && dma_fits(x, lda, w, M, N, K, pa);
   if (!ok) return hipErrorNotSupported;
   hipError_t e = launch_w<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
   if (e != hipSuccess) return e;
-  const int64_t threads = M * (epi == EPI_SWIGLU ? N / 2 : N) / 4;
-  const dim3 g((unsigned)((threads + 255) / 256));
-  switch (epi) {
-    case EPI_GATE_ADD: hipLaunchKernelGGL(k_split_sum<EPI_GATE_ADD>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL(k_split_sum<EPI_SWIGLU>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
-    case EPI_F32: hipLaunchKernelGGL(k_split_sum<EPI_F32>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
-    case EPI_BF16: hipLaunchKernelGGL(k_split_sum<EPI_BF16>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
-    default: hipLaunchKernelGGL(k_split_sum<EPI_F16>, g, dim3(256), 0, s, (int)S, M, N, part, ea); break;
-  }
-  return hipGetLastError();
+  return split_sum(s, epi, (int)S, M, N, part, ea);
 }
 
 hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t K,
@@ -1206,6 +1472,7 @@ hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w,
 hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint16_t* w, int64_t M, int64_t N,
                       int64_t K, Epi epi, const EpiArgs& ea) {
   const WOp wo{w, nullptr, nullptr, nullptr};
+  if (few_fits(x, lda, wo, M, N, K, ea)) return few_direct(s, x, lda, wo, M, N, K, epi, ea);
   if (!dma_fits(x, lda, wo, M, N, K, ea)) return dispatch<true>(s, x, lda, nullptr, nullptr, w, M, N, K, epi, ea);
   switch (epi) {
     case EPI_F32: return launch_w<EPI_F32>(s, x, lda, wo, M, N, K, ea);

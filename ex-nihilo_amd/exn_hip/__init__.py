@@ -293,9 +293,10 @@ class Weight:
         return self
 
     def free(self):
-        if getattr(self, "h", None):
+        # a weight's memory belongs to its context: once that is closed there is nothing to free
+        if getattr(self, "h", None) and self.ctx.h:
             call("exn_weight_free", self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:

@@ -136,6 +136,63 @@ def test_gemm_q8_bf16(ctx, M, N, K, resident):
     assert xo.rel_l2(got[rows], want) < 1e-2
 
 
+FEW_ROWS = [20, 24, 64, 128, 129, 200, 256]
+
+
+@pytest.mark.parametrize("M", FEW_ROWS)
+def test_few_row_products(ctx, M):
+    """Products of at most 256 rows (the few-row kernel: 128-row tiles up to 128 rows, 256-row
+    tiles above): fp32 out, the gated residual and SwiGLU, from Q8_0 and from the resident bf16
+    expansion -- the same bits from either, the same bits on a second call, and within 2e-6 of
+    float64 on the same bf16 operands."""
+    N, K = 1024, 4096
+    say("few-row products", M, N, K)
+    rng = np.random.default_rng(M)
+    xb = bf16(rng.normal(0, 1, (M, K)).astype(np.float32))
+    w = X.Weight.synth(ctx, 5, 210, N, K)
+    wf = xo.dequant_q8_0(*xo.q8_0_synth(5, 210, N, K))
+    prod = from_bf16(xb).astype(np.float64) @ from_bf16(bf16(wf)).T.astype(np.float64)
+    dx = dev(ctx, xb)
+    outs = []
+    for resident in (False, True, True):
+        w.resident(resident)
+        y = X.DevBuf(ctx, (M, N), np.float32)
+        X.call("exn_mm", ctx.h, w.h, dx.h, X.DT_BF16, y.h, X.DT_F32, M)
+        outs.append(y.get())
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+    assert xo.rel_l2(outs[0], prod) < 2e-6
+    # the gated residual, rows below p taking the second gate row
+    resid = rng.normal(0, 1, (M, N)).astype(np.float32)
+    gate = rng.normal(0, 0.5, (2, 4 * N)).astype(np.float32)
+    n0, p = 3, 11
+    got = []
+    for resident in (False, True):
+        w.resident(resident)
+        r = dev(ctx, resid)
+        X.call("exn_mm_gate_add", ctx.h, w.h, dx.h, M, r.h, n0, p, 4 * N, dev(ctx, gate).h)
+        got.append(r.get())
+    rows = np.where(n0 + np.arange(M) < p, 1, 0)
+    want = resid + np.tanh(gate[rows, :N].astype(np.float64)) * prod
+    assert np.array_equal(got[0], got[1]) and xo.rel_l2(got[0] - resid, want - resid) < 1e-5
+    w.free()
+    # SwiGLU on a paired gate_up matrix
+    ws = X.Weight.synth(ctx, 5, 211, N, K)
+    ws.pairs()
+    wsf = xo.dequant_q8_0(*xo.q8_0_synth(5, 211, N, K))
+    gu = from_bf16(xb).astype(np.float64) @ from_bf16(bf16(wsf)).T.astype(np.float64)
+    F = N // 2
+    ffs = []
+    for resident in (False, True):
+        ws.resident(resident)
+        ff = X.DevBuf(ctx, (M, F), np.uint16)
+        X.call("exn_mm_swiglu", ctx.h, ws.h, dx.h, ff.h, M)
+        ffs.append(ff.get())
+    assert np.array_equal(ffs[0], ffs[1])
+    want = gu[:, :F] / (1 + np.exp(-gu[:, :F])) * gu[:, F:]
+    assert xo.rel_l2(from_bf16(ffs[0]), want) < 4e-3
+    ws.free()
+
+
 @pytest.mark.parametrize("resident", [False, True], ids=["q8_0", "resident_bf16"])
 def test_gemm_bf16_out_and_f32_in(ctx, resident):
     say("gemm f32 in, bf16 out; gemv n <= 4")
