@@ -621,8 +621,10 @@ def main():
                           "value": rec["prompt_256"]["ms"], "unit": "ms/prompt", "n_gpus": 1, "steps": a.steps,
                           "warmup": a.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
                           "config": {"workload": "encoder-states-256-tokens",
-                                     "weights": "Q8_0 synthetic; the products stream each matrix's resident bf16 "
-                                                "expansion (exn_enc_resident, the default)",
+                                     "weights": "Q8_0 synthetic, the key/value heads once (q | k | v: 6144 rows); "
+                                                "products of at most 256 rows stream the Q8_0 codes (the few-row "
+                                                "kernel), longer ones the resident bf16 expansion "
+                                                "(exn_enc_resident, the default)",
                                      "seed": SEED}, "records": rec}), flush=True)
         return
     if a.vae_encode_only:

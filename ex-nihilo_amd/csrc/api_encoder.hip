@@ -21,17 +21,19 @@ const int kEncGroup = 4;   // query heads a key/value head (32 / 8)
 // DiT's pairwise rotary (dims 2i, 2i + 1 by angle i) applies.
 int enc_perm(int i) { return i < 64 ? 2 * i : 2 * (i - 64) + 1; }
 
-// the layer-matrix row of each source row of SLOT: q | k | v of 32 heads each (key/value head g
-// written out for query heads 4g .. 4g + 3, REP the copy), or gate/up interleaved by 32
-std::vector<int32_t> enc_rows(int slot, int rep) {
+// the key/value heads' rows in the q | k | v matrix: 8 heads of 128 each for k and for v
+constexpr int kEncKV = 8 * EXN_HD;
+
+// the layer-matrix row of each source row of SLOT: q (32 heads) | k (8) | v (8), the rotary's
+// pairs of q and k adjacent; or gate/up interleaved by 32
+std::vector<int32_t> enc_rows(int slot) {
   std::vector<int32_t> m;
   if (slot == E_Q) {
     for (int r = 0; r < EXN_W; ++r) m.push_back((r / EXN_HD) * EXN_HD + enc_perm(r % EXN_HD));
-  } else if (slot == E_K || slot == E_V) {
-    for (int r = 0; r < 8 * EXN_HD; ++r) {
-      const int head = kEncGroup * (r / EXN_HD) + rep, i = r % EXN_HD;
-      m.push_back((slot == E_K ? EXN_W : 2 * EXN_W) + head * EXN_HD + (slot == E_K ? enc_perm(i) : i));
-    }
+  } else if (slot == E_K) {
+    for (int r = 0; r < kEncKV; ++r) m.push_back(EXN_W + (r / EXN_HD) * EXN_HD + enc_perm(r % EXN_HD));
+  } else if (slot == E_V) {
+    for (int r = 0; r < kEncKV; ++r) m.push_back(EXN_W + kEncKV + r);
   } else if (slot == E_GATE || slot == E_UP) {
     for (int r = 0; r < EXN_F; ++r) m.push_back(64 * (r / 32) + (slot == E_UP ? 32 : 0) + r % 32);
   }
@@ -39,12 +41,12 @@ std::vector<int32_t> enc_rows(int slot, int rep) {
 }
 
 struct EncLayer {
-  exn_w* qkv = nullptr;      // q | k | v, 3 x 4096 rows (the rotary's pairs adjacent)
+  exn_w* qkv = nullptr;      // q | k | v, 4096 + 1024 + 1024 rows (the rotary's pairs adjacent)
   exn_w* out = nullptr;
   exn_w* gate_up = nullptr;  // gate / up interleaved by 32
   exn_w* down = nullptr;
   float* vec[E_SLOTS] = {};  // the norms' weights (q and k norms permuted as their rows)
-  unsigned have = 0;         // slots set, a bit each (K and V: all four copies)
+  unsigned have = 0;         // slots set, a bit each
 };
 
 }  // namespace
@@ -60,7 +62,7 @@ struct exn_enc {
   std::vector<EncLayer> L;
   std::map<std::string, Buf> bufs;
   float* one_gate = nullptr;  // +inf a column: the gated residual's tanh(gate) is exactly 1
-  std::map<int, int32_t*> maps;  // device row maps by slot * 4 + copy
+  std::map<int, int32_t*> maps;  // device row maps by slot
   bool bf16 = true;           // the matrices run from resident bf16 expansions (exn_enc_resident)
 };
 
@@ -79,10 +81,10 @@ static int enc_buf(exn_enc* e, const char* key, size_t bytes, void** out, bool z
   return EXN_OK;
 }
 
-static int enc_map(exn_enc* e, int slot, int rep, int32_t** out) {
-  int32_t*& m = e->maps[slot * 4 + rep];
+static int enc_map(exn_enc* e, int slot, int32_t** out) {
+  int32_t*& m = e->maps[slot];
   if (!m) {
-    const std::vector<int32_t> h = enc_rows(slot, rep);
+    const std::vector<int32_t> h = enc_rows(slot);
     TRY(dev_alloc((void**)&m, h.size() * 4));
     HIPCHK(hipMemcpyAsync(m, h.data(), h.size() * 4, hipMemcpyHostToDevice, e->ctx->stream));
     HIPCHK(hipStreamSynchronize(e->ctx->stream));
@@ -95,7 +97,8 @@ static int enc_map(exn_enc* e, int slot, int rep, int32_t** out) {
 static int enc_matrix(exn_enc* e, EncLayer& L, int slot, exn_w** out) {
   exn_w** w = slot == E_OUT ? &L.out : slot == E_DOWN ? &L.down : (slot == E_GATE || slot == E_UP) ? &L.gate_up : &L.qkv;
   if (!*w) {
-    const int64_t rows = slot == E_OUT ? EXN_W : slot == E_DOWN ? EXN_W : (slot == E_GATE || slot == E_UP) ? 2 * EXN_F : 3 * EXN_W;
+    const int64_t rows = slot == E_OUT ? EXN_W : slot == E_DOWN ? EXN_W : (slot == E_GATE || slot == E_UP) ? 2 * EXN_F
+                                                                                                   : EXN_W + 2 * kEncKV;
     const int64_t cols = slot == E_DOWN ? EXN_F : EXN_W;
     TRY(w_new(e->ctx, EXN_Q8_0, rows, cols, w));
     if (slot == E_GATE || slot == E_UP) (*w)->pairs = true;
@@ -217,12 +220,9 @@ int exn_enc_set(exn_enc* e, const char* name, int kind, const void* data, int64_
   exn_w* w = nullptr;
   TRY(enc_matrix(e, L, slot, &w));
   w->wx_ok = false;   // the expansion, if kept, is remade before the next use
-  const int copies = (slot == E_K || slot == E_V) ? kEncGroup : 1;
-  for (int rep = 0; rep < copies; ++rep) {
-    int32_t* map = nullptr;
-    if (slot != E_OUT && slot != E_DOWN) TRY(enc_map(e, slot, rep, &map));
-    TRY(upload_q8_blocks(e->ctx, data, d1, d0, map, w->qs, w->d));
-  }
+  int32_t* map = nullptr;
+  if (slot != E_OUT && slot != E_DOWN) TRY(enc_map(e, slot, &map));
+  TRY(upload_q8_blocks(e->ctx, data, d1, d0, map, w->qs, w->d));
   TRY(retile(w));
   L.have |= 1u << slot;
   return EXN_OK;
@@ -264,12 +264,9 @@ int exn_enc_synth(exn_enc* e, uint64_t seed, int64_t vocab) {
       exn_w* w = nullptr;
       TRY(enc_matrix(e, L, slot, &w));
       w->wx_ok = false;
-      const int copies = (slot == E_K || slot == E_V) ? kEncGroup : 1;
-      for (int rep = 0; rep < copies; ++rep) {
-        int32_t* map = nullptr;
-        if (slot != E_OUT && slot != E_DOWN) TRY(enc_map(e, slot, rep, &map));
-        HIPCHK(synth_q8(s, key, kEncDims[slot][1], kEncDims[slot][0], kEncDims[slot][0] / 32, map, w->qs, w->d));
-      }
+      int32_t* map = nullptr;
+      if (slot != E_OUT && slot != E_DOWN) TRY(enc_map(e, slot, &map));
+      HIPCHK(synth_q8(s, key, kEncDims[slot][1], kEncDims[slot][0], kEncDims[slot][0] / 32, map, w->qs, w->d));
       TRY(retile(w));
       L.have |= 1u << slot;
     }
@@ -350,6 +347,7 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
   TRY(enc_buf(e, "q", (size_t)n * EXN_W * 2, (void**)&q));
   TRY(enc_buf(e, "kc", (size_t)lcap * EXN_W * 2, (void**)&kc, true));
   TRY(enc_buf(e, "vt", (size_t)lcap * EXN_W * 2, (void**)&vt, true));
+  TRY(enc_buf(e, "qkv", (size_t)n * (EXN_W + 2 * kEncKV) * 2, (void**)&qkv));
   // a prompt of at most 1024 tokens is about one row of 256-row tiles: its products split K
   // over the chip (the DiT's prompt-row path), the partial sums then added in order; a longer
   // one splits the products of fewer tiles than 192 (out and down, 16 column tiles)
@@ -370,28 +368,13 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
   for (int il = 0; il < e->layers; ++il) {
     const EncLayer& L = e->L[(size_t)il];
     HIPCHK(rms_norm(s, n, EXN_W, 1e-6f, x, L.vec[E_ATTN_NORM], y, 1));
+    // q | k | v of the 8 key/value heads into fp16 rows, then the q/k norms, the rotary and the
+    // K/V stores, each key/value head for its 4 query heads
     ea = EpiArgs{};
-    ea.n0 = 0;
-    ea.wq = L.vec[E_QNORM];
-    ea.wk = L.vec[E_KNORM];
-    ea.cs = cs;
-    ea.qscale = QK_QSCALE;
-    ea.q = q;
-    ea.qld = n;
-    ea.kc = kc;
-    ea.vt = vt;
-    ea.lcap = lcap;
-    const hipError_t r = split ? hipErrorNotSupported : gemm_qkv(s, y, EXN_W, wop(L.qkv), n, EXN_W, ea);
-    if (r == hipErrorNotSupported) {
-      TRY(enc_buf(e, "qkv", (size_t)n * 3 * EXN_W * 2, (void**)&qkv));
-      ea = EpiArgs{};
-      ea.y = qkv;
-      ea.ldy = 3 * EXN_W;
-      HIPCHK(mm(L.qkv, y, EXN_W, EPI_F16, ea));
-      HIPCHK(qkv_prep(s, qkv, n, L.vec[E_QNORM], L.vec[E_KNORM], cs, q, kc, vt, 0, lcap, n));
-    } else {
-      HIPCHK(r);
-    }
+    ea.y = qkv;
+    ea.ldy = EXN_W + 2 * kEncKV;
+    HIPCHK(mm(L.qkv, y, EXN_W, EPI_F16, ea));
+    HIPCHK(qkv_prep(s, qkv, n, L.vec[E_QNORM], L.vec[E_KNORM], cs, q, kc, vt, 0, lcap, n, kEncGroup));
     HIPCHK(attend(s, q, kc, vt, att, n, 0, n, n, lcap, 0, 0, 1.f));
     ea = EpiArgs{};
     ea.resid = x;

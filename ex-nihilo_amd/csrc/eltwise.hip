@@ -198,18 +198,21 @@ hipError_t silu(hipStream_t s, int64_t count, float* x) {
   return hipGetLastError();
 }
 
-// qkv: fp16 rows of 3 x 4096 (q | k | v) for tokens 0..n-1, token t being
-// sequence row row0 + t.  Writes, all fp16 (the attention's operands, as the
-// reference's halves): q ([32][n][128], scaled by qscale after the rotation),
-// k into kc ([32][lcap][128]) rows row0.., v transposed into vt
-// ([32][128][lcap]) columns row0...  cs: cos, sin for 64 pairs, 128 floats a
-// sequence row.  grid (ceil(n/64), 32), block 256.
+// qkv: fp16 rows of q | k | v for tokens 0..n-1, token t being sequence row
+// row0 + t: q 32 heads of 128, k and v 32 / G heads each (G query heads a key/value
+// head: 1, rows of 3 x 4096, or 4, rows of 6144).  Writes, all fp16 (the attention's
+// operands, as the reference's halves): q ([32][n][128], scaled by qscale after the
+// rotation), k into kc ([32][lcap][128]) rows row0.., v transposed into vt
+// ([32][128][lcap]) columns row0.., query head h taking key/value head h / G.  cs:
+// cos, sin for 64 pairs, 128 floats a sequence row.  grid (ceil(n/64), 32), block 256.
 __global__ void __launch_bounds__(256)
 k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict__ wq, const float* __restrict__ wk,
            const float* __restrict__ cs, float qscale, uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
-           uint16_t* __restrict__ vt, int64_t row0, int64_t lcap, int64_t qld) {
+           uint16_t* __restrict__ vt, int64_t row0, int64_t lcap, int64_t qld, int g) {
   __shared__ uint16_t tile[64][128 + 2];
   const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t ld = 4096 + 2 * (4096 / g);                      // a row of qkv
+  const int64_t ko = 4096 + (h / g) * 128, vo = ko + 4096 / g;   // this head's k and v in it
   const int64_t t0 = (int64_t)blockIdx.x * 64;
   // q and k: 16 lanes a token, lane holding dims d8 .. d8+7 (its 4 rotation pairs) as one
   // 16-byte load and store; a wave takes 4 tokens a round, its 16 tokens in 4 rounds whose
@@ -226,9 +229,9 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int64_t tc = min(t0 + wave * 16 + it * 4 + sub, n - 1);   // rows past n: loaded, not stored
-    const uint16_t* rq = qkv + tc * (3 * 4096) + h * 128 + d8;
-    uq[it] = *(const u32x4*)rq;
-    uk[it] = *(const u32x4*)(rq + 4096);
+    const uint16_t* rq = qkv + tc * ld + d8;
+    uq[it] = *(const u32x4*)(rq + h * 128);
+    uk[it] = *(const u32x4*)(rq + ko);
     const float* cr = cs + (row0 + tc) * 128 + d8;   // cos, sin of pairs d8/2 .. d8/2 + 3
     ca[it] = *(const f32x4*)cr;
     cb[it] = *(const f32x4*)(cr + 4);
@@ -274,7 +277,7 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
     const int c = tid + 256 * i, tok = c >> 4, d8 = (c & 15) * 8;
     const int64_t t = t0 + tok;
     u32x4 v = u32x4{0, 0, 0, 0};
-    if (t < n) v = *(const u32x4*)(qkv + t * (3 * 4096) + 2 * 4096 + h * 128 + d8);
+    if (t < n) v = *(const u32x4*)(qkv + t * ld + vo + d8);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       *(uint32_t*)&tile[tok][d8 + 2 * e] = v[e];
@@ -291,12 +294,13 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
 
 hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk, const float* cs,
                     uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap,
-                    int64_t qld) {
+                    int64_t qld, int kv_group) {
   if (n == 0) return hipSuccess;
+  if (kv_group != 1 && kv_group != 4) return hipErrorInvalidValue;
   // q is scaled by 1/sqrt(128) * log2(e): the attention's scores are then in log2 units
   const float qscale = QK_QSCALE;
   hipLaunchKernelGGL(k_qkv_prep, dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, n, wq, wk, cs, qscale, q, k, vt,
-                     row0, lcap, qld);
+                     row0, lcap, qld, kv_group);
   return hipGetLastError();
 }
 

@@ -241,7 +241,7 @@ hipError_t gelu_tanh(hipStream_t s, int64_t count, float* x);
 hipError_t silu(hipStream_t s, int64_t count, float* x);
 hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk,
                     const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap,
-                    int64_t qld);
+                    int64_t qld, int kv_group = 1);
 hipError_t latent_rows(hipStream_t s, const float* latent, int64_t nimg, float* rows);
 hipError_t rows_to_latent(hipStream_t s, const float* rows, int64_t nimg, float* latent);
 hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float ds);
