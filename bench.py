@@ -40,10 +40,14 @@ prints its own JSON line.
 prompt_encoder: the prompt encoder (Qwen3-VL-8B's text model, 36 blocks, synthetic Q8_0
 weights) over a 256-token prompt, and over an edit prompt of 1100 tokens of which 1024 are a
 1024 x 1024 picture's rows (merged and deepstack), each the mean of 3 calls with the inputs in
-HBM; FLOPs counted with the model's 8 key/value heads (the products write them out per query
-head).
+HBM; FLOPs counted with the model's 8 key/value heads (the q | k | v product's 6144 rows).
 
     python bench.py --encoder-only [--steps K] [--warmup W]
+
+uncached: the 1024^2 step with the prompt's 256 rows through every block (the reference's
+first step), K steps after W, its own JSON line.
+
+    python bench.py --uncached-only [--steps K] [--warmup W]
 
 vision_encode_1024sq: the vision tower (Qwen3-VL's ViT, synthetic fp16-valued
 weights, fp32 arithmetic) on a 1024 x 1024 RGBA picture in HBM: 4096 patches
@@ -588,6 +592,8 @@ def main():
                          " (with --q8-only: of the Q8_0 product, into " + TRAFFIC_FILE_Q8 + ")")
     ap.add_argument("--q8-only", action="store_true",
                     help="time only the cached step from Q8_0 weights (no resident bf16 copies, no VAE)")
+    ap.add_argument("--uncached-only", action="store_true",
+                    help="time the uncached step alone (the prompt rows through every block)")
     ap.add_argument("--w8a8-only", action="store_true",
                     help="time only the cached step in the reference's int8 mode (exn_dit_w8a8)")
     ap.add_argument("--bf16-only", action="store_true",
@@ -673,6 +679,24 @@ def main():
             step(i, key)
         ctx.sync()
         power_run(a.power, step, ctx, z, latent, "Q8_0" if a.q8_only else "resident bf16 expansion")
+        d.destroy()
+        ctx.close()
+        return
+    if a.uncached_only:   # the uncached step alone: the prompt rows through every block too
+        for i in range(1 + a.warmup):
+            step(i, 0)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for i in range(a.steps):
+            step(1 + i, 0)
+        ctx.sync()
+        t = (time.perf_counter() - t0) / a.steps
+        tot = step_flops(False)[2]
+        print(json.dumps({"metric": "DiT Euler step ms @1024², uncached (the 256 prompt rows through every block)",
+                          "value": round(t * 1e3, 3), "unit": "ms/step", "steps": a.steps, "warmup": a.warmup,
+                          "tflops": round(tot / t / 1e12, 1), "mfma_peak_frac": round(tot / t / 1e12 / PEAK_TFLOPS, 4),
+                          "weights": "resident bf16 expansion; products of at most 256 rows from the Q8_0 codes"}),
+              flush=True)
         d.destroy()
         ctx.close()
         return
