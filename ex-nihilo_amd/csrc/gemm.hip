@@ -1109,9 +1109,10 @@ static hipError_t launch_w(hipStream_t s, const uint16_t* x, int64_t lda, const 
 // the weights).  Tiles of MT = 128 WMS rows x NT = 32 (8 / WMS) weight rows, 8 waves of 128 x 32
 // (WMS along M, 8 / WMS along N, two a SIMD), K split over the tile's S workgroups where the
 // tiles are fewer than the CUs:
-//   X: the tile's MT rows x 64 k a step by 16-byte buffer loads into registers a step ahead,
-//      stored into one of two LDS stages (rows of 128 bytes, the 16-byte chunks swizzled as
-//      k_gemm_bt's) after the step's MFMAs; rows past M read as zeros (the buffer's extent);
+//   X: the tile's MT rows x 64 k a step by the LDS DMA (buffer_load ... lds) a step ahead into
+//      one of two LDS stages (rows of 128 bytes, the 16-byte chunks swizzled as k_gemm_bt's),
+//      issued first in a step so that the wait for it leaves the later weight loads out; rows
+//      past M read as zeros (the buffer's extent);
 //   W: each wave's 32 weight rows go straight to registers, WD steps ahead: lane l takes row
 //      l%16 of its fragments j = 0, 1 at k 16 (l/16) .. +15 of the step -- Q8_0: 16 codes (one
 //      16-byte load from the tiled operand) and the dword of the row's two block scales; bf16: 32
@@ -1141,22 +1142,20 @@ k_gemm_few(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restri
   // 0), so that the main loop runs whole groups and keeps each weight set in its registers
   const int KT = (int)(K / 64), S = gridDim.z, z = blockIdx.z;
   const int kt0 = WD * (int)((int64_t)(KT / WD) * z / S), kt1 = WD * (int)((int64_t)(KT / WD) * (z + 1) / S);
-  // X: load i of thread t is tile row 64 i + t/8, LDS chunk t%8 holding global chunk (t%8) ^
-  // chunk_swz(row) (chunk_swz(64 i + t/8) = chunk_swz(t/8)); its LDS place i 8192 + 16 t
-  const __amdgpu_buffer_rsrc_t xrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(X + m0 * lda), 0, (int)(max((int64_t)0, M - m0) * lda * 2), 0x00020000);
+  // X(t) into stage st by the LDS DMA: round i of thread t (wave w, lane l) moves 16 bytes of tile
+  // row 64 i + t/8 (= 64 i + 8 w + l/8) into LDS chunk t%8 of that row, global chunk (t%8) ^
+  // chunk_swz(row) (chunk_swz(64 i + t/8) = chunk_swz(t/8)): a wave's round is 1 KB at i 8192 +
+  // 1024 w of the stage.  The row's offset rides in the vector offset, which the buffer's range
+  // check covers, so rows past M read as zeros
   uint32_t xoff[XR];
 #pragma unroll
   for (int i = 0; i < XR; ++i)
     xoff[i] = (uint32_t)(((64 * i + (tid >> 3)) * lda + 8 * ((tid & 7) ^ chunk_swz(tid >> 3))) * 2);
-  u32x4 xv[XR];
-  auto x_load = [&](int t) {
+  const uint32_t xext = (uint32_t)(max((int64_t)0, M - m0) * lda * 2);
+  auto x_dma = [&](int t, int st) {
 #pragma unroll
-    for (int i = 0; i < XR; ++i) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i], t * 128, 0);
-  };
-  auto x_store = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < XR; ++i) *(u32x4*)(smem + st * XST + i * 8192 + tid * 16) = xv[i];
+    for (int i = 0; i < XR; ++i)
+      tile_dma(X + m0 * lda, xext, (lds_void*)(smem + st * XST + i * 8192 + wave * 1024), xoff[i], t * 128);
   };
   // W: fragment j of the wave is tile rows f0 + JS j .. +15 (lane l: row + l%16)
   constexpr int JS = SWI ? 32 : 16;
@@ -1232,35 +1231,36 @@ k_gemm_few(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restri
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  // step t (W(t) in register set t%4, its B operands in bq[t%2], X(t + 1) in xv): the barrier
-  // (X(t) stored, the other stage free), W(t + 4) loaded into set t%4, X(t)'s fragments read, the
-  // MFMAs with W(t + 1) converted between them, X(t + 1) stored and X(t + 2) loaded.  The order
-  // is for the in-order wait counter: the wait for X(t + 1) (loaded at step t - 1's end) leaves
-  // every later weight load outstanding and forces only W(t + 3), loaded two steps before.
-  // Past the end the loads repeat the last step and nothing reads them.
+  // step t (W(t) in register set t%4, its B operands in bq[t%2]): the wait for X(t)'s DMA and
+  // the barrier (X(t) in its stage for every wave, the other stage free), X(t + 1)'s DMA into
+  // that stage, W(t + 4) loaded into set t%4, X(t)'s fragments read, the MFMAs with W(t + 1)
+  // converted between them.  The order is for the in-order wait counter: the wait for X(t)
+  // leaves step t - 1's weight loads outstanding and forces only W(t + 2) and before.  Past the
+  // end the loads repeat the last step and nothing reads them.
   auto step = [&](auto uc, int t) {
     constexpr int u = decltype(uc)::value;
     using Cur = std::integral_constant<int, u % 2>;
     using Nb = std::integral_constant<int, (u + 1) % 2>;
     using Ns = std::integral_constant<int, (u + 1) % WD>;
+    // X(t)'s DMA (issued at step t - 1's start) has landed: only step t - 1's 4 weight loads
+    // may be outstanding; then the barrier makes every wave's DMA visible
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((4 & 15) | (0x7 << 4) | (0xF << 8));
     __syncthreads();
     const int st = (t - kt0) & 1;
+    x_dma(min(t + 1, kt1 - 1), st ^ 1);
+    __builtin_amdgcn_sched_barrier(0);   // the DMA before the weight loads: the wait above counts on it
     w_load(uc, min(t + WD, kt1 - 1));
 #pragma unroll
     for (int i = 0; i < MI; ++i) a_read(st, 0, i);
     mfma_slice(Cur{}, Ns{}, Nb{}, 0, st);
     mfma_slice(Cur{}, Ns{}, Nb{}, 1, st);
-    x_store(st ^ 1);
-    x_load(min(t + 2, kt1 - 1));
   };
-  // the prologue in the same order: the weights, then X(kt0 + 1) last
-  x_load(kt0);
+  x_dma(kt0, 0);
   w_load(I0{}, kt0);
   w_load(I1{}, min(kt0 + 1, kt1 - 1));
   w_load(I2{}, min(kt0 + 2, kt1 - 1));
   w_load(I3{}, min(kt0 + 3, kt1 - 1));
-  x_store(0);
-  x_load(min(kt0 + 1, kt1 - 1));
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -1272,7 +1272,10 @@ k_gemm_few(const uint16_t* __restrict__ X, int64_t lda, const uint16_t* __restri
     step(I2{}, t + 2);
     step(I3{}, t + 3);
   }
-  __syncthreads();   // every wave done with the stages before the epilogue takes the LDS
+  // every DMA landed (the last step's spare one too) and every wave done with the stages before
+  // the epilogue takes the LDS
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));
+  __syncthreads();
   const int64_t wrow0 = m0 + wm * 128;
   if constexpr (SWI) {
     // output column n0/2 + 32 (wn/2) + 16 (wn%2) + l%16 (gate row 64 (wn/2) + 16 (wn%2) + l%16 of
