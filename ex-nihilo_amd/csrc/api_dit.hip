@@ -901,24 +901,31 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
     // the QKV product with qk-norm, RoPE and the K/V^T stores in its epilogue (bf16 or Q8_0
     // weights), else (shapes the fused path does not take) the product to fp16 rows and
     // qkv_prep over them.  An uncached pass's prompt rows (at most 256) go apart first, through
-    // the few-row product to fp16 rows and qkv_prep, so that the image rows' fused product runs
+    // the few-row product with its K split, whose partial sums qkv_prep_part reads (fp16 rows and
+    // qkv_prep where the product ran whole), so that the image rows' fused product runs
     // whole waves of tiles (4096 rows: 768 tiles, 3 waves, where the 256 prompt rows with them
     // make 816, a fourth wave of 48).  Every pass computes its image rows alike.
     int64_t qh = 0;   // the rows done apart
     if (nh > 0 && nh < n && nh <= 256) {
+      int ns = 0;   // the partial sums left in part (0: fp16 rows in qkv)
       {
         ProfScope ps(d, EXN_PROF_QKV, 2.0 * nh * 3 * Wd * Wd, nh * Wd * 2 + 3 * Wd * Wd * 1.0625 + nh * 3 * Wd * 2);
         ea = EpiArgs{};
         ea.y = qkv;
         ea.ldy = 3 * EXN_W;
-        const hipError_t r =
-            gemm_split_rows(s, y, EXN_W, wop_n(L.qkv, nh), nh, 3 * EXN_W, EXN_W, EPI_F16, ea, part, kSplitCap);
+        const hipError_t r = gemm_split_rows(s, y, EXN_W, wop_n(L.qkv, nh), nh, 3 * EXN_W, EXN_W, EPI_F16, ea, part,
+                                             kSplitCap, 8, &ns);
         if (r != hipErrorNotSupported) HIPCHK(r);
         if (r == hipSuccess) qh = nh;
       }
       if (qh) {
-        ProfScope ps(d, EXN_PROF_QKV_PREP, 0, (double)nh * (3 * Wd * 2 * 2 + 128 * 4));
-        HIPCHK(qkv_prep(s, qkv, nh, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap, n));
+        ProfScope ps(d, EXN_PROF_QKV_PREP, 0, (double)nh * (3 * Wd * (ns > 0 ? 4.0 * ns : 2.0) + 3 * Wd * 2 + 128 * 4));
+        if (ns > 0)
+          HIPCHK(qkv_prep_part(s, part, ns, nh, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0,
+                               d->lcap, n));
+        else
+          HIPCHK(qkv_prep(s, qkv, nh, L.norm_q, L.norm_k, d->cs, q, d->kc[(size_t)il], d->vt[(size_t)il], n0, d->lcap,
+                          n));
       }
     }
     const double nq = nd - (double)qh;

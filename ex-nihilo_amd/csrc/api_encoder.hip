@@ -354,34 +354,53 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
   float* part = nullptr;
   const bool split = n <= 1024;
   TRY(enc_buf(e, "part", (size_t)kSplitCap * 4, (void**)&part));
-  auto mm = [&](const exn_w* w, const uint16_t* xin, int64_t lda, Epi epi, const EpiArgs& a) -> hipError_t {
-    if (split || ((int64_t)n + 255) / 256 * ((w->rows + 255) / 256) < 192) {
-      const hipError_t r = gemm_split_rows(s, xin, lda, wop_n(w, n), n, w->rows, w->cols, epi, a, part, kSplitCap);
+  auto splits = [&](const exn_w* w) { return split || ((int64_t)n + 255) / 256 * ((w->rows + 255) / 256) < 192; };
+  // the product through EPI; with NSUM, a split product's sums are left in PART for the caller
+  // (*NSUM partials, 0 where it ran whole)
+  auto mm = [&](const exn_w* w, const uint16_t* xin, int64_t lda, Epi epi, const EpiArgs& a,
+                int* nsum = nullptr) -> hipError_t {
+    if (nsum) *nsum = 0;
+    if (splits(w)) {
+      const hipError_t r =
+          gemm_split_rows(s, xin, lda, wop_n(w, n), n, w->rows, w->cols, epi, a, part, kSplitCap, 8, nsum);
       if (r != hipErrorNotSupported) return r;
     }
     return gemm_any(s, w, xin, lda, n, epi, a);
+  };
+  // a gated-residual product into x, then the RMS norm NW of the new rows into y: a split
+  // product's sums and the norm in one pass
+  auto mm_norm = [&](const exn_w* w, const uint16_t* xin, int64_t lda, const EpiArgs& a, const float* nw) -> hipError_t {
+    int ns = 0;
+    const hipError_t r = mm(w, xin, lda, EPI_GATE_ADD, a, &ns);
+    if (r != hipSuccess) return r;
+    if (ns > 0) return split_sum_rms(s, ns, n, w->rows, part, a, 1e-6f, nw, y);
+    return rms_norm(s, n, EXN_W, 1e-6f, x, nw, y, 1);
   };
   HIPCHK(enc_embed(s, ids, n, e->vocab, e->eqs, e->ed, e->ef, EXN_W, x));
   if (m > 0)
     HIPCHK(hipMemcpyAsync(x + (int64_t)pic0 * EXN_W, merged, (size_t)m * EXN_W * 4, hipMemcpyDeviceToDevice, s));
   EpiArgs ea;
+  if (e->layers > 0) HIPCHK(rms_norm(s, n, EXN_W, 1e-6f, x, e->L[0].vec[E_ATTN_NORM], y, 1));
   for (int il = 0; il < e->layers; ++il) {
     const EncLayer& L = e->L[(size_t)il];
-    HIPCHK(rms_norm(s, n, EXN_W, 1e-6f, x, L.vec[E_ATTN_NORM], y, 1));
-    // q | k | v of the 8 key/value heads into fp16 rows, then the q/k norms, the rotary and the
-    // K/V stores, each key/value head for its 4 query heads
+    // y: the layer's attention-normed rows.  q | k | v of the 8 key/value heads (fp16 rows, or
+    // the split product's partial sums), then the q/k norms, the rotary and the K/V stores, each
+    // key/value head for its 4 query heads
     ea = EpiArgs{};
     ea.y = qkv;
     ea.ldy = EXN_W + 2 * kEncKV;
-    HIPCHK(mm(L.qkv, y, EXN_W, EPI_F16, ea));
-    HIPCHK(qkv_prep(s, qkv, n, L.vec[E_QNORM], L.vec[E_KNORM], cs, q, kc, vt, 0, lcap, n, kEncGroup));
+    int ns = 0;
+    HIPCHK(mm(L.qkv, y, EXN_W, EPI_F16, ea, &ns));
+    if (ns > 0)
+      HIPCHK(qkv_prep_part(s, part, ns, n, L.vec[E_QNORM], L.vec[E_KNORM], cs, q, kc, vt, 0, lcap, n, kEncGroup));
+    else
+      HIPCHK(qkv_prep(s, qkv, n, L.vec[E_QNORM], L.vec[E_KNORM], cs, q, kc, vt, 0, lcap, n, kEncGroup));
     HIPCHK(attend(s, q, kc, vt, att, n, 0, n, n, lcap, 0, 0, 1.f));
     ea = EpiArgs{};
     ea.resid = x;
     ea.ldy = EXN_W;
     ea.gate = e->one_gate;
-    HIPCHK(mm(L.out, att, EXN_W, EPI_GATE_ADD, ea));
-    HIPCHK(rms_norm(s, n, EXN_W, 1e-6f, x, L.vec[E_FFN_NORM], y, 1));
+    HIPCHK(mm_norm(L.out, att, EXN_W, ea, L.vec[E_FFN_NORM]));
     ea = EpiArgs{};
     ea.y = ff;
     ea.ldy = EXN_F;
@@ -390,10 +409,18 @@ static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, in
     ea.resid = x;
     ea.ldy = EXN_W;
     ea.gate = e->one_gate;
+    // the next layer's attention norm goes with the sums, unless a picture's deep rows are
+    // added in between
+    const bool deep_add = m > 0 && il < 3 && deep;
+    if (il + 1 < e->layers && !deep_add) {
+      HIPCHK(mm_norm(L.down, ff, EXN_F, ea, e->L[(size_t)il + 1].vec[E_ATTN_NORM]));
+      continue;
+    }
     HIPCHK(mm(L.down, ff, EXN_F, EPI_GATE_ADD, ea));
-    if (m > 0 && il < 3 && deep)
+    if (deep_add)
       HIPCHK(gate_add(s, (int64_t)m * EXN_W, EXN_W, 0, 0, 0, x + (int64_t)pic0 * EXN_W, deep + (int64_t)il * m * EXN_W,
                       e->one_gate));
+    if (il + 1 < e->layers) HIPCHK(rms_norm(s, n, EXN_W, 1e-6f, x, e->L[(size_t)il + 1].vec[E_ATTN_NORM], y, 1));
   }
   HIPCHK(hipMemcpyAsync(out, x, (size_t)n * EXN_W * 4, hipMemcpyDeviceToDevice, s));
   return EXN_OK;

@@ -108,6 +108,72 @@ hipError_t rms_norm(hipStream_t s, int n, int width, float eps, const float* x, 
   return hipGetLastError();
 }
 
+// The S partial sums of a split product (PART: S x M x 4096 floats, in order) into the gated
+// residual rows X (ldx; x += tanh(gate) * sum, the gate row as the product's EPI_GATE_ADD takes
+// it), then each finished row's RMS norm times W into bf16 Y (4096 wide): the split sum's and
+// rms_norm's arithmetic in one pass over the rows.  One block a row; thread t takes columns
+// 4t + 1024j in both passes, as both separate kernels do, so the values are theirs bit for bit.
+// The row's 4 S partial loads go out before any sum.
+template <int S>
+__global__ void __launch_bounds__(256)
+k_sum_rms(int64_t M, const float* __restrict__ part, float* __restrict__ x, int64_t ldx, const float* __restrict__ gate,
+          int n0, int p, int mstride, float eps, const float* __restrict__ w, uint16_t* __restrict__ y) {
+  constexpr int64_t N = 4096;
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x;
+  float* r = x + m * ldx;
+  const float* gr = gate + (n0 + m < p ? mstride : 0);
+  f32x4 pv[4][S], xv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t c = 4 * tid + 1024 * j;
+#pragma unroll
+    for (int z = 0; z < S; ++z) pv[j][z] = *(const f32x4*)(part + ((int64_t)z * M + m) * N + c);
+    xv[j] = *(const f32x4*)(r + c);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t c = 4 * tid + 1024 * j;
+    f32x4 v = pv[j][0];
+#pragma unroll
+    for (int z = 1; z < S; ++z) v += pv[j][z];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xv[j][e] = xv[j][e] + tanh_f(gr[c + e]) * v[e];
+    *(f32x4*)(r + c) = xv[j];
+    ss += xv[j][0] * xv[j][0] + xv[j][1] * xv[j][1] + xv[j][2] * xv[j][2] + xv[j][3] * xv[j][3];
+  }
+  const float inv = rsqrtf(block_sum256(ss, red) / (float)N + eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t c = 4 * tid + 1024 * j;
+    const f32x4 wv = *(const f32x4*)(w + c);
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = xv[j][e] * inv * wv[e];
+    *(u32x2*)(y + m * N + c) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+  }
+}
+
+hipError_t split_sum_rms(hipStream_t s, int S, int64_t M, int64_t N, const float* part, const EpiArgs& ea, float eps,
+                         const float* w, uint16_t* y) {
+  if (M == 0) return hipSuccess;
+  if (S < 1 || S > 8 || N != 4096 || ea.ldy % 4) return hipErrorInvalidValue;
+  const dim3 g((unsigned)M);
+  switch (S) {
+#define EXN_SUM_RMS_S(k)                                                                                             \
+  case k:                                                                                                            \
+    hipLaunchKernelGGL(k_sum_rms<k>, g, dim3(256), 0, s, M, part, ea.resid, ea.ldy, ea.gate, ea.n0, ea.p, ea.mstride, \
+                       eps, w, y);                                                                                   \
+    break;
+    EXN_SUM_RMS_S(1) EXN_SUM_RMS_S(2) EXN_SUM_RMS_S(3) EXN_SUM_RMS_S(4) EXN_SUM_RMS_S(5) EXN_SUM_RMS_S(6)
+    EXN_SUM_RMS_S(7) EXN_SUM_RMS_S(8)
+#undef EXN_SUM_RMS_S
+  }
+  return hipGetLastError();
+}
+
 // 4 values a thread; COUNT a multiple of 4 and WIDTH of 4
 __global__ void k_gate_add(int64_t count4, int width, int n0, int p, int mstride, float* __restrict__ x,
                            const float* __restrict__ h, const float* __restrict__ gate) {
@@ -205,15 +271,42 @@ hipError_t silu(hipStream_t s, int64_t count, float* x) {
 // rotation), k into kc ([32][lcap][128]) rows row0.., v transposed into vt
 // ([32][128][lcap]) columns row0.., query head h taking key/value head h / G.  cs:
 // cos, sin for 64 pairs, 128 floats a sequence row.  grid (ceil(n/64), 32), block 256.
+// S > 0: the rows are those a split product's S partial sums (S x n rows of fp32, in order)
+// give through its fp16 store -- the same sums, in the same order, rounded once -- read from
+// the partials (all S of a value's loads out before its sum) instead of fp16 rows written and
+// read back
+template <int S>
 __global__ void __launch_bounds__(256)
-k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict__ wq, const float* __restrict__ wk,
-           const float* __restrict__ cs, float qscale, uint16_t* __restrict__ q, uint16_t* __restrict__ kc,
-           uint16_t* __restrict__ vt, int64_t row0, int64_t lcap, int64_t qld, int g) {
+k_qkv_prep(const uint16_t* __restrict__ qkv, const float* __restrict__ part, int64_t n,
+           const float* __restrict__ wq, const float* __restrict__ wk, const float* __restrict__ cs, float qscale,
+           uint16_t* __restrict__ q, uint16_t* __restrict__ kc, uint16_t* __restrict__ vt, int64_t row0, int64_t lcap,
+           int64_t qld, int g) {
   __shared__ uint16_t tile[64][128 + 2];
   const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t ld = 4096 + 2 * (4096 / g);                      // a row of qkv
   const int64_t ko = 4096 + (h / g) * 128, vo = ko + 4096 / g;   // this head's k and v in it
   const int64_t t0 = (int64_t)blockIdx.x * 64;
+  // the 8 fp16 values of token TC's row at column COL
+  auto ld8 = [&](int64_t tc, int64_t col) -> u32x4 {
+    if constexpr (S == 0) {
+      return *(const u32x4*)(qkv + tc * ld + col);
+    } else {
+      const float* p0 = part + tc * ld + col;
+      f32x4 pa[S], pb[S];
+#pragma unroll
+      for (int z = 0; z < S; ++z) {
+        pa[z] = *(const f32x4*)(p0 + (int64_t)z * n * ld);
+        pb[z] = *(const f32x4*)(p0 + (int64_t)z * n * ld + 4);
+      }
+      f32x4 a = pa[0], b = pb[0];
+#pragma unroll
+      for (int z = 1; z < S; ++z) {
+        a += pa[z];
+        b += pb[z];
+      }
+      return u32x4{pack_f16x2(a[0], a[1]), pack_f16x2(a[2], a[3]), pack_f16x2(b[0], b[1]), pack_f16x2(b[2], b[3])};
+    }
+  };
   // q and k: 16 lanes a token, lane holding dims d8 .. d8+7 (its 4 rotation pairs) as one
   // 16-byte load and store; a wave takes 4 tokens a round, its 16 tokens in 4 rounds whose
   // loads are all issued first.  The RMS sum is a reduction over the 16 lanes.
@@ -229,9 +322,8 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int64_t tc = min(t0 + wave * 16 + it * 4 + sub, n - 1);   // rows past n: loaded, not stored
-    const uint16_t* rq = qkv + tc * ld + d8;
-    uq[it] = *(const u32x4*)(rq + h * 128);
-    uk[it] = *(const u32x4*)(rq + ko);
+    uq[it] = ld8(tc, h * 128 + d8);
+    uk[it] = ld8(tc, ko + d8);
     const float* cr = cs + (row0 + tc) * 128 + d8;   // cos, sin of pairs d8/2 .. d8/2 + 3
     ca[it] = *(const f32x4*)cr;
     cb[it] = *(const f32x4*)(cr + 4);
@@ -277,7 +369,7 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, int64_t n, const float* __restrict_
     const int c = tid + 256 * i, tok = c >> 4, d8 = (c & 15) * 8;
     const int64_t t = t0 + tok;
     u32x4 v = u32x4{0, 0, 0, 0};
-    if (t < n) v = *(const u32x4*)(qkv + t * ld + vo + d8);
+    if (t < n) v = ld8(t, vo + d8);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       *(uint32_t*)&tile[tok][d8 + 2 * e] = v[e];
@@ -299,8 +391,26 @@ hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* 
   if (kv_group != 1 && kv_group != 4) return hipErrorInvalidValue;
   // q is scaled by 1/sqrt(128) * log2(e): the attention's scores are then in log2 units
   const float qscale = QK_QSCALE;
-  hipLaunchKernelGGL(k_qkv_prep, dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, n, wq, wk, cs, qscale, q, k, vt,
-                     row0, lcap, qld, kv_group);
+  hipLaunchKernelGGL(k_qkv_prep<0>, dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, nullptr, n, wq, wk, cs, qscale, q,
+                     k, vt, row0, lcap, qld, kv_group);
+  return hipGetLastError();
+}
+
+hipError_t qkv_prep_part(hipStream_t s, const float* part, int S, int64_t n, const float* wq, const float* wk,
+                         const float* cs, uint16_t* q, uint16_t* k_, uint16_t* vt, int64_t row0, int64_t lcap,
+                         int64_t qld, int kv_group) {
+  if (n == 0) return hipSuccess;
+  if ((kv_group != 1 && kv_group != 4) || S < 1 || S > 8) return hipErrorInvalidValue;
+  const dim3 g(grid_of(n, 64), 32);
+  switch (S) {
+#define EXN_PREP_S(k)                                                                                        \
+  case k:                                                                                                    \
+    hipLaunchKernelGGL(k_qkv_prep<k>, g, dim3(256), 0, s, nullptr, part, n, wq, wk, cs, QK_QSCALE, q, k_, vt, \
+                       row0, lcap, qld, kv_group);                                                           \
+    break;
+    EXN_PREP_S(1) EXN_PREP_S(2) EXN_PREP_S(3) EXN_PREP_S(4) EXN_PREP_S(5) EXN_PREP_S(6) EXN_PREP_S(7) EXN_PREP_S(8)
+#undef EXN_PREP_S
+  }
   return hipGetLastError();
 }
 

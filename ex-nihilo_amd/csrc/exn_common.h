@@ -203,9 +203,12 @@ hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint1
                       int64_t M, int64_t N, int64_t K, Epi epi, const EpiArgs& ea);
 // rows 0 .. M-1 of a product too short to fill the chip (a pass's prompt rows) with its K split
 // over S workgroups a tile into PART (S x M x N floats, at most PART_CAP), then the sums in
-// order through the epilogue: EPI_GATE_ADD, EPI_SWIGLU, EPI_F32, EPI_BF16 or EPI_F16; bf16 weights
+// order through the epilogue: EPI_GATE_ADD, EPI_SWIGLU, EPI_F32, EPI_BF16 or EPI_F16.  With
+// NSUM the sums are left to the caller (split_sum_rms, qkv_prep_part): *NSUM = S, or 0 where
+// the product ran whole through the epilogue instead
 hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
-                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap, int smax = 8);
+                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap, int smax = 8,
+                           int* nsum = nullptr);
 // the QKV product with the q/k norm, RoPE and the K/V^T stores fused (EPI_QKV), bf16 or Q8_0
 // weights; hipErrorNotSupported when the shapes or alignments do not fit the fused path
 hipError_t gemm_qkv(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t K,
@@ -233,6 +236,10 @@ hipError_t f32_to_bf16(hipStream_t s, const float* x, uint16_t* y, int64_t n);
 hipError_t ln_mod(hipStream_t s, int n, int n0, int p, int mstride, const float* x, int64_t ldx,
                   const float* mod, void* out, int out_bf16);
 hipError_t rms_norm(hipStream_t s, int n, int width, float eps, const float* x, const float* w, void* out, int out_bf16);
+// a split product's S partial sums (S x M x N, S <= 8, N = 4096) through EPI_GATE_ADD's store
+// into EA's residual, then rms_norm of the finished rows (W, EPS) into bf16 Y, in one pass
+hipError_t split_sum_rms(hipStream_t s, int S, int64_t M, int64_t N, const float* part, const EpiArgs& ea, float eps,
+                         const float* w, uint16_t* y);
 hipError_t gate_add(hipStream_t s, int64_t count, int width, int n0, int p, int mstride, float* x, const float* h,
                     const float* gate);
 hipError_t swiglu(hipStream_t s, int64_t n, int f, const uint16_t* gu, uint16_t* out);
@@ -242,6 +249,11 @@ hipError_t silu(hipStream_t s, int64_t count, float* x);
 hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* wq, const float* wk,
                     const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap,
                     int64_t qld, int kv_group = 1);
+// qkv_prep on the fp16 rows a split QKV product's S partial sums (S x n rows, in order, S <= 8)
+// make
+hipError_t qkv_prep_part(hipStream_t s, const float* part, int S, int64_t n, const float* wq, const float* wk,
+                         const float* cs, uint16_t* q, uint16_t* k, uint16_t* vt, int64_t row0, int64_t lcap,
+                         int64_t qld, int kv_group = 1);
 hipError_t latent_rows(hipStream_t s, const float* latent, int64_t nimg, float* rows);
 hipError_t rows_to_latent(hipStream_t s, const float* rows, int64_t nimg, float* latent);
 hipError_t euler(hipStream_t s, int64_t count, float* z, const float* v, float ds);

@@ -1417,7 +1417,8 @@ static hipError_t split_sum(hipStream_t s, Epi epi, int S, int64_t M, int64_t N,
 }
 
 hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
-                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap, int smax) {
+                           int64_t K, Epi epi, const EpiArgs& ea, float* part, int64_t part_cap, int smax, int* nsum) {
+  if (nsum) *nsum = 0;
   if (M == 0) return hipSuccess;
   auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   const bool epi_ok = epi == EPI_GATE_ADD || epi == EPI_SWIGLU || epi == EPI_F32 || epi == EPI_BF16 || epi == EPI_F16;
@@ -1436,6 +1437,10 @@ hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const 
     pa.ldy = N;
     const hipError_t e = launch_few_w<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
     if (e != hipSuccess) return e;
+    if (nsum) {
+      *nsum = (int)S;
+      return hipSuccess;
+    }
     return split_sum(s, epi, (int)S, M, N, part, ea);
   }
   // S workgroups a tile, about one wave in all, at least 4 k-steps each, at most SMAX (in a DiT
@@ -1455,6 +1460,10 @@ hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const 
   if (!ok) return hipErrorNotSupported;
   hipError_t e = launch_w<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
   if (e != hipSuccess) return e;
+  if (nsum) {
+    *nsum = (int)S;
+    return hipSuccess;
+  }
   return split_sum(s, epi, (int)S, M, N, part, ea);
 }
 
