@@ -861,7 +861,8 @@ __device__ __forceinline__ void buffer_load_u32_into(uint32_t& v, i32x4 rsrc, ui
 //   16 KB, written by the dequantisation); two stages fill the 160 KB of LDS, so the codes go to
 //   registers: thread t loads the 16 codes of tile row t/4, k 16 (t%4) .. +15 (one 16-byte load,
 //   a wave's 64 one contiguous KB of the tiled operand) and the dword of that row's two scales,
-//   a step ahead, and converts them into the W tile of step t+2 once B1 has freed it.
+//   two steps ahead into one of two register sets (the step's parity: the loop runs steps in
+//   pairs), and converts them into the W tile of step t+2 once B1 has freed it.
 // The tiled operand's 256-row chunks hold two 128-row tiles: tile bn is chunk bn/2, rows
 // 128 (bn%2) .. (codes at 8 KB (bn%2), scales at QT_SCALES + 512 (bn%2)).
 template <int EPI>
@@ -872,6 +873,8 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
   constexpr int WM = HEADS ? 64 : 128, WN = HEADS ? 128 : 64, MI = WM / 16, NI = WN / 16;
   static_assert((512 / WM) * (128 / WN) == 8, "the waves tile 512 x 128");
   constexpr int NMF = MI * NI, NRD = MI + NI, XPARTS = 8, STAGE = 81920, WOFF = 65536;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
   extern __shared__ __align__(1024) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -911,19 +914,25 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
   const uint32_t coff = (uint32_t)((bn & 1) * 8192 + tid * 16);
   const uint32_t soff = (uint32_t)(QT_SCALES + (bn & 1) * 512 + (tid >> 2) * 4);
   const int dq_row = tid >> 2, dq_q = tid & 3;
-  u32x4 cq = {0u, 0u, 0u, 0u};
-  uint32_t sq = 0;
-  auto code_load = [&](int t) {
-    buffer_load_u128_into(cq, qrsrc, coff, (uint32_t)(t * QT_CHUNK));
-    buffer_load_u32_into(sq, qrsrc, soff, (uint32_t)(t * QT_CHUNK));
+  // two register sets, one for each step parity
+  u32x4 cq0 = {0u, 0u, 0u, 0u}, cq1 = {0u, 0u, 0u, 0u};
+  uint32_t sq0 = 0, sq1 = 0;
+  auto code_load = [&](auto bc, int t) {
+    if constexpr (decltype(bc)::value == 0) {
+      buffer_load_u128_into(cq0, qrsrc, coff, (uint32_t)(t * QT_CHUNK));
+      buffer_load_u32_into(sq0, qrsrc, soff, (uint32_t)(t * QT_CHUNK));
+    } else {
+      buffer_load_u128_into(cq1, qrsrc, coff, (uint32_t)(t * QT_CHUNK));
+      buffer_load_u32_into(sq1, qrsrc, soff, (uint32_t)(t * QT_CHUNK));
+    }
   };
   // conversion h (0, 1): codes 8h .. 8h+7 of the thread's 16 into the 16-byte chunk of bf16 at
   // k 16 q + 8h, one store a chunk: the 16 lanes of a store quarter-wave (4 rows x 4 quarters)
   // then fill 16 distinct (row parity, chunk) places, so the stores are free of bank conflicts
   // (8-byte stores of half chunks met in pairs and cost about 8% of the product)
   float dq_d = 0.f;
-  auto dq_scale = [&]() { dq_d = f16_to_f32((sq >> (16 * (dq_q >> 1))) & 0xFFFFu); };
-  auto dq_convert = [&](int h, int ws) {
+  auto dq_scale = [&](uint32_t sq) { dq_d = f16_to_f32((sq >> (16 * (dq_q >> 1))) & 0xFFFFu); };
+  auto dq_convert = [&](const u32x4& cq, int h, int ws) {
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -956,16 +965,20 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
   // A step (k_gemm_bt's): MFMAs 0..NRD-1 read this step's second-slice fragments (stage cur);
   // B1: every wave is done with stage cur; the X DMA of step t+2 into it at XP0..XP7; at DQ0 the
   // codes' wait, then two conversions (DQ0, DQ0+4) of step t+2's codes into W stage cur;
-  // at CLP the codes and scales of step t+3 into the registers just read; B2: step t+1's X has
+  // at CLP the codes and scales of step t+4 into the register set just read (so they have two
+  // steps to land: one was 0.7% slower, the loads waited on at DQ0); B2: step t+1's X has
   // landed (its W was written a step before, behind this step's B1); then step t+1's first-slice
   // fragments from stage cur^1.  The waits leave out what ops_after counts from the positions.
   constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DQ0 = B1 + 10, CLP = DQ0 + 7;
   constexpr int QPOS[10] = {B1, B1 + 4, B1 + 8, B1 + 12, CLP, CLP + 1, B1 + 20, B1 + 24, B1 + 28, B1 + 32};
-  constexpr int DQ_VM = ops_after(CLP + 1, 1, DQ0, QPOS, 10), B2_VM = ops_after(B1 + 32, 1, B2, QPOS, 10);
+  constexpr int DQ_VM = ops_after(CLP + 1, 2, DQ0, QPOS, 10), B2_VM = ops_after(B1 + 32, 1, B2, QPOS, 10);
   static_assert(B1 >= NRD && B1 + 32 < B2 && B2 + NRD <= 2 * NMF && DQ0 > B1 + 8 && DQ0 + 6 < CLP &&
-                    CLP + 1 < B1 + 20 && DQ_VM < 16 && B2_VM < 16,
+                    CLP + 1 < B1 + 20 && DQ_VM < 64 && B2_VM < 64,
                 "step schedule");
-  auto step = [&](Frag& F0, Frag& F1, int t) {
+  auto step = [&](Frag& F0, Frag& F1, int t, auto bc) {
+    constexpr int P = decltype(bc)::value;
+    u32x4& cq = P ? cq1 : cq0;
+    uint32_t& sq = P ? sq1 : sq0;
     const int cur = (t - kt0) & 1, nx = min(t + 2, kt1 - 1);
     auto pos = [&](const int x) {
       if (x == B1) {
@@ -998,10 +1011,10 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
         // the loads are invisible to the compiler; this marks their registers as written here,
         // after the wait that covers them, so that no use of them moves above the wait
         asm volatile("" : "+v"(cq), "+v"(sq));
-        dq_scale();
+        dq_scale(sq);
       }
-      if (x == DQ0 || x == DQ0 + 4) dq_convert((x - DQ0) / 4, cur);
-      if (x == CLP) code_load(min(t + 3, kt1 - 1));
+      if (x == DQ0 || x == DQ0 + 4) dq_convert(cq, (x - DQ0) / 4, cur);
+      if (x == CLP) code_load(bc, min(t + 4, kt1 - 1));
       __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
@@ -1015,33 +1028,38 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
     const int t1 = min(kt0 + 1, kt1 - 1);
 #pragma unroll
     for (int p = 0; p < XPARTS; ++p) dma_part(kt0, 0, p);
-    code_load(kt0);
+    code_load(I0{}, kt0);
     LDS_VMCNT0_BARRIER();
-    asm volatile("" : "+v"(cq), "+v"(sq));
-    dq_scale();
+    asm volatile("" : "+v"(cq0), "+v"(sq0));
+    dq_scale(sq0);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) dq_convert(h, 0);
-    code_load(t1);
+    for (int h = 0; h < 2; ++h) dq_convert(cq0, h, 0);
+    code_load(I1{}, t1);
     LDS_VMCNT0_BARRIER();
-    asm volatile("" : "+v"(cq), "+v"(sq));
-    dq_scale();
+    asm volatile("" : "+v"(cq1), "+v"(sq1));
+    dq_scale(sq1);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) dq_convert(h, 1);
+    for (int h = 0; h < 2; ++h) dq_convert(cq1, h, 1);
+    // the codes of kt0 + 2 (step kt0 - 2's load) landed with the wait below; then step kt0 - 1's
+    // operations in position order: X of kt0 + 1, the codes of kt0 + 3
+    code_load(I0{}, min(kt0 + 2, kt1 - 1));
     LDS_VMCNT0_BARRIER();   // the codes read, stages 0 and 1 of W written, stage 0 of X landed
-    // step kt0 - 1's operations in position order: X of kt0 + 1, the codes of kt0 + 2
 #pragma unroll
     for (int x = 0; x < 2 * NMF; ++x) {
 #pragma unroll
       for (int p = 0; p < XPARTS; ++p)
         if (x == QPOS[p < 4 ? p : p + 2]) dma_part(t1, 1, p);
-      if (x == CLP) code_load(min(kt0 + 2, kt1 - 1));
+      if (x == CLP) code_load(I1{}, min(kt0 + 3, kt1 - 1));
     }
 #pragma unroll
     for (int q = 0; q < NRD; ++q) rd1(F0, 0, 0, q);
   }
-  for (int t = kt0; t < kt1; ++t) step(F0, F1, t);
+  for (int t = kt0; t < kt1; t += 2) {
+    step(F0, F1, t, I0{});
+    step(F0, F1, t + 1, I1{});
+  }
   LDS_VMCNT0_BARRIER();   // the last DMA and loads have landed before the epilogue takes the LDS over
-  asm volatile("" ::"v"(cq), "v"(sq));
+  asm volatile("" ::"v"(cq0), "v"(sq0), "v"(cq1), "v"(sq1));
   if constexpr (HEADS)
     epilogue_qkv<MI, NI>(acc, (float*)smem + wave * (16 * 132), m0 + wm * WM, n0 + wn * WN, lane, M, ea);
   else if constexpr (EPI == EPI_SWIGLU)
