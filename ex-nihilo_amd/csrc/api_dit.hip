@@ -959,42 +959,50 @@ static int velocity(exn_dit* d, const float* context, int ptext, const float* la
       HIPCHK(qkv_prep(s, qkv + qh * 3 * EXN_W, n - qh, L.norm_q, L.norm_k, d->cs, q + qh * EXN_HD, d->kc[(size_t)il],
                       d->vt[(size_t)il], n0 + qh, d->lcap, n));
     }
+    // The last block's prompt rows: once their K/V are kept (the QKV product above), nothing
+    // reads what the rest of the block makes of them -- the step's output is the image rows'
+    // -- so the attention and the products from here on take rows r0.. only, the image rows,
+    // tiled as in a cached pass.  A traced pass, or one recording its numbers, takes every row.
+    const int64_t r0 = il + 1 == d->layers && !d->trace && !st ? nh : 0;
+    const int64_t nr = n - r0, nhr = nh - r0;
+    const double ndr = (double)nr;
     {
-      ProfScope ps(d, EXN_PROF_ATTEND, 4.0 * EXN_HD * EXN_H * pairs, nd * Wd * 2 * 2 + 2.0 * l * Wd * 2);
-      HIPCHK(attend(s, q, d->kc[(size_t)il], d->vt[(size_t)il], att, (int)n, n0, p, (int)l, d->lcap, b0, b1, 1.f));
+      ProfScope ps(d, EXN_PROF_ATTEND, 4.0 * EXN_HD * EXN_H * pairs, ndr * Wd * 2 * 2 + 2.0 * l * Wd * 2);
+      HIPCHK(attend(s, q + r0 * EXN_HD, d->kc[(size_t)il], d->vt[(size_t)il], att + r0 * EXN_W, (int)nr, n0 + (int)r0,
+                    p, (int)l, d->lcap, b0, b1, 1.f, 0, n));
     }
     {
-      ProfScope ps(d, EXN_PROF_OUT, 2 * nd * Wd * Wd, nd * Wd * 2 + Wd * Wd * 1.0625 + nd * Wd * 4 * 2);
+      ProfScope ps(d, EXN_PROF_OUT, 2 * ndr * Wd * Wd, ndr * Wd * 2 + Wd * Wd * 1.0625 + ndr * Wd * 4 * 2);
       ea = EpiArgs{};
-      ea.resid = x;
+      ea.resid = x + r0 * EXN_W;
       ea.ldy = EXN_W;
       ea.gate = mod + 1 * EXN_W;
-      ea.n0 = n0;
+      ea.n0 = n0 + (int)r0;
       ea.p = p;
       ea.mstride = ms;
-      HIPCHK(block_mm(s, L.out, att, EXN_W, n, nh, EPI_GATE_ADD, ea, part));
+      HIPCHK(block_mm(s, L.out, att + r0 * EXN_W, EXN_W, nr, nhr, EPI_GATE_ADD, ea, part));
     }
     {
-      ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes);
-      HIPCHK(ln_mod(s, (int)n, n0, p, ms, x, EXN_W, mod + 2 * EXN_W, y, 1));
+      ProfScope ps(d, EXN_PROF_LN_MOD, 0, ln_bytes * ndr / nd);
+      HIPCHK(ln_mod(s, (int)nr, n0 + (int)r0, p, ms, x + r0 * EXN_W, EXN_W, mod + 2 * EXN_W, y + r0 * EXN_W, 1));
     }
     {
-      ProfScope ps(d, EXN_PROF_GATE_UP, 2 * nd * Wd * 2 * Fd, nd * Wd * 2 + 2 * Fd * Wd * 1.0625 + nd * Fd * 2);
+      ProfScope ps(d, EXN_PROF_GATE_UP, 2 * ndr * Wd * 2 * Fd, ndr * Wd * 2 + 2 * Fd * Wd * 1.0625 + ndr * Fd * 2);
       ea = EpiArgs{};
-      ea.y = ff;
+      ea.y = ff + r0 * EXN_F;
       ea.ldy = EXN_F;
-      HIPCHK(block_mm(s, L.gate_up, y, EXN_W, n, nh, EPI_SWIGLU, ea, part));
+      HIPCHK(block_mm(s, L.gate_up, y + r0 * EXN_W, EXN_W, nr, nhr, EPI_SWIGLU, ea, part));
     }
     {
-      ProfScope ps(d, EXN_PROF_DOWN, 2 * nd * Fd * Wd, nd * Fd * 2 + Fd * Wd * 1.0625 + nd * Wd * 4 * 2);
+      ProfScope ps(d, EXN_PROF_DOWN, 2 * ndr * Fd * Wd, ndr * Fd * 2 + Fd * Wd * 1.0625 + ndr * Wd * 4 * 2);
       ea = EpiArgs{};
-      ea.resid = x;
+      ea.resid = x + r0 * EXN_W;
       ea.ldy = EXN_W;
       ea.gate = mod + 3 * EXN_W;
-      ea.n0 = n0;
+      ea.n0 = n0 + (int)r0;
       ea.p = p;
       ea.mstride = ms;
-      HIPCHK(block_mm(s, L.down, ff, EXN_F, n, nh, EPI_GATE_ADD, ea, part));
+      HIPCHK(block_mm(s, L.down, ff + r0 * EXN_F, EXN_F, nr, nhr, EPI_GATE_ADD, ea, part));
     }
     HIPCHK(stat(il + 1, 0, x, 0, n * EXN_W));
     HIPCHK(stat(il + 1, 1, att, 1, n * EXN_W));

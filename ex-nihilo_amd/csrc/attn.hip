@@ -66,11 +66,11 @@ __device__ __forceinline__ float xsum32(float v) {
   return a + b;
 }
 
-// grid (ceil(n/128), 32 heads), block 256; O bf16, or fp32 when OF32
+// grid (ceil(n/128), 32 heads), block 256; O bf16, or fp32 when OF32; Q's heads QLD rows apart
 template <bool OF32>
 __global__ void __launch_bounds__(256, 2)
 k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vt,
-         void* __restrict__ O, int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale) {
+         void* __restrict__ O, int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale, int64_t qld) {
   // Two rings, one tile apart: K stage s (64 keys x 256 B) at s * 16 KB, V^T stage s (128 dims x
   // 128 B) at 32 KB + s * 16 KB.  Step t reads K of tile t+1 and V^T of tile t, so the DMA of K
   // t+2 and V^T t+1 go into the stages step t-1 read.
@@ -89,7 +89,7 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
   // Q^T as the B operand: 8 steps of 16 dims, this lane's query, dims 16s + 8*hi ..
   f16x8 qf[8];
   {
-    const uint16_t* qr = Q + ((int64_t)h * n + tqc) * 128 + 8 * hi;
+    const uint16_t* qr = Q + ((int64_t)h * qld + tqc) * 128 + 8 * hi;
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = *(const f16x8*)(qr + 16 * s);
   }
@@ -318,16 +318,18 @@ k_attend(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const 
 }
 
 hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, void* out, int n,
-                  int q0, int p, int l, int64_t lcap, int b0, int b1, float scale, int of32) {
+                  int q0, int p, int l, int64_t lcap, int b0, int b1, float scale, int of32, int64_t qld) {
   if (n <= 0) return hipSuccess;
+  if (qld == 0) qld = n;
+  if (qld < n) return hipErrorInvalidValue;
   // the DMA reads whole 64-key tiles: keys up to roundup(l, 64) - 1 must lie inside lcap
   // and a head's K (or V^T) is one buffer of lcap * 256 bytes
   if (lcap % AK || l > lcap || l <= 0 || lcap > (1 << 22)) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((n + AQ - 1) / AQ), 32);
   if (of32)
-    hipLaunchKernelGGL(k_attend<true>, grid, dim3(256), 0, s, q, k, vt, out, n, q0, p, l, lcap, b0, b1, scale);
+    hipLaunchKernelGGL(k_attend<true>, grid, dim3(256), 0, s, q, k, vt, out, n, q0, p, l, lcap, b0, b1, scale, qld);
   else
-    hipLaunchKernelGGL(k_attend<false>, grid, dim3(256), 0, s, q, k, vt, out, n, q0, p, l, lcap, b0, b1, scale);
+    hipLaunchKernelGGL(k_attend<false>, grid, dim3(256), 0, s, q, k, vt, out, n, q0, p, l, lcap, b0, b1, scale, qld);
   return hipGetLastError();
 }
 

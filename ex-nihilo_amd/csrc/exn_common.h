@@ -267,8 +267,10 @@ hipError_t quant_q8(hipStream_t s, const void* x, int xbf16, int64_t ldx, int64_
                     uint16_t* d);
 hipError_t gemm_w8a8(hipStream_t s, const int8_t* xq, const uint16_t* xd, int64_t M, const int8_t* wq,
                      const uint16_t* wd, int64_t N, int64_t K, void* y, int64_t ldy, int f16out);
+// Q [32][QLD][128] (QLD 0: N), queries Q0 .. Q0 + N - 1 over keys 0 .. L - 1 under xa_lim
 hipError_t attend(hipStream_t s, const uint16_t* q, const uint16_t* k, const uint16_t* vt, void* out,
-                  int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale, int of32 = 0);
+                  int n, int q0, int p, int l, int64_t lcap, int b0, int b1, float scale, int of32 = 0,
+                  int64_t qld = 0);
 
 // the VAE decoder (vae.hip).  vae_conv's outputs: fp32 (+ bias, + res when given), bf16 (+ bias,
 // + res when given), fp32 (+ bias) clamped to -1 .. 1, fp32 (+ bias, + DupUp3D of keep: kcin
