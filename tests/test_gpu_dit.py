@@ -149,6 +149,24 @@ def test_prefix_cache_follows_the_weights_and_the_prompt(ctx):
     d.destroy()
 
 
+@pytest.mark.parametrize("p,h,w", [(20, 4, 6), (256, 32, 32)])
+def test_last_block_image_rows_alone(ctx, p, h, w):
+    """An uncached pass's last block runs its attention and products on the image rows alone
+    (nothing reads the prompt rows past their kept K/V); a pass recording exn_dit_stats takes
+    every row.  Both give the same velocity bit for bit, and so does a cached pass over the
+    K/V the shortened pass kept."""
+    say("last block on the image rows: p", p, "image", h, "x", w)
+    d = model(ctx, 3, 5)
+    ctxa, lat = xo.synth_inputs(5, p, h, w)
+    v_short = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7, prefix_key="k")
+    v_cached = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7, prefix_key="k")
+    d.stats(True)
+    v_full = X.dit_velocity(d, ctxa, p, lat, h, w, 0.7)
+    d.stats(False)
+    assert np.array_equal(v_short, v_full) and np.array_equal(v_cached, v_full)
+    d.destroy()
+
+
 class _Weights:
     """The oracle's synthetic weights with some matrices replaced."""
 
