@@ -630,7 +630,8 @@ def main():
                                      "weights": "Q8_0 synthetic, the key/value heads once (q | k | v: 6144 rows); "
                                                 "products of at most 256 rows stream the Q8_0 codes (the few-row "
                                                 "kernel), longer ones the resident bf16 expansion "
-                                                "(exn_enc_resident, the default)",
+                                                "(exn_enc_resident, the default; made by the first prompt "
+                                                "of more than 256 tokens)",
                                      "seed": SEED}, "records": rec}), flush=True)
         return
     if a.vae_encode_only:

@@ -284,15 +284,18 @@ int exn_enc_check(exn_enc* e) {
   return EXN_OK;
 }
 
-// the layers' matrices multiplied from resident bf16 expansions (1, the default, 16 GB beside
-// the 8.4 GB of Q8_0) or from Q8_0 alone, dequantised in the products (0)
+// the layers' matrices multiplied from resident bf16 expansions (1, the default, 14 GB beside
+// the 7.4 GB of Q8_0, made by the first prompt of more than 256 tokens: shorter ones run every
+// product through the few-row kernel, which streams the Q8_0 codes) or from Q8_0 alone,
+// dequantised in the products (0: any expansions are dropped)
 int exn_enc_resident(exn_enc* e, int bf16) {
   if (!e) FAIL(EXN_EINVAL, "null encoder");
   TRY(use(e->ctx));
   e->bf16 = bf16 != 0;
-  for (auto& L : e->L)
-    for (exn_w* m : {L.qkv, L.out, L.gate_up, L.down})
-      if (m) TRY(w_resident(m, e->bf16));
+  if (!e->bf16)
+    for (auto& L : e->L)
+      for (exn_w* m : {L.qkv, L.out, L.gate_up, L.down})
+        if (m) TRY(w_resident(m, false));
   HIPCHK(hipStreamSynchronize(e->ctx->stream));
   return EXN_OK;
 }
@@ -334,7 +337,9 @@ int exn_enc_rope_table(const int32_t* pos, int n, double base, float* cs) {
 static int enc_states(exn_enc* e, const int32_t* ids, int n, const float* cs, int pic0, int m, const float* merged,
                       const float* deep, float* out) {
   hipStream_t s = e->ctx->stream;
-  if (e->bf16)   // expansions made (or remade after a set) once, then kept
+  // expansions made (or remade after a set) once a prompt reads them, then kept: a prompt of at
+  // most 256 tokens takes every product from the Q8_0 codes (wop_n) and leaves them unmade
+  if (e->bf16 && n > 256)
     for (auto& L : e->L)
       for (exn_w* w : {L.qkv, L.out, L.gate_up, L.down}) TRY(w_resident(w, true));
   const int64_t lcap = ((int64_t)n + 63) / 64 * 64;

@@ -403,9 +403,10 @@ int exn_enc_destroy(exn_enc* e);
 int exn_enc_memory(exn_enc* e, int64_t* weights, int64_t* scratch);
 /* No reference counterpart (illatio multiplies from Q8_0): BF16 1, the default, runs the
  * layers' products from a resident bf16 expansion of each Q8_0 matrix (bf16(fp32(d) q), the
- * operand values the Q8_0 products make in LDS; 16 GB beside the 8.4 GB of Q8_0, made at the
- * first exn_enc_states and after a matrix is set); 0 drops them and multiplies from Q8_0. The
- * states are the same either way. */
+ * operand values the Q8_0 products make in LDS; 14 GB beside the 7.4 GB of Q8_0, made by the
+ * first exn_enc_states of more than 256 tokens and after a matrix is set: shorter prompts
+ * stream the Q8_0 codes in every product and leave them unmade); 0 drops them and multiplies
+ * from Q8_0. The states are the same either way. */
 int exn_enc_resident(exn_enc* e, int bf16);
 
 #ifdef __cplusplus

@@ -156,11 +156,16 @@ def test_resident_expansion_equals_q8_products(enc2, n):
 
 
 def test_a_set_matrix_remakes_its_expansion(ctx, owt2):
-    """A matrix set after its expansion was made is multiplied from the new values."""
+    """A matrix set after its expansion was made is multiplied from the new values; the
+    expansions are made by the first prompt longer than 256 tokens, not by shorter ones."""
     e = X.load_encoder(seed=SEED, layers=2, vocab=VOCAB, ctx=ctx)
     try:
-        ids = eo.synth_ids(SEED + 7, 40, VOCAB)
+        w0, _ = e.memory()
+        X.encoder_states(e, eo.synth_ids(SEED + 8, 40, VOCAB))
+        assert e.memory()[0] == w0                            # a short prompt leaves them unmade
+        ids = eo.synth_ids(SEED + 7, 300, VOCAB)
         before = X.encoder_states(e, ids)
+        assert e.memory()[0] > w0
         other = eo.SynthEncoder(SEED + 100, eo.EShape(layers=2))
         name = "blk.1.ffn_down.weight"
         shape = dict(eo.enc_expected(eo.EShape(layers=2)))[name]
