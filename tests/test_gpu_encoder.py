@@ -45,7 +45,9 @@ def owt2():
     return eo.SynthEncoder(SEED, eo.EShape(layers=2))
 
 
-@pytest.mark.parametrize("n", [1, 37, 300, 1024, 1025, 1100])   # 1025 on: past the split-K path
+# 1, 37: the few-row 128 x 256 tiles; 200: 256 x 128 (ragged rows, q | k | v split 5 ways); 1025 on:
+# past the split-K path
+@pytest.mark.parametrize("n", [1, 37, 200, 300, 1024, 1025, 1100])
 def test_states_two_layers_against_oracle(enc2, owt2, n):
     say("encoder states, 2 layers, n", n)
     ids = eo.synth_ids(SEED + n, n, VOCAB)
