@@ -180,6 +180,20 @@ def test_a_set_matrix_remakes_its_expansion(ctx, owt2):
         e.destroy()
 
 
+def test_release_frees_scratch_and_keeps_weights(enc2):
+    """encoder release (the scratch freed, weights and expansions kept): the memory it reports
+    drops to the weights, and the next prompt makes its buffers again (no larger than before)
+    with the same states."""
+    ids = eo.synth_ids(SEED + 9, 37, VOCAB)
+    a = X.encoder_states(enc2, ids)
+    w, s = enc2.memory()
+    assert s > 0
+    enc2.release()
+    assert enc2.memory() == (w, 0)
+    b = X.encoder_states(enc2, ids)
+    assert np.array_equal(a, b) and 0 < enc2.memory()[1] <= s
+
+
 def test_encoder_errors(ctx, enc2):
     e = X.Encoder(ctx, 2)
     try:

@@ -189,6 +189,20 @@ def test_decode_against_reference_script(vae, golden, case):
     assert e < 1e-2 and m <= PICTURE_MAX
 
 
+def test_release_frees_scratch_and_keeps_weights(vae, golden):
+    """vae-release (src/cuda-vae.lisp:28-33): the scratch freed, the weights kept; the next
+    decode makes its buffers again and gives the same picture bit for bit."""
+    z = golden["latent_0"]
+    h, w = z.shape[1:]
+    a, _, _ = X.vae_decode(vae, z, h, w)
+    wb, sb = vae.memory()
+    assert sb > 0
+    vae.release()
+    assert vae.memory() == (wb, 0)
+    b, _, _ = X.vae_decode(vae, z, h, w)
+    assert np.array_equal(a, b) and 0 < vae.memory()[1] <= sb
+
+
 def test_decode_square_against_oracle(vae, golden):
     """A 4 x 4 latent (a 64 x 64 picture: every stage with several tiles of
     pixels), against the oracle on the same weights."""
@@ -262,6 +276,15 @@ def test_encode_against_oracle(enc_vae, h, w):
     e = xo.rel_l2(got, want)
     say("encode %d x %d: latent rel-L2 %.2e, |z| %.3f" % (h, w, e, float(np.sqrt((want * want).mean()))))
     assert got.shape == (64, h // 16, w // 16) and np.isfinite(got).all() and e < ENC_REL
+
+
+def test_release_then_encode(enc_vae):
+    """An encode after vae-release makes its buffers again: the same latent bit for bit."""
+    px = vo.synth_picture(6, 64, 64)
+    a = X.vae_encode(enc_vae, px, 64, 64)
+    enc_vae.release()
+    assert enc_vae.memory()[1] == 0
+    assert np.array_equal(X.vae_encode(enc_vae, px, 64, 64), a)
 
 
 def test_encode_device_entry_matches_host(ctx, enc_vae):

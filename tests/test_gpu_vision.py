@@ -189,6 +189,19 @@ def test_encode_reads_a_table_of_another_side_and_f16_tensors(ctx, owt):
         v.destroy()
 
 
+def test_release_frees_scratch_and_keeps_weights(tower):
+    """vision-release (src/cuda-vision.lisp:103-107): the scratch freed, the weights kept; the
+    next encode makes its buffers again and gives the same rows bit for bit."""
+    px = vo.synth_picture(SEED + 3, 128, 128)
+    a, da, m = X.vision_encode(tower, px, 128, 128)
+    w, s = tower.memory()
+    assert s > 0
+    tower.release()
+    assert tower.memory() == (w, 0)
+    b, db, _ = X.vision_encode(tower, px, 128, 128)
+    assert np.array_equal(a, b) and np.array_equal(da, db) and 0 < tower.memory()[1] <= s
+
+
 def test_vision_errors(ctx, tower):
     v = X.Vision(ctx)
     try:
