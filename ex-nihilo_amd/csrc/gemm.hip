@@ -1517,24 +1517,31 @@ hipError_t gemm_wbf16(hipStream_t s, const uint16_t* x, int64_t lda, const uint1
 
 // --- the edge products in fp32 -------------------------------------------------------
 // img_in, txt_in and proj_out feed the residual stream and the velocity straight,
-// and are 0.01% of a step's FLOPs: they run in fp32 on the SIMD lanes, the weights
-// as they are stored -- fp32 rows (the reference's d41_mm_f32, src/cuda-dit.lisp:
-// 127-130), bf16 rows, or Q8_0 dequantised exactly.  64 x 64 tiles, K 32 (a Q8_0
-// block) a step, each thread 4 x 4 outputs at a 16-row and 16-column stride.
+// and are 0.01% of a step's FLOPs: they run in fp32, the weights as they are stored --
+// fp32 rows (the reference's d41_mm_f32, src/cuda-dit.lisp:127-130), bf16 rows, or
+// Q8_0 dequantised exactly -- on v_mfma_f32_16x16x4_f32.  64 x 64 tiles, K 32 (a
+// Q8_0 block) a step staged k-major in LDS as fp32; 4 waves of 32 x 32, each 2 x 2
+// MFMA blocks (A: lane l holds row l % 16 at k l / 16, B: column l % 16 at k l / 16;
+// D: lane l holds column l % 16, rows 4 (l / 16) + e), every k summed once.
 __global__ void __launch_bounds__(256)
 k_gemm_f32(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ QS, const uint16_t* __restrict__ D,
            const uint16_t* __restrict__ WB, const float* __restrict__ WF, int64_t M, int64_t N, int64_t K,
            float* __restrict__ Y, int64_t ldy, int gelu) {
   __shared__ float xs[32][64 + 1];
   __shared__ float ws[32][64 + 1];
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32, c16 = lane & 15, g = lane >> 4;
   const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
   const int lr = tid >> 2, lk = (tid & 3) * 8;   // loader: row lr of the tile, k lk .. lk+7
   // split K: workgroup z of gridDim.z takes blocks of 32 kb0 .. kb1-1 and writes its raw sums
   // to Y + z M ldy (gelu then applies after the sum)
   const int64_t KB = K / 32, kb0 = KB * blockIdx.z / gridDim.z, kb1 = KB * (blockIdx.z + 1) / gridDim.z;
   if (gridDim.z > 1) Y += (int64_t)blockIdx.z * M * ldy;
-  float acc[4][4] = {};
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int64_t k0 = 32 * kb0; k0 < 32 * kb1; k0 += 32) {
     {
       const int64_t m = min(m0 + lr, M - 1);
@@ -1569,30 +1576,32 @@ k_gemm_f32(const float* __restrict__ X, int64_t ldx, const int8_t* __restrict__ 
       }
     }
     __syncthreads();
-#pragma unroll 8
-    for (int kk = 0; kk < 32; ++kk) {
-      float a[4], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = xs[kk][ty + 16 * i];
+    for (int kk = 0; kk < 32; kk += 4) {
+      float a[2], b[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = ws[kk][tx + 16 * j];
+      for (int i = 0; i < 2; ++i) a[i] = xs[kk + g][wm + 16 * i + c16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 2; ++j) b[j] = ws[kk + g][wn + 16 * j + c16];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t m = m0 + ty + 16 * i;
-    if (m >= M) continue;
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t n = n0 + tx + 16 * j;
-      if (n < N) Y[m * ldy + n] = gelu && gridDim.z == 1 ? gelu_tanh_f(acc[i][j]) : acc[i][j];
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = n0 + wn + 16 * j + c16;
+      if (n >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t m = m0 + wm + 16 * i + 4 * g + e;
+        if (m < M) Y[m * ldy + n] = gelu && gridDim.z == 1 ? gelu_tanh_f(acc[i][j][e]) : acc[i][j][e];
+      }
     }
-  }
 }
 
 // Y = the S partial sums of a split edge product in order (M x N, ldy apart), GELU-tanh when asked
