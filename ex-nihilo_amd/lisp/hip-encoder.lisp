@@ -29,6 +29,8 @@
   (pic0 sb-alien:int) (m sb-alien:int) (merged sb-sys:system-area-pointer) (deep sb-sys:system-area-pointer)
   (out sb-sys:system-area-pointer))
 (sb-alien:define-alien-routine ("exn_enc_release" %exn-enc-release) sb-alien:int (e sb-sys:system-area-pointer))
+(sb-alien:define-alien-routine ("exn_enc_resident" %exn-enc-resident) sb-alien:int
+  (e sb-sys:system-area-pointer) (bf16 sb-alien:int))
 (sb-alien:define-alien-routine ("exn_alloc" %exn-alloc) sb-alien:int
   (ctx sb-sys:system-area-pointer) (bytes (sb-alien:unsigned 64)) (out sb-sys:system-area-pointer))
 (sb-alien:define-alien-routine ("exn_free" %exn-free) sb-alien:int
@@ -115,6 +117,7 @@
    4096 floats.  ROPE: rope rows for the positions (mrope-table's, an edit prompt's), else text
    positions; inside call-with-picture-rows the picture's rows too."
   (destructuring-bind (ctx . e) (or (gethash model *hip-encoders*) (error "not a GPU encoder: ~A" model))
+    (exn-check (%exn-enc-resident e (if *hip-resident* 1 0)))   ; hip-dit.lisp's switch
     (let* ((n (length ids))
            (iv (make-array n :element-type '(signed-byte 32) :initial-contents (coerce ids 'list)))
            (out (f32vec (* n 4096))))
