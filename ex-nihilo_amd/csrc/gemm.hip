@@ -865,14 +865,19 @@ __device__ __forceinline__ void buffer_load_u32_into(uint32_t& v, i32x4 rsrc, ui
 //   pairs), and converts them into the W tile of step t+2 once B1 has freed it.
 // The tiled operand's 256-row chunks hold two 128-row tiles: tile bn is chunk bn/2, rows
 // 128 (bn%2) .. (codes at 8 KB (bn%2), scales at QT_SCALES + 512 (bn%2)).
-template <int EPI>
+// TR = 256: the products of 129 to 256 rows (a prompt's) on 256 x 128 tiles, 8 waves of 64 x 64:
+// a weight row dequantised once a workgroup into LDS, where the few-row kernel's waves convert
+// their own weight rows into registers twice a tile; a step of 32 MFMA positions, the same order
+// of operations and the same waits counted from their positions.
+template <int EPI, int TR = 512>
 __global__ void __launch_bounds__(512)
 k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __restrict__ QT, int64_t M, int64_t N,
                int64_t K, EpiArgs ea) {
   constexpr bool HEADS = EPI == EPI_QKV;
-  constexpr int WM = HEADS ? 64 : 128, WN = HEADS ? 128 : 64, MI = WM / 16, NI = WN / 16;
-  static_assert((512 / WM) * (128 / WN) == 8, "the waves tile 512 x 128");
-  constexpr int NMF = MI * NI, NRD = MI + NI, XPARTS = 8, STAGE = 81920, WOFF = 65536;
+  static_assert(TR == 512 || (TR == 256 && !HEADS), "512-row tiles, or 256-row tiles without the QKV epilogue");
+  constexpr int WM = HEADS ? 64 : TR / 4, WN = HEADS ? 128 : 64, MI = WM / 16, NI = WN / 16;
+  static_assert((TR / WM) * (128 / WN) == 8, "the waves tile TR x 128");
+  constexpr int NMF = MI * NI, NRD = MI + NI, XPARTS = TR / 64, WOFF = TR * 128, STAGE = WOFF + 16384;
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   extern __shared__ __align__(1024) uint8_t smem[];
@@ -890,7 +895,7 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
     bm = first + in % sz;
     bn = in / sz;
   }
-  const int64_t m0 = (int64_t)bm * 512, n0 = (int64_t)bn * 128;
+  const int64_t m0 = (int64_t)bm * TR, n0 = (int64_t)bn * 128;
   // split K (EPI_PART): workgroup z of gridDim.z takes k-steps kt0 .. kt1-1, cut in pairs as
   // k_gemm_bt cuts them (K % 128 == 0), so that both give the same partial sums
   const int KT = (int)(K / 64), SK = gridDim.z, zk = blockIdx.z;
@@ -969,11 +974,18 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
   // steps to land: one was 0.7% slower, the loads waited on at DQ0); B2: step t+1's X has
   // landed (its W was written a step before, behind this step's B1); then step t+1's first-slice
   // fragments from stage cur^1.  The waits leave out what ops_after counts from the positions.
-  constexpr int B1 = 14 * NMF / 32, B2 = 52 * NMF / 32, DQ0 = B1 + 10, CLP = DQ0 + 7;
-  constexpr int QPOS[10] = {B1, B1 + 4, B1 + 8, B1 + 12, CLP, CLP + 1, B1 + 20, B1 + 24, B1 + 28, B1 + 32};
-  constexpr int DQ_VM = ops_after(CLP + 1, 2, DQ0, QPOS, 10), B2_VM = ops_after(B1 + 32, 1, B2, QPOS, 10);
-  static_assert(B1 >= NRD && B1 + 32 < B2 && B2 + NRD <= 2 * NMF && DQ0 > B1 + 8 && DQ0 + 6 < CLP &&
-                    CLP + 1 < B1 + 20 && DQ_VM < 64 && B2_VM < 64,
+  // 512-row tiles (64 positions): X parts 0-3 at B1 + 4i, the codes at CLP, parts 4-7 after
+  // them; 256-row tiles (32 positions): the 4 parts at B1 + 2i, the codes after the conversions
+  constexpr bool T5 = TR == 512;
+  constexpr int B1 = T5 ? 14 * NMF / 32 : 8, B2 = T5 ? 52 * NMF / 32 : 24, DQ0 = T5 ? B1 + 10 : 13,
+                CLP = T5 ? DQ0 + 7 : 20, NQ = XPARTS + 2;
+  constexpr int QPOS[10] = {B1,          B1 + (T5 ? 4 : 2),  B1 + (T5 ? 8 : 4),  B1 + (T5 ? 12 : 6), CLP,
+                            CLP + 1,     B1 + 20,            B1 + 24,            B1 + 28,            B1 + 32};
+  constexpr int XLAST = QPOS[T5 ? 9 : 3];   // the step's last X part
+  constexpr int DQ_VM = ops_after(CLP + 1, 2, DQ0, QPOS, NQ), B2_VM = ops_after(XLAST, 1, B2, QPOS, NQ);
+  static_assert(B1 >= NRD && XLAST < B2 && B2 + NRD <= 2 * NMF && DQ_VM < 64 && B2_VM < 64, "step schedule");
+  static_assert(T5 ? (B1 + 32 < B2 && DQ0 > B1 + 8 && DQ0 + 6 < CLP && CLP + 1 < B1 + 20)
+                   : (B2 == 2 * NMF - NRD && DQ0 > XLAST - 2 && DQ0 + 4 < CLP && CLP + 1 < B2 && B2 >= NMF),
                 "step schedule");
   auto step = [&](Frag& F0, Frag& F1, int t, auto bc) {
     constexpr int P = decltype(bc)::value;
@@ -1096,16 +1108,16 @@ static bool dma_fits(const uint16_t* x, int64_t lda, const WOp& w, int64_t M, in
          ea.ldy % 4 == 0 && a16(ea.y) && a16(ea.resid) && a16(ea.gate) && ea.mstride % 4 == 0;
 }
 
-template <int EPI>
+template <int EPI, int TR = 512>
 static hipError_t launch_tall(hipStream_t s, const uint16_t* x, int64_t lda, const uint8_t* qt, int64_t M, int64_t N,
                               int64_t K, const EpiArgs& ea, int split) {
-  const size_t shm = 2 * 81920;
-  auto kern = k_gemm_q8_tall<EPI>;
+  const size_t shm = 2 * (TR * 128 + 16384);
+  auto kern = k_gemm_q8_tall<EPI, TR>;
   {
     const hipError_t e = ensure_lds((const void*)kern, (int)shm);
     if (e != hipSuccess) return e;
   }
-  dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 511) / 512), (unsigned)split);
+  dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + TR - 1) / TR), (unsigned)split);
   hipLaunchKernelGGL(kern, grid, dim3(512), shm, s, x, lda, qt, M, N, K, ea);
   return hipGetLastError();
 }
@@ -1366,8 +1378,32 @@ static hipError_t few_direct(hipStream_t s, const uint16_t* x, int64_t lda, cons
   }
 }
 
+// Q8_0 products of 129 to 256 rows: the tall kernel's 256 x 128 tiles, each weight row dequantised
+// once a workgroup (the few-row kernel's waves convert theirs twice), where a workgroup's share of
+// K (K / S) is at least 768: gate_up 67.8 -> 60.5 us at 256 rows, q | k | v 46.3 -> 43.0; with
+// fewer k-steps its prologue outweighs that (to_out split 8 ways, 8 steps: 25.9 -> 26.7 us)
+static bool tall256_fits(const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K, int64_t S,
+                         const EpiArgs& ea) {
+  return !w.wb && w.qt && M > 128 && M <= 256 && N % 128 == 0 && K / S >= 768 && dma_fits(x, lda, w, M, N, K, ea);
+}
+
+static hipError_t tall256(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N,
+                          int64_t K, Epi epi, const EpiArgs& ea, int S) {
+  switch (epi) {
+    case EPI_F32: return launch_tall<EPI_F32, 256>(s, x, lda, w.qt, M, N, K, ea, S);
+    case EPI_BF16: return launch_tall<EPI_BF16, 256>(s, x, lda, w.qt, M, N, K, ea, S);
+    case EPI_GATE_ADD: return launch_tall<EPI_GATE_ADD, 256>(s, x, lda, w.qt, M, N, K, ea, S);
+    case EPI_SWIGLU: return launch_tall<EPI_SWIGLU, 256>(s, x, lda, w.qt, M, N, K, ea, S);
+    case EPI_GELU_BF16: return launch_tall<EPI_GELU_BF16, 256>(s, x, lda, w.qt, M, N, K, ea, S);
+    case EPI_F16: return launch_tall<EPI_F16, 256>(s, x, lda, w.qt, M, N, K, ea, S);
+    case EPI_PART: return launch_tall<EPI_PART, 256>(s, x, lda, w.qt, M, N, K, ea, S);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t gemm_q8(hipStream_t s, const uint16_t* x, int64_t lda, const WOp& w, int64_t M, int64_t N, int64_t K,
                    Epi epi, const EpiArgs& ea) {
+  if (tall256_fits(x, lda, w, M, N, K, 1, ea)) return tall256(s, x, lda, w, M, N, K, epi, ea, 1);
   if (few_fits(x, lda, w, M, N, K, ea)) return few_direct(s, x, lda, w, M, N, K, epi, ea);
   if (!dma_fits(x, lda, w, M, N, K, ea)) return dispatch<false>(s, x, lda, w.qs, w.qd, nullptr, M, N, K, epi, ea);
   switch (epi) {
@@ -1449,11 +1485,15 @@ hipError_t gemm_split_rows(hipStream_t s, const uint16_t* x, int64_t lda, const 
     if (S > K / 256) S = K / 256;
     if (S > smax) S = smax;
     if (S > part_cap / (M * N)) S = part_cap / (M * N);
-    if (S <= 1) return few_direct(s, x, lda, w, M, N, K, epi, ea);
     EpiArgs pa{};
     pa.y = part;
     pa.ldy = N;
-    const hipError_t e = launch_few_w<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
+    if (S <= 1)
+      return tall256_fits(x, lda, w, M, N, K, 1, ea) ? tall256(s, x, lda, w, M, N, K, epi, ea, 1)
+                                                     : few_direct(s, x, lda, w, M, N, K, epi, ea);
+    const hipError_t e = tall256_fits(x, lda, w, M, N, K, S, pa)
+                             ? tall256(s, x, lda, w, M, N, K, EPI_PART, pa, (int)S)
+                             : launch_few_w<EPI_PART>(s, x, lda, w, M, N, K, pa, (int)S);
     if (e != hipSuccess) return e;
     if (nsum) {
       *nsum = (int)S;
