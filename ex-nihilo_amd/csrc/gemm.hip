@@ -975,17 +975,17 @@ k_gemm_q8_tall(const uint16_t* __restrict__ X, int64_t lda, const uint8_t* __res
   // landed (its W was written a step before, behind this step's B1); then step t+1's first-slice
   // fragments from stage cur^1.  The waits leave out what ops_after counts from the positions.
   // 512-row tiles (64 positions): X parts 0-3 at B1 + 4i, the codes at CLP, parts 4-7 after
-  // them; 256-row tiles (32 positions): the 4 parts at B1 + 2i, the codes after the conversions
+  // them; 256-row tiles (32 positions): the 4 parts at B1 + 3i, the codes after the conversions
   constexpr bool T5 = TR == 512;
   constexpr int B1 = T5 ? 14 * NMF / 32 : 8, B2 = T5 ? 52 * NMF / 32 : 24, DQ0 = T5 ? B1 + 10 : 13,
                 CLP = T5 ? DQ0 + 7 : 20, NQ = XPARTS + 2;
-  constexpr int QPOS[10] = {B1,          B1 + (T5 ? 4 : 2),  B1 + (T5 ? 8 : 4),  B1 + (T5 ? 12 : 6), CLP,
+  constexpr int QPOS[10] = {B1,          B1 + (T5 ? 4 : 3),  B1 + (T5 ? 8 : 6),  B1 + (T5 ? 12 : 9), CLP,
                             CLP + 1,     B1 + 20,            B1 + 24,            B1 + 28,            B1 + 32};
   constexpr int XLAST = QPOS[T5 ? 9 : 3];   // the step's last X part
   constexpr int DQ_VM = ops_after(CLP + 1, 2, DQ0, QPOS, NQ), B2_VM = ops_after(XLAST, 1, B2, QPOS, NQ);
   static_assert(B1 >= NRD && XLAST < B2 && B2 + NRD <= 2 * NMF && DQ_VM < 64 && B2_VM < 64, "step schedule");
   static_assert(T5 ? (B1 + 32 < B2 && DQ0 > B1 + 8 && DQ0 + 6 < CLP && CLP + 1 < B1 + 20)
-                   : (B2 == 2 * NMF - NRD && DQ0 > XLAST - 2 && DQ0 + 4 < CLP && CLP + 1 < B2 && B2 >= NMF),
+                   : (B2 == 2 * NMF - NRD && DQ0 > B1 + 3 && DQ0 + 4 < CLP && XLAST < CLP && CLP + 1 < B2 && B2 >= NMF),
                 "step schedule");
   auto step = [&](Frag& F0, Frag& F1, int t, auto bc) {
     constexpr int P = decltype(bc)::value;
