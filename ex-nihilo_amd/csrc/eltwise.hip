@@ -270,22 +270,26 @@ hipError_t silu(hipStream_t s, int64_t count, float* x) {
 // operands, as the reference's halves): q ([32][n][128], scaled by qscale after the
 // rotation), k into kc ([32][lcap][128]) rows row0.., v transposed into vt
 // ([32][128][lcap]) columns row0.., query head h taking key/value head h / G.  cs:
-// cos, sin for 64 pairs, 128 floats a sequence row.  grid (ceil(n/64), 32), block 256.
+// cos, sin for 64 pairs, 128 floats a sequence row.  grid (ceil(n/TB), 32), block 256: TB
+// tokens a workgroup, 64, or 32 for passes of at most 512 rows (a prompt's: twice the
+// workgroups, and half the registers a thread holds the partial sums' loads in).
 // S > 0: the rows are those a split product's S partial sums (S x n rows of fp32, in order)
 // give through its fp16 store -- the same sums, in the same order, rounded once -- read from
 // the partials (all S of a value's loads out before its sum) instead of fp16 rows written and
 // read back
-template <int S>
+template <int S, int TB>
 __global__ void __launch_bounds__(256)
 k_qkv_prep(const uint16_t* __restrict__ qkv, const float* __restrict__ part, int64_t n,
            const float* __restrict__ wq, const float* __restrict__ wk, const float* __restrict__ cs, float qscale,
            uint16_t* __restrict__ q, uint16_t* __restrict__ kc, uint16_t* __restrict__ vt, int64_t row0, int64_t lcap,
            int64_t qld, int g) {
-  __shared__ uint16_t tile[64][128 + 2];
+  static_assert(TB == 64 || TB == 32, "64 or 32 tokens a workgroup");
+  constexpr int RQ = TB / 16;   // a wave's rounds of 4 tokens
+  __shared__ uint16_t tile[TB][128 + 2];
   const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t ld = 4096 + 2 * (4096 / g);                      // a row of qkv
   const int64_t ko = 4096 + (h / g) * 128, vo = ko + 4096 / g;   // this head's k and v in it
-  const int64_t t0 = (int64_t)blockIdx.x * 64;
+  const int64_t t0 = (int64_t)blockIdx.x * TB;
   // the 8 fp16 values of token TC's row at column COL
   auto ld8 = [&](int64_t tc, int64_t col) -> u32x4 {
     if constexpr (S == 0) {
@@ -308,7 +312,7 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, const float* __restrict__ part, int
     }
   };
   // q and k: 16 lanes a token, lane holding dims d8 .. d8+7 (its 4 rotation pairs) as one
-  // 16-byte load and store; a wave takes 4 tokens a round, its 16 tokens in 4 rounds whose
+  // 16-byte load and store; a wave takes 4 tokens a round, its TB / 4 tokens in RQ rounds whose
   // loads are all issued first.  The RMS sum is a reduction over the 16 lanes.
   const int sub = lane >> 4, d8 = (lane & 15) * 8;
   float wqv[8], wkv[8];
@@ -317,11 +321,11 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, const float* __restrict__ part, int
     wqv[j] = wq[d8 + j];
     wkv[j] = wk[d8 + j];
   }
-  u32x4 uq[4], uk[4];
-  f32x4 ca[4], cb[4];
+  u32x4 uq[RQ], uk[RQ];
+  f32x4 ca[RQ], cb[RQ];
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int64_t tc = min(t0 + wave * 16 + it * 4 + sub, n - 1);   // rows past n: loaded, not stored
+  for (int it = 0; it < RQ; ++it) {
+    const int64_t tc = min(t0 + wave * (TB / 4) + it * 4 + sub, n - 1);   // rows past n: loaded, not stored
     uq[it] = ld8(tc, h * 128 + d8);
     uk[it] = ld8(tc, ko + d8);
     const float* cr = cs + (row0 + tc) * 128 + d8;   // cos, sin of pairs d8/2 .. d8/2 + 3
@@ -329,8 +333,8 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, const float* __restrict__ part, int
     cb[it] = *(const f32x4*)(cr + 4);
   }
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int64_t t = t0 + wave * 16 + it * 4 + sub;
+  for (int it = 0; it < RQ; ++it) {
+    const int64_t t = t0 + wave * (TB / 4) + it * 4 + sub;
     const float c[8] = {ca[it][0], ca[it][1], ca[it][2], ca[it][3], cb[it][0], cb[it][1], cb[it][2], cb[it][3]};
     float a[8], ssq = 0.f, ssk = 0.f;
 #pragma unroll
@@ -364,8 +368,8 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, const float* __restrict__ part, int
       *(u32x4*)(kc + ((int64_t)h * lcap + row0 + t) * 128 + d8) = ok;
     }
   }
-  // v: 64 tokens x 128 dims through LDS, out as 128 rows of 64 consecutive keys
-  for (int i = 0; i < 4; ++i) {
+  // v: TB tokens x 128 dims through LDS, out as 128 rows of TB consecutive keys
+  for (int i = 0; i < TB / 16; ++i) {
     const int c = tid + 256 * i, tok = c >> 4, d8 = (c & 15) * 8;
     const int64_t t = t0 + tok;
     u32x4 v = u32x4{0, 0, 0, 0};
@@ -376,11 +380,11 @@ k_qkv_prep(const uint16_t* __restrict__ qkv, const float* __restrict__ part, int
     }
   }
   __syncthreads();
-  const int tok = tid & 63;
+  const int tok = tid % TB;
   const int64_t t = t0 + tok;
   if (t < n) {
     const int64_t col = vt_pos(row0 + t);
-    for (int d = tid >> 6; d < 128; d += 4) vt[((int64_t)h * 128 + d) * lcap + col] = tile[tok][d];
+    for (int d = tid / TB; d < 128; d += 256 / TB) vt[((int64_t)h * 128 + d) * lcap + col] = tile[tok][d];
   }
 }
 
@@ -391,8 +395,12 @@ hipError_t qkv_prep(hipStream_t s, const uint16_t* qkv, int64_t n, const float* 
   if (kv_group != 1 && kv_group != 4) return hipErrorInvalidValue;
   // q is scaled by 1/sqrt(128) * log2(e): the attention's scores are then in log2 units
   const float qscale = QK_QSCALE;
-  hipLaunchKernelGGL(k_qkv_prep<0>, dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, nullptr, n, wq, wk, cs, qscale, q,
-                     k, vt, row0, lcap, qld, kv_group);
+  if (n <= 512)
+    hipLaunchKernelGGL((k_qkv_prep<0, 32>), dim3(grid_of(n, 32), 32), dim3(256), 0, s, qkv, nullptr, n, wq, wk, cs,
+                       qscale, q, k, vt, row0, lcap, qld, kv_group);
+  else
+    hipLaunchKernelGGL((k_qkv_prep<0, 64>), dim3(grid_of(n, 64), 32), dim3(256), 0, s, qkv, nullptr, n, wq, wk, cs,
+                       qscale, q, k, vt, row0, lcap, qld, kv_group);
   return hipGetLastError();
 }
 
@@ -401,12 +409,17 @@ hipError_t qkv_prep_part(hipStream_t s, const float* part, int S, int64_t n, con
                          int64_t qld, int kv_group) {
   if (n == 0) return hipSuccess;
   if ((kv_group != 1 && kv_group != 4) || S < 1 || S > 8) return hipErrorInvalidValue;
-  const dim3 g(grid_of(n, 64), 32);
+  const bool t32 = n <= 512;   // 32 tokens a workgroup (as qkv_prep)
+  const dim3 g(grid_of(n, t32 ? 32 : 64), 32);
   switch (S) {
-#define EXN_PREP_S(k)                                                                                        \
-  case k:                                                                                                    \
-    hipLaunchKernelGGL(k_qkv_prep<k>, g, dim3(256), 0, s, nullptr, part, n, wq, wk, cs, QK_QSCALE, q, k_, vt, \
-                       row0, lcap, qld, kv_group);                                                           \
+#define EXN_PREP_S(k)                                                                                         \
+  case k:                                                                                                     \
+    if (t32)                                                                                                  \
+      hipLaunchKernelGGL((k_qkv_prep<k, 32>), g, dim3(256), 0, s, nullptr, part, n, wq, wk, cs, QK_QSCALE, q, \
+                         k_, vt, row0, lcap, qld, kv_group);                                                  \
+    else                                                                                                      \
+      hipLaunchKernelGGL((k_qkv_prep<k, 64>), g, dim3(256), 0, s, nullptr, part, n, wq, wk, cs, QK_QSCALE, q, \
+                         k_, vt, row0, lcap, qld, kv_group);                                                  \
     break;
     EXN_PREP_S(1) EXN_PREP_S(2) EXN_PREP_S(3) EXN_PREP_S(4) EXN_PREP_S(5) EXN_PREP_S(6) EXN_PREP_S(7) EXN_PREP_S(8)
 #undef EXN_PREP_S
