@@ -138,14 +138,15 @@ def test_gemm_q8_bf16(ctx, M, N, K, resident):
 
 FEW_ROWS = [(20, 1024, 4096), (24, 1024, 4096), (64, 1024, 4096), (128, 1024, 4096), (129, 1024, 4096),
             (200, 1024, 4096), (256, 1024, 4096), (37, 512, 256), (256, 256, 12288), (200, 1024, 512),
-            (256, 384, 512)]
+            (256, 384, 512), (200, 384, 1024)]
 
 
 @pytest.mark.parametrize("M,N,K", FEW_ROWS)
 def test_few_row_products(ctx, M, N, K):
     """Products of at most 256 rows: the few-row kernel (128-row tiles up to 128 rows, 256-row
     tiles above where K is under 768: 512 here) and, from 129 rows with K of 768 or more, the
-    tall kernel's 256 x 128 tiles; K of one group of 4 steps up to the down product's 12288:
+    tall kernel's 256 x 128 tiles (N 384: the last tile half of a 256-row chunk of the tiled
+    operand); K of one group of 4 steps up to the down product's 12288:
     fp32 out, the gated residual and SwiGLU, from Q8_0 and from the resident bf16 expansion --
     the same bits from either, the same bits on a second call, and within 2e-6 of float64 on the
     same bf16 operands."""
